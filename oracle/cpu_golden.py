@@ -1,0 +1,44 @@
+"""The reference tests' CPU golden expressions, used as the timed CPU baseline
+(``cpu_baseline`` in bench.py) -- TEST/MEASUREMENT INFRASTRUCTURE ONLY.
+
+Each function is the expression a reference test asserts against, evaluated
+with torch on the host cores:
+  vadd        x + y                                   README.md:53; python/test/asc2/kernels/test_vadd.py:48
+  softmax     torch.softmax(x, dim=1)                 python/test/asc2/kernels/test_softmax.py:43
+  matmul      a.to(float32) @ b.to(float32)           python/test/asc2/kernels/test_matmul_tiled.py:49
+  int8        a.to(int32) @ b.to(int32)               python/test/generalization/adv/test_matmul_iterate_all.py:116
+  dequant     (acc.float() * scale).half()            build definition of DEQF16 (test_matmul_quant.py:94-106)
+  attention   softmax(q k^T * scale + mask) v in fp32 (no reference golden; build-defined)
+"""
+from __future__ import annotations
+
+import torch
+
+
+def vadd(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    return x + y
+
+
+def softmax(x: torch.Tensor) -> torch.Tensor:
+    return torch.softmax(x, dim=1)
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return a.to(torch.float32) @ b.to(torch.float32)
+
+
+def matmul_i8(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return a.to(torch.int32) @ b.to(torch.int32)
+
+
+def dequant(acc: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    return (acc.float() * scale).half()
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float, causal: bool) -> torch.Tensor:
+    """One (batch, head) slice [S, D] in fp32."""
+    s = (q.float() @ k.float().T) * sm_scale
+    if causal:
+        n = s.shape[0]
+        s = s.masked_fill(torch.ones(n, s.shape[1], dtype=torch.bool).triu(1), float("-inf"))
+    return torch.softmax(s, dim=-1) @ v.float()

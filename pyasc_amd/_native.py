@@ -1,0 +1,109 @@
+"""ctypes binding of libasc_hip.so (the C ABI declared in include/asc_hip.h).
+
+This replaces the reference's runtime shim: rt_wrapper.cpp compiled at first
+use and loaded with ctypes (python/asc/lib/runtime/state.py:25-50,140-144;
+python/asc/lib/runtime/interface.py:25-39).  Error handling keeps the
+reference's contract: a nonzero return becomes
+``RuntimeError("Function <name> returned <code>")``
+(python/asc/lib/runtime/state.py:63-75), extended with the library's message.
+
+There is no fallback: if the library is missing, or no HIP device is present
+when a kernel is launched, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libasc_hip.so"
+
+# dtype codes of include/asc_hip.h
+DT_FLOAT32 = 0
+DT_FLOAT16 = 1
+DT_BFLOAT16 = 2
+DT_INT32 = 3
+DT_INT8 = 4
+
+ERR_INVALID_ARG = -1
+ERR_UNSUPPORTED = -2
+ERR_ALIGNMENT = -3
+
+_c_i32, _c_i64, _c_p, _c_f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
+
+# name -> argtypes; every entry point returns int32_t.
+SIGNATURES = {
+    "asc_device_info": [_c_i32, ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32),
+                        ctypes.c_char_p],
+    "asc_stream_synchronize": [_c_p],
+    "asc_vadd": [_c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
+    "asc_softmax_rows_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
+    "asc_softmax_blocks_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
+    "asc_matmul": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
+    "asc_matmul_i8_i32": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
+    "asc_matmul_i8_dequant_f16": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
+    "asc_flash_attention_fwd_bf16": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_f32, _c_i32,
+                                     _c_p],
+}
+# entry points returning a C string
+STRING_FUNCS = ("asc_last_error", "asc_version")
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Loads libasc_hip.so once and declares every entry point's prototype."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        lib_path = Path(path) if path is not None else LIB_PATH
+        if not lib_path.exists():
+            raise RuntimeError(f"{lib_path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                               "or `python pyasc_amd/build.py`")
+        # torch's bundled HIP runtime has the same soname as ROCm's; importing
+        # torch first makes the library bind to that already-loaded runtime, so
+        # torch tensors and streams are valid in both.
+        import torch  # noqa: F401
+        lib = ctypes.CDLL(str(lib_path), mode=ctypes.RTLD_GLOBAL)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int32
+        for name in STRING_FUNCS:
+            fn = getattr(lib, name)
+            fn.argtypes = []
+            fn.restype = ctypes.c_char_p
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load_library().asc_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(code: int, fn_name: str) -> None:
+    """Raises the reference's RuntimeError form for a nonzero return code."""
+    if code != 0:
+        detail = last_error()
+        raise RuntimeError(f"Function {fn_name} returned {code}" + (f": {detail}" if detail else ""))
+
+
+def call(fn_name: str, *args) -> None:
+    fn = getattr(load_library(), fn_name)
+    check(fn(*args), fn_name)
+
+
+def version() -> str:
+    return load_library().asc_version().decode()
+
+
+def device_info(device: int = 0) -> dict:
+    cu, lds, wave = _c_i32(), _c_i32(), _c_i32()
+    arch = ctypes.create_string_buffer(64)
+    call("asc_device_info", device, ctypes.byref(cu), ctypes.byref(lds), ctypes.byref(wave), arch)
+    return {"cu_count": cu.value, "lds_bytes": lds.value, "wave_size": wave.value, "arch": arch.value.decode()}

@@ -1,0 +1,118 @@
+"""Kernel launch: argument handling, host<->device copies, stream choice.
+
+Mirrors python/asc/runtime/launcher.py:
+  - ``LaunchOptions(core_num, stream)`` (launcher.py:79-102): ``kernel[n]`` or
+    ``kernel[n, stream]``; ``core_num`` is the logical block count the kernel body
+    is written for.
+  - ``Launcher.run`` (launcher.py:204-238): DRY_RUN skips the launch; a block count
+    <= 0 raises ValueError.
+  - Host buffers (CPU torch tensors, numpy arrays) are copied to the device, the
+    kernel runs, the stream is synchronised and every pointer argument is copied
+    back (launcher.py:176-195).  ROCm torch tensors are passed zero-copy and the
+    launch stays asynchronous on the chosen stream.
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional, Tuple
+
+import numpy as np
+
+from ...registry import KernelCall, KernelEntry
+
+
+@dataclass(frozen=True)
+class LaunchOptions:
+    core_num: int = 0
+    stream: Optional[Any] = None
+
+
+def stream_handle(stream: Any) -> int:
+    """hipStream_t of ``stream`` (None -> torch's current stream)."""
+    import torch
+    if stream is None:
+        return int(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return stream
+    handle = getattr(stream, "cuda_stream", None)
+    if handle is None:
+        raise TypeError(f"Unsupported stream object: {stream!r}")
+    return int(handle)
+
+
+def is_pointer_arg(value: Any) -> bool:
+    if isinstance(value, np.ndarray):
+        return True
+    try:
+        import torch
+        return isinstance(value, torch.Tensor) and value.dim() > 0
+    except ModuleNotFoundError:
+        return False
+
+
+def require_device() -> None:
+    import torch
+    if not torch.cuda.is_available():
+        raise RuntimeError("No HIP device is available: asc2 kernels run only on the MI355X (gfx950) device "
+                           "through libasc_hip.so; there is no CPU fallback.")
+
+
+class Launcher:
+
+    def __init__(self, options: LaunchOptions):
+        self.options = options
+
+    @staticmethod
+    def scalar_value(value: Any) -> Any:
+        """Python value of a by-value argument (0-dim tensor, numpy scalar, int, float, bool)."""
+        if isinstance(value, np.generic):
+            return value.item()
+        try:
+            import torch
+            if isinstance(value, torch.Tensor) and value.dim() == 0:
+                return value.item()
+        except ModuleNotFoundError:
+            pass
+        return value
+
+    def prepare(self, runtime_args: Dict[str, Any]) -> Tuple[Dict[str, Any], List[Tuple[Any, Any]]]:
+        """Device-side view of every runtime arg, plus (host, device) pairs to copy back."""
+        import torch
+        device_args: Dict[str, Any] = {}
+        copy_back: List[Tuple[Any, Any]] = []
+        for name, value in runtime_args.items():
+            if isinstance(value, np.ndarray):
+                dev = torch.from_numpy(np.ascontiguousarray(value)).to("cuda")
+                device_args[name] = dev
+                copy_back.append((value, dev))
+            elif isinstance(value, torch.Tensor) and value.dim() > 0:
+                if value.device.type == "cuda":
+                    device_args[name] = value
+                else:
+                    dev = value.contiguous().to("cuda")
+                    device_args[name] = dev
+                    copy_back.append((value, dev))
+            else:
+                device_args[name] = self.scalar_value(value)
+        return device_args, copy_back
+
+    def run(self, entry: KernelEntry, function_name: str, runtime_args: Dict[str, Any],
+            constexprs: Dict[str, Any]) -> None:
+        if os.environ.get("DRY_RUN"):
+            return
+        if self.options.core_num <= 0:
+            raise ValueError("Core number should be large than 0")
+        require_device()
+        device_args, copy_back = self.prepare(runtime_args)
+        stream = stream_handle(self.options.stream)
+        call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream)
+        entry.launch(call)
+        if copy_back:
+            from ... import _native
+            _native.call("asc_stream_synchronize", stream)
+            for host, dev in copy_back:
+                if isinstance(host, np.ndarray):
+                    np.copyto(host, dev.cpu().numpy())
+                else:
+                    host.copy_(dev.cpu())

@@ -1,0 +1,94 @@
+"""Builds libasc_hip.so (all HIP kernels + the C ABI of include/asc_hip.h) for gfx950.
+
+Each ``csrc/*.hip`` file is compiled separately with hipcc (in parallel), then
+linked into ``pyasc_amd/lib/libasc_hip.so``.  The result stays in-tree so it
+travels with the source tree to the GPU machine.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC_DIR = PKG_DIR / "csrc"
+INCLUDE_DIR = REPO_DIR / "include"
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "libasc_hip.so"
+BUILD_DIR = PKG_DIR / "_build"
+
+ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    # Packed fp32 VALU forms are disabled for every device pass.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE_DIR}",
+    f"-I{CSRC_DIR}",
+]
+
+# Files whose results are compared bit-exactly (or to 1e-6) keep IEEE op-by-op
+# rounding: no FMA contraction.
+PER_FILE_FLAGS = {
+    "vadd.hip": ["-ffp-contract=off"],
+    "softmax.hip": ["-ffp-contract=off"],
+    "matmul_i8.hip": ["-ffp-contract=off"],
+    "elementwise.hip": ["-ffp-contract=off"],
+}
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found (ROCm is required to build libasc_hip.so)")
+    return path
+
+
+def _compile(src: Path, verbose: bool) -> Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature; that warning is expected.
+    noise = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
+    msg = "\n".join(line for line in (res.stdout + res.stderr).splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{msg}")
+    if msg.strip() and verbose:
+        print(msg, flush=True)
+    return obj
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compiles every csrc/*.hip and links libasc_hip.so; returns its path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC_DIR.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    jobs = jobs or min(len(sources), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), sources))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of libasc_hip.so failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose="-v" in sys.argv))

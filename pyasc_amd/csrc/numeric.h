@@ -1,0 +1,29 @@
+// Scalar conversions shared by the kernels.  Rounding is IEEE round-to-nearest-
+// even everywhere, matching torch's CPU casts that the reference tests compare with.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace asc {
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return static_cast<float>(v);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  _Float16 v = static_cast<_Float16>(f);  // v_cvt_f16_f32 rounds to nearest even
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+}  // namespace asc

@@ -1,0 +1,142 @@
+// Elementwise vadd for asc2 vadd_kernel (python/test/asc2/kernels/test_vadd.py:16-28).
+//
+// HBM-bound: 3 x 4 bytes per fp32 element.  Each thread moves 4 independent
+// 16-byte vectors per operand (global_load_dwordx4) so a wave keeps 8 loads in
+// flight; the physical grid is sized by the covered length, not by the
+// Ascend-style logical grid, which only decides how far the writes reach.
+#include "common.h"
+#include "numeric.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+// 16-byte vector as a clang ext-vector so the nontemporal builtins accept it.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct AddF32 {
+  using T = float;
+  __device__ static float op(float a, float b) { return a + b; }
+};
+struct AddI32 {
+  using T = int32_t;
+  // two's-complement wraparound without signed-overflow UB
+  __device__ static int32_t op(int32_t a, int32_t b) {
+    return static_cast<int32_t>(static_cast<uint32_t>(a) + static_cast<uint32_t>(b));
+  }
+};
+struct AddF16 {
+  using T = uint16_t;
+  // fp32 add then RNE to fp16 equals the correctly rounded fp16 add (24 >= 2*11+2 bits)
+  __device__ static uint16_t op(uint16_t a, uint16_t b) {
+    return asc::f32_to_f16_rne(asc::f16_to_f32(a) + asc::f16_to_f32(b));
+  }
+};
+struct AddBF16 {
+  using T = uint16_t;
+  __device__ static uint16_t op(uint16_t a, uint16_t b) {
+    return asc::f32_to_bf16_rne(asc::bf16_to_f32(a) + asc::bf16_to_f32(b));
+  }
+};
+
+template <typename Op>
+__device__ __forceinline__ u32x4 add_vec(u32x4 a, u32x4 b) {
+  using T = typename Op::T;
+  constexpr int kN = 16 / sizeof(T);
+  T ea[kN], eb[kN], ec[kN];
+  __builtin_memcpy(ea, &a, 16);
+  __builtin_memcpy(eb, &b, 16);
+#pragma unroll
+  for (int i = 0; i < kN; ++i) ec[i] = Op::op(ea[i], eb[i]);
+  u32x4 c;
+  __builtin_memcpy(&c, ec, 16);
+  return c;
+}
+
+// out[v] = x[v] + y[v] for 16-byte vectors v < n_vec.
+template <typename Op>
+__global__ void __launch_bounds__(kThreads) vadd_vec_kernel(const u32x4* __restrict__ x, const u32x4* __restrict__ y,
+                                                            u32x4* __restrict__ out, int64_t n_vec) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
+  u32x4 a[kUnroll], b[kUnroll];
+  if (base + (kUnroll - 1) * kThreads < n_vec) {
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) a[j] = __builtin_nontemporal_load(x + base + j * kThreads);
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) b[j] = __builtin_nontemporal_load(y + base + j * kThreads);
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) __builtin_nontemporal_store(add_vec<Op>(a[j], b[j]), out + base + j * kThreads);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) {
+      const int64_t v = base + j * kThreads;
+      if (v < n_vec) out[v] = add_vec<Op>(x[v], y[v]);
+    }
+  }
+}
+
+// Element-wise path for [begin, end): unaligned buffers and the sub-vector tail.
+template <typename Op>
+__global__ void __launch_bounds__(kThreads) vadd_scalar_kernel(const typename Op::T* __restrict__ x,
+                                                               const typename Op::T* __restrict__ y,
+                                                               typename Op::T* __restrict__ out, int64_t begin,
+                                                               int64_t end) {
+  for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < end;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    out[i] = Op::op(x[i], y[i]);
+  }
+}
+
+template <typename Op>
+int32_t launch(const void* xv, const void* yv, void* outv, int64_t covered, hipStream_t stream) {
+  using T = typename Op::T;
+  const T* x = static_cast<const T*>(xv);
+  const T* y = static_cast<const T*>(yv);
+  T* out = static_cast<T*>(outv);
+  constexpr int64_t kPerVec = 16 / sizeof(T);
+  int64_t done = 0;
+  if (asc::aligned16(x) && asc::aligned16(y) && asc::aligned16(out)) {
+    const int64_t n_vec = covered / kPerVec;
+    if (n_vec > 0) {
+      const int64_t blocks = asc::ceil_div(n_vec, kThreads * kUnroll);
+      hipLaunchKernelGGL(vadd_vec_kernel<Op>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
+                         reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(y),
+                         reinterpret_cast<u32x4*>(out), n_vec);
+      int32_t rc = asc::check_launch("asc_vadd");
+      if (rc != ASC_OK) return rc;
+    }
+    done = n_vec * kPerVec;
+  }
+  if (done < covered) {
+    const int64_t rest = covered - done;
+    const int64_t blocks = asc::ceil_div(rest, kThreads) < 4096 ? asc::ceil_div(rest, kThreads) : 4096;
+    hipLaunchKernelGGL(vadd_scalar_kernel<Op>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, x, y,
+                       out, done, covered);
+    return asc::check_launch("asc_vadd");
+  }
+  return ASC_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t asc_vadd(int32_t dtype, const void* x, const void* y, void* out, int64_t size, int32_t tile_size,
+                            int32_t tile_per_block, int32_t grid, asc_stream_t stream) {
+  ASC_REQUIRE(size >= 0, ASC_ERR_INVALID_ARG, "asc_vadd: size must be >= 0, got %lld", (long long)size);
+  ASC_REQUIRE(tile_size > 0 && tile_per_block >= 0 && grid > 0, ASC_ERR_INVALID_ARG,
+              "asc_vadd: need tile_size > 0, tile_per_block >= 0, grid > 0 (got %d, %d, %d)", tile_size,
+              tile_per_block, grid);
+  // Coverage of the reference kernel body: grid*tpb tiles of tile_size, clipped at size.
+  const int64_t reach = static_cast<int64_t>(grid) * tile_per_block * tile_size;
+  const int64_t covered = reach < size ? reach : size;
+  if (covered == 0) return ASC_OK;
+  ASC_REQUIRE(x && y && out, ASC_ERR_INVALID_ARG, "asc_vadd: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ASC_DT_FLOAT32: return launch<AddF32>(x, y, out, covered, s);
+    case ASC_DT_INT32: return launch<AddI32>(x, y, out, covered, s);
+    case ASC_DT_FLOAT16: return launch<AddF16>(x, y, out, covered, s);
+    case ASC_DT_BFLOAT16: return launch<AddBF16>(x, y, out, covered, s);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_vadd: unsupported dtype code %d", dtype);
+  }
+}

@@ -1,0 +1,206 @@
+"""Typed host API over libasc_hip.so: torch device tensors in, kernels launched.
+
+Every function checks on the host that the buffers hold everything the kernel
+will touch (shape, dtype, device, layout) before it reaches the C ABI, so an
+inconsistent call raises ValueError/TypeError here instead of faulting on the
+GPU.  Launches are asynchronous on ``stream`` (default: torch's current stream).
+"""
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+
+from . import _native
+
+_DTYPE_CODES = {
+    torch.float32: _native.DT_FLOAT32,
+    torch.float16: _native.DT_FLOAT16,
+    torch.bfloat16: _native.DT_BFLOAT16,
+    torch.int32: _native.DT_INT32,
+    torch.int8: _native.DT_INT8,
+}
+
+
+def _stream(stream: Any) -> int:
+    if stream is None:
+        return int(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return stream
+    return int(stream.cuda_stream)
+
+
+def _device_tensor(t: Any, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"'{name}' must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"'{name}' must be on the HIP device, got {t.device}")
+    return t
+
+
+def _contiguous(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_contiguous():
+        raise ValueError(f"'{name}' must be contiguous")
+    return t
+
+
+def _code(t: torch.Tensor, name: str, allowed) -> int:
+    if t.dtype not in allowed:
+        raise TypeError(f"'{name}' has unsupported dtype {t.dtype}; expected one of {sorted(map(str, allowed))}")
+    return _DTYPE_CODES[t.dtype]
+
+
+# ---------------------------------------------------------------------------------------------- vadd
+
+def vadd_covered(size: int, tile_size: int, tile_per_block: int, grid: int) -> int:
+    """Elements written by asc2 vadd_kernel: [0, min(size, grid*tpb*tile))
+    (python/test/asc2/kernels/test_vadd.py:22-28 with the store clipped at ``size``)."""
+    return max(0, min(size, grid * tile_per_block * tile_size))
+
+
+def vadd(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
+         grid: int, stream: Any = None) -> None:
+    for t, n in ((x, "x"), (y, "y"), (out, "out")):
+        _contiguous(_device_tensor(t, n), n)
+    allowed = (torch.float32, torch.float16, torch.bfloat16, torch.int32)
+    code = _code(x, "x", allowed)
+    if y.dtype != x.dtype or out.dtype != x.dtype:
+        raise TypeError(f"vadd operands must share one dtype, got {x.dtype}, {y.dtype}, {out.dtype}")
+    if tile_size <= 0 or tile_per_block < 0 or grid <= 0 or size < 0:
+        raise ValueError(f"invalid vadd launch: size={size}, tile_size={tile_size}, "
+                         f"tile_per_block={tile_per_block}, grid={grid}")
+    covered = vadd_covered(size, tile_size, tile_per_block, grid)
+    for t, n in ((x, "x"), (y, "y"), (out, "out")):
+        if t.numel() < covered:
+            raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {covered}")
+    _native.call("asc_vadd", code, x.data_ptr(), y.data_ptr(), out.data_ptr(), size, tile_size, tile_per_block,
+                 grid, _stream(stream))
+
+
+# ------------------------------------------------------------------------------------------- softmax
+
+def _check_softmax(x: torch.Tensor, out: torch.Tensor, rows: int, num_cols: int) -> None:
+    for t, n in ((x, "x"), (out, "out")):
+        _contiguous(_device_tensor(t, n), n)
+        if t.dtype != torch.float32:
+            raise TypeError(f"softmax supports float32 only, '{n}' is {t.dtype}")
+        if t.numel() < rows * num_cols:
+            raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {rows}x{num_cols}")
+
+
+def softmax_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, grid: int,
+                 stream: Any = None) -> None:
+    """asc2 softmax_kernel(x, out, num_rows, num_cols, tile_size) of
+    python/test/asc2/kernels/test_softmax.py:16-27."""
+    if tile_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
+        raise ValueError(f"invalid softmax launch: rows={num_rows}, cols={num_cols}, tile={tile_size}, grid={grid}")
+    if tile_size > num_cols:
+        raise ValueError(f"tile_size {tile_size} > num_cols {num_cols}: the reference kernel's reduction would "
+                         "include the zero padding and its store would spill into the next row")
+    _check_softmax(x, out, num_rows, num_cols)
+    _native.call("asc_softmax_rows_f32", x.data_ptr(), out.data_ptr(), num_rows, num_cols, tile_size, grid,
+                 _stream(stream))
+
+
+def softmax_blocks_covered(num_rows: int, block_size: int, grid: int) -> int:
+    """Rows written by the fused asc2 softmax_kernel: [0, min(num_rows, grid*block_size))."""
+    return max(0, min(num_rows, grid * block_size))
+
+
+def softmax_blocks(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, block_size: int, grid: int,
+                   stream: Any = None) -> None:
+    """asc2 softmax_kernel(x, out, num_rows, num_cols, block_size) of
+    python/test/asc2/kernels/test_softmax_fused.py:16-24."""
+    if block_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
+        raise ValueError(f"invalid softmax launch: rows={num_rows}, cols={num_cols}, block={block_size}, "
+                         f"grid={grid}")
+    _check_softmax(x, out, softmax_blocks_covered(num_rows, block_size, grid), num_cols)
+    _native.call("asc_softmax_blocks_f32", x.data_ptr(), out.data_ptr(), num_rows, num_cols, block_size, grid,
+                 _stream(stream))
+
+
+# -------------------------------------------------------------------------------------------- matmul
+
+def _row_major_2d(t: torch.Tensor, name: str) -> int:
+    """Leading dimension of a 2-D row-major (unit inner stride) tensor."""
+    if t.dim() != 2:
+        raise ValueError(f"'{name}' must be 2-D, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.shape[1] > 1:
+        raise ValueError(f"'{name}' must have unit stride along its last dimension")
+    return max(t.stride(0), t.shape[1], 1)
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False, stream: Any = None) -> None:
+    """c = cast(relu?(a @ b)) with fp32 accumulation; the cast is chosen by c's dtype
+    (float32: no cast; float16/bfloat16: RNE)."""
+    for t, n in ((a, "a"), (b, "b"), (c, "c")):
+        _device_tensor(t, n)
+    in_code = _code(a, "a", (torch.float32, torch.float16, torch.bfloat16))
+    if b.dtype != a.dtype:
+        raise TypeError(f"a and b must share a dtype, got {a.dtype} and {b.dtype}")
+    out_code = _code(c, "c", (torch.float32, torch.float16, torch.bfloat16))
+    lda, ldb, ldc = _row_major_2d(a, "a"), _row_major_2d(b, "b"), _row_major_2d(c, "c")
+    M, K = a.shape
+    K2, N = b.shape
+    if K2 != K:
+        raise ValueError(f"inner dimensions differ: a is {tuple(a.shape)}, b is {tuple(b.shape)}")
+    if tuple(c.shape) != (M, N):
+        raise ValueError(f"c must be {(M, N)}, got {tuple(c.shape)}")
+    _native.call("asc_matmul", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, lda, ldb, ldc,
+                 int(bool(relu)), _stream(stream))
+
+
+def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional[torch.Tensor] = None,
+              trunc19: bool = False, stream: Any = None) -> None:
+    """int8 GEMM with exact int32 accumulation.  c int32: raw accumulators.  c float16:
+    c = fp16(fp32(acc) * scale[n]) (scale required, fp32 of length N)."""
+    for t, n in ((a, "a"), (b, "b"), (c, "c")):
+        _contiguous(_device_tensor(t, n), n)
+    _code(a, "a", (torch.int8,))
+    _code(b, "b", (torch.int8,))
+    if a.dim() != 2 or b.dim() != 2 or c.dim() != 2:
+        raise ValueError("a, b and c must be 2-D")
+    M, K = a.shape
+    K2, N = b.shape
+    if K2 != K or tuple(c.shape) != (M, N):
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)}, b {tuple(b.shape)}, c {tuple(c.shape)}")
+    s = _stream(stream)
+    if c.dtype == torch.int32:
+        _native.call("asc_matmul_i8_i32", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, s)
+        return
+    if c.dtype != torch.float16:
+        raise TypeError(f"c must be int32 (accumulators) or float16 (dequantised), got {c.dtype}")
+    if scale is None:
+        raise ValueError("a float16 output needs the per-channel scale vector")
+    _contiguous(_device_tensor(scale, "scale"), "scale")
+    if scale.dtype != torch.float32 or scale.numel() != N:
+        raise ValueError(f"scale must be float32 with {N} elements, got {scale.dtype} with {scale.numel()}")
+    _native.call("asc_matmul_i8_dequant_f16", a.data_ptr(), b.data_ptr(), scale.data_ptr(), c.data_ptr(), M, N, K,
+                 int(bool(trunc19)), s)
+
+
+# --------------------------------------------------------------------------------------- attention
+
+FA_HEAD_DIMS = (64, 128)
+
+
+def flash_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, sm_scale: float,
+                        causal: bool, lse: Optional[torch.Tensor] = None, stream: Any = None) -> None:
+    """o = softmax(q k^T * sm_scale + causal mask) v for bf16 [batch, heads, seq, head_dim]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
+        _contiguous(_device_tensor(t, n), n)
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"'{n}' must be bfloat16, got {t.dtype}")
+        if t.dim() != 4 or tuple(t.shape) != tuple(q.shape):
+            raise ValueError(f"'{n}' must be [batch, heads, seq_len, head_dim] like q {tuple(q.shape)}")
+    batch, heads, seq_len, head_dim = q.shape
+    if head_dim not in FA_HEAD_DIMS:
+        raise ValueError(f"head_dim {head_dim} not supported (supported: {FA_HEAD_DIMS})")
+    lse_ptr = 0
+    if lse is not None:
+        _contiguous(_device_tensor(lse, "lse"), "lse")
+        if lse.dtype != torch.float32 or lse.numel() != batch * heads * seq_len:
+            raise ValueError("lse must be float32 [batch, heads, seq_len]")
+        lse_ptr = lse.data_ptr()
+    _native.call("asc_flash_attention_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse_ptr,
+                 batch, heads, seq_len, head_dim, float(sm_scale), int(bool(causal)), _stream(stream))

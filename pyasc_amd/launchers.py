@@ -1,0 +1,207 @@
+"""Registered kernel signatures: each maps one asc2 kernel of the reference (or a
+build-defined asc2-style kernel where the reference has none) onto pyasc_amd.kernels.
+
+Coverage rules follow the reference kernel bodies: the logical grid decides which
+elements a launch writes, the physical HIP grid is the library's own choice.
+"""
+from __future__ import annotations
+
+from typing import List, Tuple
+
+import torch
+
+from . import kernels
+from .asc.core import as_torch_dtype
+from .registry import KernelCall, register
+
+
+def _shape2(v, name: str) -> Tuple[int, int]:
+    shape = tuple(int(s) for s in v)
+    if len(shape) != 2:
+        raise ValueError(f"'{name}' must be a 2-D shape, got {v}")
+    return shape
+
+
+def _check_shapes(call: KernelCall) -> Tuple[int, int, int]:
+    a, b, c = call.args["a_ptr"], call.args["b_ptr"], call.args["c_ptr"]
+    M, K = _shape2(call.consts["a_shape"], "a_shape")
+    K2, N = _shape2(call.consts["b_shape"], "b_shape")
+    if K2 != K:
+        raise ValueError(f"a_shape {M, K} and b_shape {K2, N} do not chain")
+    if tuple(_shape2(call.consts["c_shape"], "c_shape")) != (M, N):
+        raise ValueError(f"c_shape must be {(M, N)}")
+    for t, n, shp in ((a, "a_ptr", (M, K)), (b, "b_ptr", (K, N)), (c, "c_ptr", (M, N))):
+        if t.numel() < shp[0] * shp[1]:
+            raise ValueError(f"'{n}' holds {t.numel()} elements, {shp} needed")
+    return M, N, K
+
+
+def _as2d(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    return t.reshape(-1)[:rows * cols].view(rows, cols)
+
+
+def _asc2_matmul_dtype(t: torch.Tensor) -> None:
+    # asc2 matmul accepts f32/f16/bf16 tiles only (python/asc/language/tile/utils.py:129-139)
+    if t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise TypeError(f"asc2 matmul supports float32, float16 and bfloat16 operands, got {t.dtype}")
+
+
+# ---------------------------------------------------------------------------------------------- vadd
+
+@register("vadd_kernel", ("x_ptr", "y_ptr", "out_ptr", "size", "tile_size", "tile_per_block"),
+          "python/test/asc2/kernels/test_vadd.py:16-28")
+def _vadd(call: KernelCall) -> None:
+    kernels.vadd(call.args["x_ptr"], call.args["y_ptr"], call.args["out_ptr"], int(call.args["size"]),
+                 int(call.consts["tile_size"]), int(call.consts["tile_per_block"]), call.grid, call.stream)
+
+
+# ------------------------------------------------------------------------------------------- softmax
+
+@register("softmax_kernel", ("x_ptr", "out_ptr", "num_rows", "num_cols", "tile_size"),
+          "python/test/asc2/kernels/test_softmax.py:16-27")
+def _softmax_rows(call: KernelCall) -> None:
+    kernels.softmax_rows(call.args["x_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
+                         int(call.get("num_cols")), int(call.get("tile_size")), call.grid, call.stream)
+
+
+@register("softmax_kernel", ("x_ptr", "out_ptr", "num_rows", "num_cols", "block_size"),
+          "python/test/asc2/kernels/test_softmax_fused.py:16-24")
+def _softmax_blocks(call: KernelCall) -> None:
+    kernels.softmax_blocks(call.args["x_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
+                           int(call.get("num_cols")), int(call.get("block_size")), call.grid, call.stream)
+
+
+# -------------------------------------------------------------------------------------------- matmul
+
+def mnblock_rectangles(M: int, N: int, grid: int, m_tile: int, m_tiles_per_block: int, n_tile: int,
+                       n_tiles_per_block: int) -> List[Tuple[int, int, int, int]]:
+    """C rectangles (m0, m1, n0, n1) written by the mnblock kernel body for a logical grid
+    (python/test/asc2/kernels/test_matmul_mnblock.py:23-36): block b starts at
+    m = (m_tile*mtpb*b) % M, n = ((m_tile*mtpb*b) // M) * n_tile*ntpb and covers
+    m_tile*mtpb rows and n_tile*ntpb columns, clipped to C."""
+    m_span, n_span = m_tile * m_tiles_per_block, n_tile * n_tiles_per_block
+    rects = set()
+    for blk in range(grid):
+        m0 = (m_span * blk) % M
+        n0 = ((m_span * blk) // M) * n_span
+        m1, n1 = min(M, m0 + m_span), min(N, n0 + n_span)
+        if m0 < m1 and n0 < n1:
+            rects.add((m0, m1, n0, n1))
+    return sorted(rects)
+
+
+def _merge_full(rects: List[Tuple[int, int, int, int]], M: int, N: int) -> List[Tuple[int, int, int, int]]:
+    covered = torch.zeros(M, N, dtype=torch.bool)
+    for m0, m1, n0, n1 in rects:
+        covered[m0:m1, n0:n1] = True
+    return [(0, M, 0, N)] if bool(covered.all()) else rects
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "m_tile",
+                            "m_tiles_per_block", "n_tile", "n_tiles_per_block"),
+          "python/test/asc2/kernels/test_matmul_mnblock.py:17-36")
+def _matmul_mnblock(call: KernelCall) -> None:
+    M, N, K = _check_shapes(call)
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    _asc2_matmul_dtype(a)
+    rects = mnblock_rectangles(M, N, call.grid, int(call.consts["m_tile"]), int(call.consts["m_tiles_per_block"]),
+                               int(call.consts["n_tile"]), int(call.consts["n_tiles_per_block"]))
+    for m0, m1, n0, n1 in _merge_full(rects, M, N):
+        kernels.matmul(a[m0:m1], b[:, n0:n1], c[m0:m1, n0:n1], stream=call.stream)
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "k_tiles"),
+          "python/test/asc2/kernels/test_matmul_tiled.py:17-31")
+def _matmul_ktiled(call: KernelCall) -> None:
+    M, N, K = _check_shapes(call)
+    k_tiles = int(call.consts["k_tiles"])
+    if k_tiles <= 0:
+        raise ValueError("k_tiles must be positive")
+    # acc = sum_{i<k_tiles} A[:, i*ko:(i+1)*ko] @ B[i*ko:(i+1)*ko, :] with ko = K // k_tiles
+    k_used = (K // k_tiles) * k_tiles
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    _asc2_matmul_dtype(a)
+    if k_used == 0:
+        c.zero_()
+        return
+    kernels.matmul(a[:, :k_used], b[:k_used], c, stream=call.stream)
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape"),
+          "python/test/asc2/kernels/test_matmul_fixpipe.py:17-27")
+def _matmul_fixpipe(call: KernelCall) -> None:
+    # c = relu(a @ b).to(c's dtype), relu and cast fused into the store
+    M, N, K = _check_shapes(call)
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    _asc2_matmul_dtype(a)
+    kernels.matmul(a, b, c, relu=True, stream=call.stream)
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "dtype"),
+          "python/test/asc2/kernels/test_matmul_l0c_to_l1.py:17-30")
+def _matmul_chained(call: KernelCall) -> None:
+    # t = (a @ b).to(dtype); c = t @ b  (needs N == K)
+    M, N, K = _check_shapes(call)
+    if N != K:
+        raise ValueError(f"the chained matmul multiplies (a@b) by b again and needs N == K, got N={N}, K={K}")
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    _asc2_matmul_dtype(a)
+    mid_dtype = as_torch_dtype(call.consts["dtype"])
+    if mid_dtype != b.dtype:
+        raise TypeError(f"the intermediate dtype {mid_dtype} must match b's dtype {b.dtype} for the second matmul")
+    t = torch.empty((M, N), dtype=mid_dtype, device=a.device)
+    kernels.matmul(a, b, t, stream=call.stream)
+    kernels.matmul(t, b, c, stream=call.stream)
+
+
+# ------------------------------------------------------------- int8 matmul (build-defined asc2 style)
+
+@register("matmul_int8_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape"),
+          "python/test/generalization/adv/test_matmul_iterate_all.py:106-120 (int8 -> int32 case)")
+def _matmul_int8(call: KernelCall) -> None:
+    M, N, K = _check_shapes(call)
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    kernels.matmul_i8(a, b, c, stream=call.stream)
+
+
+def _dequant(call: KernelCall, trunc19: bool) -> None:
+    M, N, K = _check_shapes(call)
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    scale = call.args["quant_ptr"].reshape(-1)
+    kernels.matmul_i8(a, b, c, scale=scale, trunc19=trunc19, stream=call.stream)
+
+
+@register("matmul_dequant_kernel", ("a_ptr", "b_ptr", "c_ptr", "quant_ptr", "a_shape", "b_shape", "c_shape"),
+          "python/test/generalization/adv/test_matmul_quant.py:23-51")
+def _matmul_dequant(call: KernelCall) -> None:
+    _dequant(call, False)
+
+
+@register("matmul_dequant_kernel",
+          ("a_ptr", "b_ptr", "c_ptr", "quant_ptr", "a_shape", "b_shape", "c_shape", "trunc_scale"),
+          "python/test/generalization/adv/test_matmul_quant.py:23-51,94-106")
+def _matmul_dequant_trunc(call: KernelCall) -> None:
+    _dequant(call, bool(call.consts["trunc_scale"]))
+
+
+# -------------------------------------------------------- flash attention (build-defined asc2 style)
+
+@register("flash_attention_fwd_kernel",
+          ("q_ptr", "k_ptr", "v_ptr", "o_ptr", "batch", "heads", "seq_len", "head_dim", "sm_scale", "causal",
+           "block_m", "block_n"), "none (the reference has no attention kernel)")
+def _flash_attention(call: KernelCall) -> None:
+    batch, heads, seq = int(call.get("batch")), int(call.get("heads")), int(call.get("seq_len"))
+    head_dim = int(call.get("head_dim"))
+    if int(call.get("block_m")) <= 0 or int(call.get("block_n")) <= 0:
+        raise ValueError("block_m and block_n must be positive")
+    shape = (batch, heads, seq, head_dim)
+    n = batch * heads * seq * head_dim
+    views = []
+    for name in ("q_ptr", "k_ptr", "v_ptr", "o_ptr"):
+        t = call.args[name]
+        if t.numel() < n:
+            raise ValueError(f"'{name}' holds {t.numel()} elements, {shape} needed")
+        views.append(t.reshape(-1)[:n].view(shape))
+    q, k, v, o = views
+    kernels.flash_attention_fwd(q, k, v, o, float(call.get("sm_scale")), bool(call.get("causal")),
+                                stream=call.stream)

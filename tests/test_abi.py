@@ -1,0 +1,54 @@
+"""The C ABI (include/asc_hip.h) without a GPU: the library loads, exports every
+declared entry point, and rejects invalid arguments before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from pyasc_amd import _native
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "asc_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(asc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _native.load_library()
+    names = declared_functions()
+    assert len(names) >= 11
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _native.SIGNATURES or name in _native.STRING_FUNCS, name
+
+
+def test_version_string():
+    assert "gfx950" in _native.version()
+
+
+@pytest.mark.parametrize("fn,args,code", [
+    ("asc_vadd", (0, 0, 0, 0, -1, 128, 4, 16, None), _native.ERR_INVALID_ARG),
+    ("asc_vadd", (0, 0, 0, 0, 16, 0, 4, 16, None), _native.ERR_INVALID_ARG),
+    ("asc_vadd", (0, 0, 0, 0, 16, 4, 4, 16, None), _native.ERR_INVALID_ARG),  # null buffers
+    ("asc_vadd", (9, 1, 1, 1, 16, 4, 4, 16, None), _native.ERR_UNSUPPORTED),
+    ("asc_softmax_rows_f32", (0, 0, 4, 8, 16, 1, None), _native.ERR_UNSUPPORTED),
+    ("asc_softmax_rows_f32", (0, 0, 4, 8, 0, 1, None), _native.ERR_INVALID_ARG),
+    ("asc_softmax_blocks_f32", (0, 0, 4, 8, 1, 0, None), _native.ERR_INVALID_ARG),
+])
+def test_argument_errors_are_reported(fn, args, code):
+    lib = _native.load_library()
+    rc = getattr(lib, fn)(*args)
+    assert rc == code
+    assert fn in _native.last_error()
+    with pytest.raises(RuntimeError, match=f"Function {fn} returned {code}"):
+        _native.check(rc, fn)
+
+
+def test_zero_sized_launch_is_a_noop():
+    lib = _native.load_library()
+    assert lib.asc_vadd(0, None, None, None, 0, 128, 4, 16, None) == 0
+    assert lib.asc_vadd(0, None, None, None, 100, 128, 0, 16, None) == 0  # tile_per_block 0 covers nothing

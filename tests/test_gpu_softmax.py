@@ -1,0 +1,83 @@
+"""Row softmax parity on the GPU: within 1e-6 relative of torch.softmax on the CPU
+(the reference's golden, python/test/asc2/kernels/test_softmax.py:43) and of the
+oracle; untouched columns/rows are bit-identical."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import asc2_oracle as O
+from pyasc_amd import kernels
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+RTOL = 1e-6  # north-star tolerance for softmax (relative, no absolute slack)
+
+
+def _rand(rows, cols, seed, scale=2.0):
+    return torch.randn(rows, cols, generator=torch.Generator().manual_seed(seed)) * scale
+
+
+def test_fixture_64x1024(device):
+    f = np.load(os.path.join(GOLDEN, "softmax_64x1024.npz"))
+    x = torch.from_numpy(f["x"]).to(device)
+    out = torch.empty_like(x)
+    kernels.softmax_rows(x, out, 64, 1024, 1024, 16)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu(), torch.from_numpy(f["expected"]), rtol=RTOL, atol=0)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (16384, 1024)])
+def test_config_shapes_vs_torch_cpu(device, rows, cols):
+    x = _rand(rows, cols, 1)
+    out = torch.empty(rows, cols, device=device)
+    kernels.softmax_rows(x.to(device), out, rows, cols, cols, 16)
+    torch.cuda.synchronize()
+    ref = torch.softmax(x, dim=1)
+    torch.testing.assert_close(out.cpu(), ref, rtol=RTOL, atol=0)
+    sums = out.double().sum(1).cpu()
+    assert (sums - 1).abs().max() < cols * 2**-24
+
+
+@pytest.mark.parametrize("cols", [1, 7, 64, 100, 255, 256, 300, 512, 700, 1000, 1024, 1500, 2048, 3000, 4096,
+                                  6000, 8192, 10000, 20000])
+def test_row_lengths_vs_oracle(device, cols):
+    rows = 37
+    x = _rand(rows, cols, cols)
+    out = torch.empty(rows, cols, device=device)
+    kernels.softmax_rows(x.to(device), out, rows, cols, cols, 16)
+    torch.cuda.synchronize()
+    expected = O.softmax_rows(x.numpy(), np.zeros((rows, cols), np.float32), rows, cols, cols, 16)
+    np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=RTOL, atol=0)
+    torch.testing.assert_close(out.cpu(), torch.softmax(x, 1), rtol=RTOL, atol=0)
+
+
+def test_partial_tile_leaves_columns(device):
+    rows, cols, tile = 50, 1000, 640
+    x = _rand(rows, cols, 3)
+    out = torch.full((rows, cols), 9.0, device=device)
+    kernels.softmax_rows(x.to(device), out, rows, cols, tile, 5)
+    torch.cuda.synchronize()
+    expected = O.softmax_rows(x.numpy(), np.full((rows, cols), 9.0, np.float32), rows, cols, tile, 5)
+    np.testing.assert_array_equal(out.cpu().numpy()[:, tile:], 9.0)
+    np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=RTOL, atol=0)
+
+
+@pytest.mark.parametrize("rows,cols,block,grid", [(64, 1024, 4, 16), (100, 333, 7, 10), (10, 4096, 3, 2),
+                                                  (16384, 1024, 1024, 16)])
+def test_fused_blocks_coverage(device, rows, cols, block, grid):
+    x = _rand(rows, cols, rows + cols)
+    out = torch.full((rows, cols), -2.0, device=device)
+    kernels.softmax_blocks(x.to(device), out, rows, cols, block, grid)
+    torch.cuda.synchronize()
+    expected = O.softmax_blocks(x.numpy(), np.full((rows, cols), -2.0, np.float32), rows, cols, block, grid)
+    np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=RTOL, atol=0)
+
+
+def test_extreme_rows(device):
+    x = torch.tensor([[0.0] * 8, [1e4] + [0.0] * 7, [-1e30] * 8, [3.0, -90.0, 1.0, -200.0, 0.5, 0.25, 88.0, 88.0]])
+    out = torch.empty(4, 8, device=device)
+    kernels.softmax_rows(x.to(device), out, 4, 8, 8, 2)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu(), torch.softmax(x, 1), rtol=RTOL, atol=0)

@@ -1,0 +1,268 @@
+"""Pins the CPU oracle (oracle/asc2_oracle.py) before anything is compared with it.
+
+Each check is chosen so a plausible mistake in the oracle (a dropped term, a wrong
+index, a transposed operand, a wrong rounding) fails it: hand-derived fixtures,
+literal loops of the reference kernel bodies, closed forms, and library routines
+(torch CPU) standing for the reference tests' own golden expressions.
+"""
+import os
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import asc2_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def load(name):
+    return np.load(os.path.join(GOLDEN, name))
+
+
+# ---------------------------------------------------------------------------------------------- vadd
+
+def test_vadd_coverage_fixture():
+    f = load("vadd_coverage.npz")
+    out = np.full_like(f["x"], -1.0)
+    got = O.vadd(f["x"], f["y"], out, int(f["size"]), int(f["tile_size"]), int(f["tile_per_block"]), int(f["grid"]))
+    np.testing.assert_array_equal(got, f["expected"])
+
+
+def test_vadd_reference_recipe_fixture():
+    f = load("vadd_rng2026.npz")
+    out = np.zeros_like(f["x"])
+    got = O.vadd(f["x"], f["y"], out, 8192, 128, 4, 16)
+    np.testing.assert_array_equal(got, f["expected"])
+
+
+def _kernel_body_loop(x, y, out, size, tile, tpb, grid):
+    """Literal per-element walk of test_vadd.py:22-28 with Python float32 scalars."""
+    res = list(out)
+    for b in range(grid):
+        base = b * tile * tpb
+        for i in range(tpb):
+            off = base + i * tile
+            for j in range(off, min(off + tile, size)):
+                s = struct.unpack("f", struct.pack("f", float(x[j]) + float(y[j])))[0]
+                res[j] = s
+    return np.array(res, dtype=np.float32)
+
+
+@pytest.mark.parametrize("size,tile,tpb,grid", [(300, 16, 3, 4), (1000, 128, 2, 3), (64, 8, 0, 5), (50, 7, 2, 2),
+                                                (129, 128, 1, 1)])
+def test_vadd_matches_kernel_body_loop(size, tile, tpb, grid):
+    rng = np.random.default_rng(size + tile)
+    x = rng.random(size, dtype=np.float32) * 10
+    y = rng.random(size, dtype=np.float32) * 10
+    out = np.full(size, -7.0, dtype=np.float32)
+    np.testing.assert_array_equal(O.vadd(x, y, out, size, tile, tpb, grid), _kernel_body_loop(x, y, out, size,
+                                                                                               tile, tpb, grid))
+
+
+def test_vadd_int32_wraparound_known_answers():
+    x = np.array([2**31 - 1, -2**31, -1, 123456789], dtype=np.int32)
+    y = np.array([1, -1, 1, 987654321], dtype=np.int32)
+    got = O.add_elements(x, y, "int32")
+    np.testing.assert_array_equal(got, np.array([-2**31, 2**31 - 1, 0, 1111111110], dtype=np.int32))
+
+
+def test_vadd_bf16_matches_torch_and_ties():
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(4096, generator=g).to(torch.bfloat16)
+    b = torch.randn(4096, generator=g).to(torch.bfloat16)
+    got = O.add_elements(a.view(torch.int16).numpy().view(np.uint16), b.view(torch.int16).numpy().view(np.uint16),
+                         "bfloat16")
+    np.testing.assert_array_equal(got, (a + b).view(torch.int16).numpy().view(np.uint16))
+    # 1 + 2^-8 is a tie between 1 and 1 + 2^-7 in bfloat16: RNE keeps the even 1.0 (0x3F80)
+    one = np.array([0x3F80], dtype=np.uint16)
+    tiny = O.f32_to_bf16_bits(np.array([2.0**-8], dtype=np.float32))
+    assert O.add_elements(one, tiny, "bfloat16")[0] == 0x3F80
+    # 1 + 3*2^-8 ties upward to the even 1 + 2^-6 (0x3F82)
+    assert O.f32_to_bf16_bits(np.array([1 + 3 * 2.0**-8], dtype=np.float32))[0] == 0x3F82
+
+
+def test_vadd_f16_matches_torch():
+    g = torch.Generator().manual_seed(4)
+    a = (torch.randn(4096, generator=g) * 100).to(torch.float16)
+    b = (torch.randn(4096, generator=g) * 100).to(torch.float16)
+    np.testing.assert_array_equal(O.add_elements(a.numpy(), b.numpy(), "float16"), (a + b).numpy())
+
+
+# ------------------------------------------------------------------------------------------- softmax
+
+def test_softmax_closed_forms():
+    np.testing.assert_array_equal(O.softmax_row(np.full(1024, 3.25, np.float32)), np.full(1024, 1 / 1024,
+                                                                                          np.float32))
+    # [0, ln 3] -> [1/4, 3/4]
+    got = O.softmax_row(np.array([0.0, np.log(3.0)], dtype=np.float32))
+    np.testing.assert_allclose(got, [0.25, 0.75], rtol=2e-7)
+    # a row with one dominant entry: exp(-200) underflows to 0 in fp32
+    got = O.softmax_row(np.array([0.0, -200.0, -200.0], dtype=np.float32))
+    np.testing.assert_array_equal(got, np.array([1.0, 0.0, 0.0], dtype=np.float32))
+
+
+def test_softmax_shift_invariance_and_sum():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(4096) * 2).astype(np.float32)
+    a = O.softmax_row(x)
+    b = O.softmax_row(x + np.float32(8.0))  # exact shift for |x| < 2^20
+    np.testing.assert_allclose(a, b, rtol=2e-6)
+    assert abs(float(a.astype(np.float64).sum()) - 1.0) < 4096 * 2**-24
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (16, 4096), (8, 777)])
+def test_softmax_matches_torch_golden(rows, cols):
+    g = torch.Generator().manual_seed(rows * cols)
+    x = torch.randn(rows, cols, generator=g) * 2
+    out = np.zeros((rows, cols), np.float32)
+    got = O.softmax_rows(x.numpy(), out, rows, cols, cols, 16)
+    torch.testing.assert_close(torch.from_numpy(got), torch.softmax(x, dim=1), rtol=1e-6, atol=0)
+
+
+def test_softmax_fixture_and_partial_columns():
+    f = load("softmax_64x1024.npz")
+    got = O.softmax_rows(f["x"], np.zeros_like(f["x"]), 64, 1024, 1024, 16)
+    np.testing.assert_allclose(got, f["expected"], rtol=1e-6, atol=0)
+    # tile_size < num_cols: columns >= tile_size keep their old values
+    out = np.full_like(f["x"], 5.0)
+    got = O.softmax_rows(f["x"], out, 64, 1024, 512, 3)
+    np.testing.assert_array_equal(got[:, 512:], 5.0)
+    np.testing.assert_allclose(got[:, :512], torch.softmax(torch.from_numpy(f["x"][:, :512]), 1).numpy(),
+                               rtol=1e-6, atol=0)
+    with pytest.raises(ValueError):
+        O.softmax_rows(f["x"], out, 64, 1024, 2048, 16)
+
+
+def test_softmax_blocks_coverage():
+    x = np.random.default_rng(0).standard_normal((10, 32)).astype(np.float32)
+    out = np.full_like(x, -3.0)
+    got = O.softmax_blocks(x, out, 10, 32, 3, 2)  # rows [0, 6) written
+    np.testing.assert_array_equal(got[6:], -3.0)
+    np.testing.assert_allclose(got[:6], torch.softmax(torch.from_numpy(x[:6]), 1).numpy(), rtol=1e-6, atol=0)
+    got = O.softmax_blocks(x, out, 10, 32, 4, 16)  # last block clipped at row 10
+    np.testing.assert_allclose(got, torch.softmax(torch.from_numpy(x), 1).numpy(), rtol=1e-6, atol=0)
+
+
+# -------------------------------------------------------------------------------------------- matmul
+
+def _loop_matmul(a, b):
+    M, K = a.shape
+    N = b.shape[1]
+    c = np.zeros((M, N))
+    for i in range(M):
+        for j in range(N):
+            c[i, j] = sum(float(a[i, k]) * float(b[k, j]) for k in range(K))
+    return c
+
+
+def test_matmul_identity_permutation_and_loop():
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((12, 20)).astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(O.matmul(a, np.eye(20, dtype=np.float32)), a)
+    perm = np.eye(20, dtype=np.float32)[::-1]
+    np.testing.assert_array_equal(O.matmul(a, perm), a[:, ::-1])
+    b = rng.standard_normal((20, 7)).astype(np.float16).astype(np.float32)
+    np.testing.assert_allclose(O.matmul(a, b), _loop_matmul(a, b), rtol=1e-6, atol=1e-6)
+    # the transposed product is not accepted as the product
+    sq = rng.standard_normal((8, 8)).astype(np.float32)
+    sq2 = rng.standard_normal((8, 8)).astype(np.float32)
+    assert not np.allclose(O.matmul(sq, sq2), O.matmul(sq2, sq))
+
+
+def test_matmul_relu_cast_matches_torch_fixpipe_golden():
+    g = torch.Generator().manual_seed(5)
+    for dtype, out in ((torch.float16, "float16"), (torch.bfloat16, "float16")):
+        a = (torch.rand((64, 128), generator=g, dtype=dtype) - .5) * 10
+        b = (torch.rand((128, 256), generator=g, dtype=dtype) - .5) * 10
+        ref = (a.to(torch.float32) @ b.to(torch.float32)).relu().to(torch.float16)
+        got = O.matmul(a.float().numpy(), b.float().numpy(), relu=True, out_dtype=out)
+        torch.testing.assert_close(torch.from_numpy(got), ref, atol=1e-3, rtol=1e-3)
+    bits = O.matmul(np.array([[1.0, 2.0 ** -8]], np.float32), np.array([[1.0], [1.0]], np.float32),
+                    out_dtype="bfloat16")
+    assert bits[0, 0] == 0x3F80  # 1 + 2^-8 rounds to even 1.0 in bfloat16
+
+
+def test_matmul_mnblock_fixture():
+    f = load("matmul_mnblock_f16.npz")
+    for idx in range(len(f["cases"])):
+        got = O.matmul(f[f"a{idx}"].astype(np.float32), f[f"b{idx}"].astype(np.float32))
+        np.testing.assert_allclose(got, f[f"c{idx}"], rtol=1e-5, atol=1e-5)
+
+
+def test_mnblock_rectangles():
+    cases = [(16, 16, 16, 1, 16, 16, 1), (16, 160, 16, 1, 16, 16, 1), (32, 16, 16, 2, 16, 16, 1),
+             (16, 16, 32, 2, 16, 16, 1), (32, 16, 32, 2, 16, 16, 1), (32, 16, 32, 2, 16, 16, 2),
+             (32, 16, 32, 4, 16, 16, 1), (480, 224, 1344, 30, 48, 32, 7)]
+    for m, k, n, core_num, m_tile, n_tile, ntpb in cases:
+        tiles_per_core = (m // m_tile) * (n // n_tile) // core_num
+        mtpb = tiles_per_core // ntpb
+        rects = O.mnblock_rectangles(m, n, core_num, m_tile, mtpb, n_tile, ntpb)
+        cover = np.zeros((m, n), dtype=int)
+        for m0, m1, n0, n1 in rects:
+            cover[m0:m1, n0:n1] += 1
+        assert (cover == 1).all(), (m, k, n)
+    # hand-derived partial grid: M=32, N=32, 16x16 tiles, 1 tile per block, 2 blocks
+    # block 0 -> (0, 0), block 1 -> (16, 0): only the left column of tiles
+    assert O.mnblock_rectangles(32, 32, 2, 16, 1, 16, 1) == [(0, 16, 0, 16), (16, 32, 0, 16)]
+
+
+# ---------------------------------------------------------------------------------------- int8 matmul
+
+def test_matmul_i8_loop_and_extremes():
+    rng = np.random.default_rng(3)
+    a = rng.integers(-127, 128, (9, 33), dtype=np.int8)
+    b = rng.integers(-127, 128, (33, 5), dtype=np.int8)
+    np.testing.assert_array_equal(O.matmul_i8_acc(a, b), _loop_matmul(a.astype(np.int64), b.astype(np.int64)))
+    K = 4096
+    a = np.full((2, K), -128, dtype=np.int8)
+    b = np.full((K, 3), -128, dtype=np.int8)
+    np.testing.assert_array_equal(O.matmul_i8_acc(a, b), np.full((2, 3), 128 * 128 * K, dtype=np.int32))
+    a[0] = 127
+    np.testing.assert_array_equal(O.matmul_i8_acc(a, b)[0], np.full(3, -127 * 128 * K, dtype=np.int32))
+
+
+def test_dequant_known_answers():
+    acc = np.array([[1, -3, 70000, 2049]], dtype=np.int32)
+    scale = np.array([0.5, 0.25, 1.0, 1.0], dtype=np.float32)
+    got = O.dequant_f16(acc, scale)
+    # 70000 overflows fp16 to inf; 2049 is a tie between 2048 and 2050 -> even 2048
+    np.testing.assert_array_equal(got, np.array([[0.5, -0.75, np.inf, 2048.0]], dtype=np.float16))
+    assert O.trunc19(np.array([1.0 + 2.0**-11], np.float32))[0] == np.float32(1.0)
+    assert O.trunc19(np.array([1.0 + 2.0**-10], np.float32))[0] == np.float32(1.0 + 2.0**-10)
+
+
+def test_dequant_reference_golden_fixture():
+    f = load("matmul_quant.npz")
+    for idx in range(3):
+        acc = O.matmul_i8_acc(f[f"a{idx}"], f[f"b{idx}"])
+        np.testing.assert_array_equal(acc, f[f"acc{idx}"])
+        gold = O.dequant_reference_golden(acc, f[f"scale{idx}"])
+        np.testing.assert_array_equal(gold, f[f"golden{idx}"])
+        assert np.abs(acc).max() <= 2048
+        np.testing.assert_array_equal(O.dequant_f16(acc, f[f"scale{idx}"], use_trunc19=True), gold)
+
+
+# --------------------------------------------------------------------------------- flash attention
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(4)
+    S, D = 37, 16
+    q, k, v = (rng.standard_normal((S, D)) for _ in range(3))
+    out = O.attention(q, k, v, 0.3, causal=True)
+    np.testing.assert_allclose(out[0], v[0], rtol=1e-12)  # row 0 sees only key 0
+    z = np.zeros((S, D))
+    np.testing.assert_allclose(O.attention(z, k, v, 1.0, causal=False), np.tile(v.mean(0), (S, 1)), rtol=1e-12)
+    prefix = np.cumsum(v, axis=0) / np.arange(1, S + 1)[:, None]
+    np.testing.assert_allclose(O.attention(z, k, v, 1.0, causal=True), prefix, rtol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_matches_torch_sdpa(causal):
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(1, 2, 64, 32, generator=g) for _ in range(3))
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=0.2)
+    for h in range(2):
+        got = O.attention(q[0, h].numpy(), k[0, h].numpy(), v[0, h].numpy(), 0.2, causal)
+        np.testing.assert_allclose(got, ref[0, h].numpy(), rtol=1e-4, atol=1e-5)

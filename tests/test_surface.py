@@ -1,0 +1,158 @@
+"""Launch-surface behaviour (CPU only): decorator options, argument classification,
+ConstExpr handling, signature dispatch and error paths of the asc/asc2 drop-in.
+The native launch is replaced by a recorder, as the reference's unit tests patch
+Launcher.run (python/test/unit/conftest.py:35-38)."""
+import numpy as np
+import pytest
+import torch
+
+import asc
+import asc2
+import asc.runtime.config as config
+from pyasc_amd import registry
+from pyasc_amd.asc.runtime import launcher as launcher_mod
+from pyasc_amd.asc.runtime.jit import JITFunction
+from pyasc_amd.launchers import mnblock_rectangles
+
+
+@asc2.jit(always_compile=True)
+def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+    x_gm = asc2.tensor(x_ptr, [size])  # never executed
+    asc2.store(x_gm, x_gm, offsets=[0])
+
+
+@pytest.fixture
+def recorded(monkeypatch):
+    calls = []
+
+    def fake_run(self, entry, function_name, runtime_args, constexprs):
+        calls.append((entry, function_name, runtime_args, constexprs, self.options))
+
+    monkeypatch.setattr(launcher_mod.Launcher, "run", fake_run)
+    return calls
+
+
+def test_dispatch_by_signature(recorded):
+    x = np.zeros(8192, np.float32)
+    vadd_kernel[16](x, x, x, 8192, 128, 4)
+    entry, name, rt, ce, opts = recorded[0]
+    assert name == "vadd_kernel" and entry.params[-1] == "tile_per_block"
+    assert entry.reference.startswith("python/test/asc2/kernels/test_vadd.py")
+    assert list(rt) == ["x_ptr", "y_ptr", "out_ptr", "size"] and ce == {"tile_size": 128, "tile_per_block": 4}
+    assert opts.core_num == 16 and opts.stream is None
+
+
+def test_launch_tuple_with_stream(recorded):
+    x = torch.zeros(16)
+    vadd_kernel[4, 1234](x, x, x, 16, 4, 1)
+    assert recorded[0][4].core_num == 4 and recorded[0][4].stream == 1234
+
+
+def test_bad_launch_options():
+    with pytest.raises(TypeError, match="Parse user launch options failed"):
+        vadd_kernel[1, 2, 3]
+
+
+def test_unknown_option_and_clash():
+    with pytest.raises(RuntimeError, match="unknown"):
+        asc2.jit(not_an_option=1)(lambda x: None)
+
+    def k(x, always_compile):
+        pass
+
+    with pytest.raises(RuntimeError, match="conflict"):
+        asc2.jit(k)
+
+
+def test_reference_option_names_accepted():
+    for opt in ("vf_fusion", "always_compile", "opt_level", "insert_sync", "static_alloc", "kernel_type"):
+        asc2.jit(**{opt: None})(lambda x: None)
+
+
+def test_constexpr_type_check(recorded):
+    with pytest.raises(RuntimeError, match=r"ConstExpr\[int\] is required for 'tile_size'"):
+        vadd_kernel[1](np.zeros(4, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 1.5, 1)
+
+
+def test_arg_type_classification():
+    gat = JITFunction.get_arg_type
+    assert gat(True).kind == "plain" and str(gat(True).dtype) == "int8"
+    assert str(gat(3).dtype) == "int32" and str(gat(3.0).dtype) == "float32"
+    assert gat(np.zeros(3, np.float16)).kind == "pointer"
+    assert gat(np.float32(1)).kind == "plain"
+    assert gat(torch.zeros(2, dtype=torch.bfloat16)).kind == "pointer"
+    t0 = gat(torch.tensor(1.0, dtype=torch.bfloat16))
+    assert t0.kind == "plain" and str(t0.dtype) == "bfloat16"
+    with pytest.raises(TypeError, match="not supported: str"):
+        gat("x")
+
+
+def test_unsupported_runtime_arg_raises(recorded):
+    with pytest.raises(TypeError):
+        vadd_kernel[1]("a", "b", "c", 4, 1, 1)
+
+
+def test_unknown_kernel_raises():
+
+    @asc2.jit
+    def my_kernel(a_ptr: asc.GlobalAddress, n: int):
+        pass
+
+    with pytest.raises(NotImplementedError, match="my_kernel"):
+        my_kernel[1](np.zeros(4, np.float32), 4)
+
+
+def test_core_num_and_dry_run(monkeypatch):
+    monkeypatch.delenv("DRY_RUN", raising=False)
+    with pytest.raises(ValueError, match="Core number"):
+        vadd_kernel[0](np.zeros(4, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 4, 1)
+    monkeypatch.setenv("DRY_RUN", "1")
+    vadd_kernel[1](np.zeros(4, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 4, 1)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error")
+def test_no_device_fails_loudly(monkeypatch):
+    monkeypatch.delenv("DRY_RUN", raising=False)
+    with pytest.raises(RuntimeError, match="No HIP device"):
+        vadd_kernel[1](np.zeros(4, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 4, 1)
+
+
+def test_tile_ops_are_not_callable_outside_kernels():
+    with pytest.raises(RuntimeError, match="only appear inside"):
+        asc2.load(None, [1], offsets=[0])
+    with pytest.raises(ValueError):
+        asc2.range(4, unroll_factor=0)
+
+
+def test_kernel_called_without_grid():
+    with pytest.raises(TypeError, match="launch it as"):
+        vadd_kernel(1, 2, 3, 4, 5, 6)
+
+
+def test_registry_contents():
+    names = {(n, p[-1]) for n, p in registry.entries()}
+    assert ("softmax_kernel", "tile_size") in names and ("softmax_kernel", "block_size") in names
+    assert sum(1 for n, _ in names if n == "matmul_kernel") == 4
+    assert ("flash_attention_fwd_kernel", "block_n") in names
+    assert ("matmul_dequant_kernel", "c_shape") in names
+
+
+def test_set_platform_surface():
+    with pytest.raises(ValueError):
+        config.set_platform("Bogus")
+    config.set_platform(config.Backend.Model, config.Platform.Ascend950PR_9599, 0, check=False)
+    assert config.platform_to_arch(config.Platform.Ascend950PR_9599) == config.CompilationArch.C310
+    assert config.platform_to_arch(config.Platform.MI355X) == config.CompilationArch.GFX950
+
+
+def test_launcher_mnblock_rectangles_merge():
+    # all 8 parametrisations of test_matmul_mnblock.py cover C exactly
+    rects = mnblock_rectangles(480, 1344, 30, 48, 2, 32, 7)  # 420 tiles, 14 per block
+    area = sum((m1 - m0) * (n1 - n0) for m0, m1, n0, n1 in rects)
+    assert area == 480 * 1344
+
+
+def test_ceildiv_and_dtypes():
+    assert asc.ceildiv(8192, 128) == 64 and asc.ceildiv(1, 16) == 1
+    assert asc.float16.to_torch() == torch.float16 and asc.bfloat16.is_float() and asc.int8.is_int()
