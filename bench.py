@@ -151,14 +151,74 @@ class Vadd(Workload):
                 "kind": "port", "sample": f"x + y on {n} fp32 elements (README.md:53)", "seconds_per_call": secs}
 
 
+class Matmul(Workload):
+    bound, unit, kernel_hint = "mfma", "TFLOP/s", "gemm_mfma"
+
+    def __init__(self, n: int, dtype: str):
+        self.n, self.dt = n, dtype
+        self.dtype = {"bfloat16": "bf16", "float16": "f16"}[dtype]
+        self.peak = BF16_PEAK_TFLOPS if dtype == "bfloat16" else FP16_PEAK_TFLOPS
+        self.name = f"matmul_{n}x{n}x{n}_{self.dtype}"
+
+    def setup(self, dev):
+        import torch
+        td = getattr(torch, self.dt)
+        g = torch.Generator(device=dev).manual_seed(2)
+        self.a = (torch.randn(self.n, self.n, device=dev, generator=g) / math.sqrt(self.n)).to(td)
+        self.b = (torch.randn(self.n, self.n, device=dev, generator=g) / math.sqrt(self.n)).to(td)
+        self.c = torch.empty(self.n, self.n, device=dev, dtype=td)
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        kernels.matmul(self.a, self.b, self.c)
+
+    def work(self) -> float:
+        return 2.0 * self.n ** 3
+
+    def config(self) -> dict:
+        return {"workload": self.name, "M": self.n, "N": self.n, "K": self.n, "layout": "A row-major, B row-major",
+                "input": "randn/sqrt(K), seed 2", "accumulate": "fp32", "out": self.dtype}
+
+
+class MatmulI8(Workload):
+    bound, unit, dtype, kernel_hint = "mfma", "TOPS", "int8", "gemm_i8"
+    peak = INT8_PEAK_TOPS
+
+    def __init__(self, M: int, N: int, K: int):
+        self.M, self.N, self.K = M, N, K
+        self.name = f"matmul_i8_dequant_{M}x{N}x{K}"
+
+    def setup(self, dev):
+        import torch
+        g = torch.Generator(device=dev).manual_seed(3)
+        self.a = torch.randint(-127, 128, (self.M, self.K), dtype=torch.int8, device=dev, generator=g)
+        self.b = torch.randint(-127, 128, (self.K, self.N), dtype=torch.int8, device=dev, generator=g)
+        self.s = torch.rand(self.N, device=dev, generator=g) * 0.009 + 0.001
+        self.c = torch.empty(self.M, self.N, dtype=torch.float16, device=dev)
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        kernels.matmul_i8(self.a, self.b, self.c, scale=self.s)
+
+    def work(self) -> float:
+        return 2.0 * self.M * self.N * self.K
+
+    def config(self) -> dict:
+        return {"workload": self.name, "M": self.M, "N": self.N, "K": self.K, "accumulate": "int32 (exact)",
+                "epilogue": "fp16(fp32(acc) * scale[n])", "input": "int8 uniform[-127,127], seed 3"}
+
+
 WORKLOADS = {
     "softmax_4096x4096": lambda: Softmax(4096, 4096),
     "softmax_16384x1024": lambda: Softmax(16384, 1024),
     "vadd_268435456": lambda: Vadd(1 << 28),
     "vadd_8192": lambda: Vadd(8192),
+    "matmul_bf16_8192": lambda: Matmul(8192, "bfloat16"),
+    "matmul_f16_8192": lambda: Matmul(8192, "float16"),
+    "matmul_i8_4096x11008x4096": lambda: MatmulI8(4096, 11008, 4096),
 }
 HEADLINE = "softmax_4096x4096"
-SUITE = ["softmax_16384x1024", "vadd_268435456"]
+SUITE = ["softmax_16384x1024", "vadd_268435456", "matmul_bf16_8192", "matmul_f16_8192", "matmul_i8_4096x11008x4096"]
 
 
 def _time_cpu(fn, budget_s: float) -> float:

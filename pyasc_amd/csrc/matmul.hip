@@ -1,5 +1,322 @@
+// Dense matmul C = epilogue(A . B) for the asc2 cube path
+// (python/asc/language/tile/binary_ops.py:180-221; kernels in
+// python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py).
+//
+// fp16/bf16 inputs run on MFMA (v_mfma_f32_32x32x16_{bf16,f16}) with fp32
+// accumulation:
+//   - 256x256 output tile per 256-thread workgroup, 4 waves in 2x2, each wave
+//     owns 128x128 = 4x4 MFMA blocks (256 fp32 accumulators per lane);
+//   - K advances 64 at a time through two LDS stages (2 x 64 KiB): while one
+//     stage feeds the MFMAs, the next k-tile is fetched from HBM into registers
+//     and written to the other stage;
+//   - A (row-major, K contiguous) is copied as is; B (row-major, N contiguous)
+//     is transposed in registers (8x8 blocks of 16-bit, v_perm_b32) so both LDS
+//     tiles are K-contiguous and every MFMA operand is one ds_read_b128;
+//   - XCD-aware, grouped tile order (gemm_common.h).
+// The epilogue applies the fixpipe relu and the RNE cast to fp16/bf16, or
+// stores fp32 as is.  Shapes that are not multiples of the tile run the same
+// kernel with bounds-checked loads (zero fill) and masked stores.
+//
+// fp32 inputs (test_matmul_fixpipe.py's float32 case) use a plain LDS-tiled
+// FMA kernel.
 #include "common.h"
-extern "C" int32_t asc_matmul(int32_t, int32_t, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
-                              int64_t, int64_t, int32_t, asc_stream_t) {
-  return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: not built yet");
+#include "gemm_common.h"
+#include "numeric.h"
+
+namespace {
+
+using asc::gemm::u32x4;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256;
+constexpr int BN = 256;
+constexpr int BK = 64;             // 16-bit elements per LDS row = 128 bytes
+constexpr int kThreads = 256;
+constexpr int kStageBytes = (BM + BN) * 128;
+constexpr int kGroupM = 8;
+
+enum OutKind { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
+
+struct GemmArgs {
+  const uint16_t* a;
+  const uint16_t* b;
+  void* c;
+  int M, N, K;
+  int64_t lda, ldb, ldc;
+  int relu;
+  int tiles_m, tiles_n;
+};
+
+template <bool kBf16>
+__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+// 8 consecutive 16-bit elements p[0..7] of row `row`, columns col..col+7 of a
+// row-major [rows x cols] matrix; out-of-range elements read as 0.
+template <bool kChecked>
+__device__ __forceinline__ u32x4 load_chunk(const uint16_t* base, int64_t ld, int row, int col, int rows, int cols,
+                                            bool vec_ok) {
+  const uint16_t* p = base + row * ld + col;
+  if (!kChecked) return *reinterpret_cast<const u32x4*>(p);
+  if (row < rows && vec_ok && col + 7 < cols) return *reinterpret_cast<const u32x4*>(p);
+  uint16_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = (row < rows && col + i < cols) ? p[i] : uint16_t(0);
+  u32x4 v;
+  __builtin_memcpy(&v, e, 16);
+  return v;
+}
+
+template <bool kBf16, bool kChecked, int kOut>
+__global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tm, tn;
+  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // vector loads need 16-byte aligned chunks
+  const bool a_vec = ((reinterpret_cast<uintptr_t>(p.a) | (p.lda * 2)) & 15) == 0;
+  const bool b_vec = ((reinterpret_cast<uintptr_t>(p.b) | (p.ldb * 2)) & 15) == 0;
+
+  // A loader: chunk c = tid + 256*i -> row c/8, k-chunk c%8
+  // B loader: one 8(k) x 8(n) block per thread: n-chunk tid%32, k-group tid/32
+  const int b_nc = tid & 31, b_kg = tid >> 5;
+
+  u32x4 ra[8], rb[8];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + kThreads * i;
+      ra[i] = load_chunk<kChecked>(p.a, p.lda, m0 + (c >> 3), k0 + (c & 7) * 8, p.M, p.K, a_vec);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      rb[r] = load_chunk<kChecked>(p.b, p.ldb, k0 + b_kg * 8 + r, n0 + b_nc * 8, p.K, p.N, b_vec);
+    }
+  };
+  auto stash = [&](int stage) {
+    uint8_t* as = smem + stage * kStageBytes;
+    uint8_t* bs = as + BM * 128;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + kThreads * i;
+      *reinterpret_cast<u32x4*>(as + asc::gemm::lds_offset(c >> 3, c & 7)) = ra[i];
+    }
+    u32x4 tb[8];
+    asc::gemm::transpose8x8_b16(rb, tb);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      *reinterpret_cast<u32x4*>(bs + asc::gemm::lds_offset(b_nc * 8 + e, b_kg)) = tb[e];
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  const int k_tiles = (p.K + BK - 1) / BK;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+
+  const int arow = wm * 128 + (lane & 31);
+  const int brow = wn * 128 + (lane & 31);
+  const int khalf = lane >> 5;
+
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int stage = kt & 1;
+    if (kt + 1 < k_tiles) fetch((kt + 1) * BK);
+    const uint8_t* as = smem + stage * kStageBytes;
+    const uint8_t* bs = as + BM * 128;
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int chunk = s * 2 + khalf;
+      u32x4 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = *reinterpret_cast<const u32x4*>(as + asc::gemm::lds_offset(arow + i * 32, chunk));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        fb[j] = *reinterpret_cast<const u32x4*>(bs + asc::gemm::lds_offset(brow + j * 32, chunk));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<kBf16>(fa[i], fb[j], acc[i][j]);
+    }
+    if (kt + 1 < k_tiles) stash(stage ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue.  MFMA 32x32 result layout: lane holds column lane%32 of the block,
+  // register r holds row 8*(r/4) + 4*(lane/32) + r%4.
+  const int col_in = lane & 31;
+  const int row_q = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 128 + j * 32 + col_in;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
+        if (kChecked && (m >= p.M || n >= p.N)) continue;
+        float v = acc[i][j][r];
+        if (p.relu) v = fmaxf(v, 0.0f);
+        const int64_t off = static_cast<int64_t>(m) * p.ldc + n;
+        if constexpr (kOut == kOutF32) {
+          static_cast<float*>(p.c)[off] = v;
+        } else if constexpr (kOut == kOutF16) {
+          static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
+        } else {
+          static_cast<uint16_t*>(p.c)[off] = asc::f32_to_bf16_rne(v);
+        }
+      }
+    }
+  }
+}
+
+// ---- fp32 inputs: LDS-tiled FMA kernel (64x64 tile, 256 threads, 4x4 per thread)
+template <int kOut>
+__global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                       void* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                                                       int64_t ldc, int relu) {
+  __shared__ float as[16][64 + 1];
+  __shared__ float bs[16][64 + 1];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      const int kk = i & 15, mm = i >> 4;
+      as[kk][mm] = (m0 + mm < M && k0 + kk < K) ? a[(m0 + mm) * lda + k0 + kk] : 0.f;
+      const int nn = i & 63, kb = i >> 6;
+      bs[kb][nn] = (n0 + nn < N && k0 + kb < K) ? b[(k0 + kb) * ldb + n0 + nn] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(as[kk][ty * 4 + i], bs[kk][tx * 4 + j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+      if (m >= M || n >= N) continue;
+      float v = relu ? fmaxf(acc[i][j], 0.f) : acc[i][j];
+      const int64_t off = static_cast<int64_t>(m) * ldc + n;
+      if constexpr (kOut == kOutF32) static_cast<float*>(c)[off] = v;
+      else if constexpr (kOut == kOutF16) static_cast<uint16_t*>(c)[off] = asc::f32_to_f16_rne(v);
+      else static_cast<uint16_t*>(c)[off] = asc::f32_to_bf16_rne(v);
+    }
+  }
+}
+
+template <bool kBf16, bool kChecked, int kOut>
+int32_t launch_mfma(const GemmArgs& p, hipStream_t stream) {
+  auto kern = gemm_mfma_kernel<kBf16, kChecked, kOut>;
+  static bool configured = false;  // per instantiation; the attribute is idempotent
+  if (!configured) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
+    if (err != hipSuccess)
+      return asc::set_error(static_cast<int32_t>(err), "asc_matmul: hipFuncSetAttribute: %s", hipGetErrorString(err));
+    configured = true;
+  }
+  const int blocks = p.tiles_m * p.tiles_n;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), 2 * kStageBytes, stream, p);
+  return asc::check_launch("asc_matmul");
+}
+
+template <bool kBf16, int kOut>
+int32_t dispatch_checked(const GemmArgs& p, bool fast, hipStream_t stream) {
+  return fast ? launch_mfma<kBf16, false, kOut>(p, stream) : launch_mfma<kBf16, true, kOut>(p, stream);
+}
+
+template <bool kBf16>
+int32_t dispatch_out(const GemmArgs& p, int out_dtype, bool fast, hipStream_t stream) {
+  switch (out_dtype) {
+    case ASC_DT_FLOAT32: return dispatch_checked<kBf16, kOutF32>(p, fast, stream);
+    case ASC_DT_FLOAT16: return dispatch_checked<kBf16, kOutF16>(p, fast, stream);
+    case ASC_DT_BFLOAT16: return dispatch_checked<kBf16, kOutBF16>(p, fast, stream);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
+  }
+}
+
+}  // namespace
+
+extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M,
+                              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,
+                              asc_stream_t stream) {
+  ASC_REQUIRE(M >= 0 && N >= 0 && K >= 0, ASC_ERR_INVALID_ARG, "asc_matmul: negative shape");
+  ASC_REQUIRE(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), ASC_ERR_UNSUPPORTED, "asc_matmul: shape too large");
+  ASC_REQUIRE(lda >= K && ldb >= N && ldc >= N, ASC_ERR_INVALID_ARG,
+              "asc_matmul: leading dimensions (%lld, %lld, %lld) smaller than the rows", (long long)lda,
+              (long long)ldb, (long long)ldc);
+  if (M == 0 || N == 0) return ASC_OK;
+  ASC_REQUIRE(a && b && c, ASC_ERR_INVALID_ARG, "asc_matmul: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (in_dtype == ASC_DT_FLOAT32) {
+    dim3 grid(static_cast<uint32_t>((N + 63) / 64), static_cast<uint32_t>((M + 63) / 64));
+    const float* af = static_cast<const float*>(a);
+    const float* bf = static_cast<const float*>(b);
+    switch (out_dtype) {
+      case ASC_DT_FLOAT32:
+        hipLaunchKernelGGL(gemm_f32_kernel<kOutF32>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
+                           ldb, ldc, relu);
+        break;
+      case ASC_DT_FLOAT16:
+        hipLaunchKernelGGL(gemm_f32_kernel<kOutF16>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
+                           ldb, ldc, relu);
+        break;
+      case ASC_DT_BFLOAT16:
+        hipLaunchKernelGGL(gemm_f32_kernel<kOutBF16>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
+                           ldb, ldc, relu);
+        break;
+      default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
+    }
+    return asc::check_launch("asc_matmul");
+  }
+  ASC_REQUIRE(in_dtype == ASC_DT_FLOAT16 || in_dtype == ASC_DT_BFLOAT16, ASC_ERR_UNSUPPORTED,
+              "asc_matmul: unsupported input dtype %d", in_dtype);
+  GemmArgs p;
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  p.c = c;
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.lda = lda;
+  p.ldb = ldb;
+  p.ldc = ldc;
+  p.relu = relu;
+  p.tiles_m = static_cast<int>((M + BM - 1) / BM);
+  p.tiles_n = static_cast<int>((N + BN - 1) / BN);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
+                       (lda % 8) == 0 && (ldb % 8) == 0;
+  const bool fast = aligned && (M % BM) == 0 && (N % BN) == 0 && (K % BK) == 0 && K > 0;
+  // K == 0 takes the checked kernel: no k-tile runs and C receives cast(0).
+  return in_dtype == ASC_DT_BFLOAT16 ? dispatch_out<true>(p, out_dtype, fast, s)
+                                     : dispatch_out<false>(p, out_dtype, fast, s);
 }

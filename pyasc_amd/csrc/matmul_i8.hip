@@ -1,9 +1,241 @@
+// int8 GEMM with exact int32 accumulation and the per-output-channel fp16
+// dequant of the reference's DEQF16 fixpipe mode
+// (python/test/generalization/adv/test_matmul_quant.py:23-51,94-106;
+//  lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:116-117).
+//
+// Same structure as the fp16/bf16 kernel (matmul.hip) on v_mfma_i32_32x32x32_i8:
+// 256x256 output tile, 4 waves of 128x128, K advancing 128 bytes per LDS stage
+// (128-byte LDS rows, swizzled chunks), B transposed in registers as 16(k) x
+// 8(n) byte blocks (64 v_perm_b32 per block).  The epilogue either stores the
+// int32 accumulators or out = fp16_rne(fp32_rne(acc) * s[n]) with s[n] the
+// fp32 scale (optionally with its low 13 mantissa bits cleared, the reference
+// golden's trunc-19 form).
 #include "common.h"
-extern "C" int32_t asc_matmul_i8_i32(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t,
-                                     asc_stream_t) {
-  return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul_i8_i32: not built yet");
+#include "gemm_common.h"
+#include "numeric.h"
+
+namespace {
+
+using asc::gemm::u32x2;
+using asc::gemm::u32x4;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256;
+constexpr int BN = 256;
+constexpr int BK = 128;  // int8 elements per LDS row = 128 bytes
+constexpr int kThreads = 256;
+constexpr int kStageBytes = (BM + BN) * 128;
+constexpr int kGroupM = 8;
+
+struct I8Args {
+  const int8_t* a;
+  const int8_t* b;
+  const float* scale;
+  void* c;
+  int M, N, K;
+  int trunc19;
+  int tiles_m, tiles_n;
+};
+
+template <bool kChecked>
+__device__ __forceinline__ u32x4 load16(const int8_t* base, int64_t ld, int row, int col, int rows, int cols,
+                                        bool vec_ok) {
+  const int8_t* p = base + row * ld + col;
+  if (!kChecked) return *reinterpret_cast<const u32x4*>(p);
+  if (row < rows && vec_ok && col + 15 < cols) return *reinterpret_cast<const u32x4*>(p);
+  uint8_t e[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) e[i] = (row < rows && col + i < cols) ? static_cast<uint8_t>(p[i]) : uint8_t(0);
+  u32x4 v;
+  __builtin_memcpy(&v, e, 16);
+  return v;
 }
-extern "C" int32_t asc_matmul_i8_dequant_f16(const int8_t*, const int8_t*, const float*, void*, int64_t, int64_t,
-                                             int64_t, int32_t, asc_stream_t) {
-  return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul_i8_dequant_f16: not built yet");
+
+template <bool kChecked>
+__device__ __forceinline__ u32x2 load8(const int8_t* base, int64_t ld, int row, int col, int rows, int cols,
+                                       bool vec_ok) {
+  const int8_t* p = base + row * ld + col;
+  if (!kChecked) return *reinterpret_cast<const u32x2*>(p);
+  if (row < rows && vec_ok && col + 7 < cols) return *reinterpret_cast<const u32x2*>(p);
+  uint8_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = (row < rows && col + i < cols) ? static_cast<uint8_t>(p[i]) : uint8_t(0);
+  u32x2 v;
+  __builtin_memcpy(&v, e, 8);
+  return v;
+}
+
+// kMode: 0 = int32 accumulators, 1 = fp16 dequant
+template <bool kChecked, int kMode>
+__global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tm, tn;
+  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int64_t lda = p.K, ldb = p.N;
+  const bool a_vec = ((reinterpret_cast<uintptr_t>(p.a) | static_cast<uintptr_t>(lda)) & 15) == 0;
+  const bool b_vec = ((reinterpret_cast<uintptr_t>(p.b) | static_cast<uintptr_t>(ldb)) & 7) == 0;
+
+  // B loader: one 16(k) x 8(n) byte block per thread: n-chunk tid%32, k-group tid/32
+  const int b_nc = tid & 31, b_kg = tid >> 5;
+
+  u32x4 ra[8];
+  u32x2 rb[16];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + kThreads * i;
+      ra[i] = load16<kChecked>(p.a, lda, m0 + (c >> 3), k0 + (c & 7) * 16, p.M, p.K, a_vec);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      rb[r] = load8<kChecked>(p.b, ldb, k0 + b_kg * 16 + r, n0 + b_nc * 8, p.K, p.N, b_vec);
+    }
+  };
+  auto stash = [&](int stage) {
+    uint8_t* as = smem + stage * kStageBytes;
+    uint8_t* bs = as + BM * 128;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + kThreads * i;
+      *reinterpret_cast<u32x4*>(as + asc::gemm::lds_offset(c >> 3, c & 7)) = ra[i];
+    }
+    u32x4 tb[8];
+    asc::gemm::transpose16x8_b8(rb, tb);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      *reinterpret_cast<u32x4*>(bs + asc::gemm::lds_offset(b_nc * 8 + e, b_kg)) = tb[e];
+    }
+  };
+
+  i32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = i32x16{};
+
+  const int k_tiles = (p.K + BK - 1) / BK;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+
+  const int arow = wm * 128 + (lane & 31);
+  const int brow = wn * 128 + (lane & 31);
+  const int khalf = lane >> 5;
+
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int stage = kt & 1;
+    if (kt + 1 < k_tiles) fetch((kt + 1) * BK);
+    const uint8_t* as = smem + stage * kStageBytes;
+    const uint8_t* bs = as + BM * 128;
+#pragma unroll
+    for (int s = 0; s < BK / 32; ++s) {
+      const int chunk = s * 2 + khalf;
+      u32x4 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = *reinterpret_cast<const u32x4*>(as + asc::gemm::lds_offset(arow + i * 32, chunk));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        fb[j] = *reinterpret_cast<const u32x4*>(bs + asc::gemm::lds_offset(brow + j * 32, chunk));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fa[i]),
+                                                            __builtin_bit_cast(i32x4, fb[j]), acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < k_tiles) stash(stage ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds column lane%32 of each 32x32 block, register r row
+  // 8*(r/4) + 4*(lane/32) + r%4.
+  const int col_in = lane & 31;
+  const int row_q = (lane >> 5) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 128 + j * 32 + col_in;
+    float s = 0.f;
+    if constexpr (kMode == 1) {
+      if (!kChecked || n < p.N) {
+        s = p.scale[n];
+        if (p.trunc19) s = __uint_as_float(__float_as_uint(s) & 0xFFFFE000u);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
+        if (kChecked && (m >= p.M || n >= p.N)) continue;
+        const int64_t off = static_cast<int64_t>(m) * p.N + n;
+        if constexpr (kMode == 0) {
+          static_cast<int32_t*>(p.c)[off] = acc[i][j][r];
+        } else {
+          const float v = static_cast<float>(acc[i][j][r]) * s;
+          static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
+        }
+      }
+    }
+  }
+}
+
+template <bool kChecked, int kMode>
+int32_t launch(const I8Args& p, hipStream_t stream, const char* who) {
+  auto kern = gemm_i8_kernel<kChecked, kMode>;
+  static bool configured = false;
+  if (!configured) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
+    if (err != hipSuccess)
+      return asc::set_error(static_cast<int32_t>(err), "%s: hipFuncSetAttribute: %s", who, hipGetErrorString(err));
+    configured = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), 2 * kStageBytes, stream, p);
+  return asc::check_launch(who);
+}
+
+int32_t run(const int8_t* a, const int8_t* b, const float* scale, void* c, int64_t M, int64_t N, int64_t K,
+            int32_t trunc19, int mode, hipStream_t stream, const char* who) {
+  ASC_REQUIRE(M >= 0 && N >= 0 && K >= 0, ASC_ERR_INVALID_ARG, "%s: negative shape", who);
+  ASC_REQUIRE(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), ASC_ERR_UNSUPPORTED, "%s: shape too large", who);
+  // |acc| <= K * 128 * 128 must fit int32
+  ASC_REQUIRE(K <= (int64_t{1} << 17), ASC_ERR_UNSUPPORTED, "%s: K=%lld could overflow the int32 accumulator", who,
+              (long long)K);
+  if (M == 0 || N == 0) return ASC_OK;
+  ASC_REQUIRE(a && b && c && (mode == 0 || scale), ASC_ERR_INVALID_ARG, "%s: null buffer", who);
+  I8Args p;
+  p.a = a;
+  p.b = b;
+  p.scale = scale;
+  p.c = c;
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.trunc19 = trunc19;
+  p.tiles_m = static_cast<int>((M + BM - 1) / BM);
+  p.tiles_n = static_cast<int>((N + BN - 1) / BN);
+  const bool fast = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
+                    (M % BM) == 0 && (N % BN) == 0 && (K % BK) == 0 && K > 0;
+  if (mode == 0) return fast ? launch<false, 0>(p, stream, who) : launch<true, 0>(p, stream, who);
+  return fast ? launch<false, 1>(p, stream, who) : launch<true, 1>(p, stream, who);
+}
+
+}  // namespace
+
+extern "C" int32_t asc_matmul_i8_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N, int64_t K,
+                                     asc_stream_t stream) {
+  return run(a, b, nullptr, c, M, N, K, 0, 0, static_cast<hipStream_t>(stream), "asc_matmul_i8_i32");
+}
+
+extern "C" int32_t asc_matmul_i8_dequant_f16(const int8_t* a, const int8_t* b, const float* scale, void* c,
+                                             int64_t M, int64_t N, int64_t K, int32_t trunc19, asc_stream_t stream) {
+  return run(a, b, scale, c, M, N, K, trunc19, 1, static_cast<hipStream_t>(stream), "asc_matmul_i8_dequant_f16");
 }

@@ -1,0 +1,103 @@
+"""fp16/bf16 (and fp32-input) matmul parity on the GPU through the C ABI.
+
+Tolerances: the north-star bound for fp16/bf16 matmul is atol/rtol 1e-2 against
+an fp32 torch CPU reference; the reference tests' own tolerances are used where
+they are tighter (fixpipe / chained: 1e-3; mnblock / K-tiled fp32 output: the
+default fp32 assert_close, relaxed to 2e-5 relative for fp32 accumulation order).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import asc2_oracle as O
+from pyasc_amd import kernels
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+TOL = 1e-2  # north star: fp16/bf16 matmul within atol/rtol 1e-2 of fp32 CPU
+
+
+def _gen(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def test_mnblock_fixture(device):
+    f = np.load(os.path.join(GOLDEN, "matmul_mnblock_f16.npz"))
+    for idx in range(len(f["cases"])):
+        a = torch.from_numpy(f[f"a{idx}"]).to(device)
+        b = torch.from_numpy(f[f"b{idx}"]).to(device)
+        c = torch.zeros(a.shape[0], b.shape[1], device=device)
+        kernels.matmul(a, b, c)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(c.cpu(), torch.from_numpy(f[f"c{idx}"]), rtol=2e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (16, 16, 16), (17, 33, 65), (300, 257, 129), (256, 256, 64),
+                                   (512, 768, 320), (64, 128, 256), (1000, 1000, 1000)])
+def test_shapes_vs_oracle(device, dtype, out_dtype, M, N, K):
+    a = _gen((M, K), dtype, M * 7 + K, 1 / np.sqrt(K))
+    b = _gen((K, N), dtype, N * 11 + K)
+    c = torch.full((M, N), 123.0, dtype=out_dtype, device=device)
+    kernels.matmul(a.to(device), b.to(device), c)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(O.matmul(a.float().numpy(), b.float().numpy()))
+    torch.testing.assert_close(c.cpu().float(), ref.to(out_dtype).float(), atol=TOL, rtol=TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_relu_cast_fixpipe(device, dtype):
+    # python/test/asc2/kernels/test_matmul_fixpipe.py:36-48
+    g = torch.Generator().manual_seed(5)
+    a = (torch.rand((64, 128), generator=g, dtype=dtype) - .5) * 10
+    b = (torch.rand((128, 256), generator=g, dtype=dtype) - .5) * 10
+    c = torch.zeros((64, 256), dtype=torch.float16, device=device)
+    kernels.matmul(a.to(device), b.to(device), c, relu=True)
+    torch.cuda.synchronize()
+    ref = (a.to(torch.float32) @ b.to(torch.float32)).relu().to(torch.float16)
+    torch.testing.assert_close(c.cpu(), ref, atol=1e-3, rtol=1e-3)
+
+
+def test_fp32_inputs(device):
+    g = torch.Generator().manual_seed(6)
+    a = (torch.rand((64, 128), generator=g) - .5) * 10
+    b = (torch.rand((128, 128), generator=g) - .5) * 10
+    c = torch.zeros((64, 128), dtype=torch.float16, device=device)
+    kernels.matmul(a.to(device), b.to(device), c, relu=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(c.cpu(), (a @ b).relu().to(torch.float16), atol=1e-3, rtol=1e-3)
+
+
+def test_strided_views(device):
+    a = _gen((300, 200), torch.float16, 1, 0.1).to(device)
+    b = _gen((200, 400), torch.float16, 2).to(device)
+    c = torch.full((300, 400), -5.0, device=device)
+    kernels.matmul(a[10:110, 8:136], b[8:136, 16:272], c[50:150, 100:356])
+    torch.cuda.synchronize()
+    ref = O.matmul(a[10:110, 8:136].float().cpu().numpy(), b[8:136, 16:272].float().cpu().numpy())
+    got = c.cpu().numpy()
+    np.testing.assert_allclose(got[50:150, 100:356], ref, atol=TOL, rtol=TOL)
+    mask = np.ones_like(got, dtype=bool)
+    mask[50:150, 100:356] = False
+    assert (got[mask] == -5.0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config_8192_sampled_rows(device, dtype):
+    """BASELINE config: M=N=K=8192, randn/sqrt(K) inputs from seed 2; every column of
+    128 sampled rows is checked against the fp32 CPU product."""
+    n = 8192
+    g = torch.Generator().manual_seed(2)
+    a = (torch.randn(n, n, generator=g) / np.sqrt(n)).to(dtype)
+    b = (torch.randn(n, n, generator=g) / np.sqrt(n)).to(dtype)
+    c = torch.empty(n, n, dtype=dtype, device=device)
+    kernels.matmul(a.to(device), b.to(device), c)
+    torch.cuda.synchronize()
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(9))[:128]
+    ref = a[rows].float() @ b.float()
+    torch.testing.assert_close(c[rows.to(device)].cpu().float(), ref.to(dtype).float(), atol=TOL, rtol=TOL)
+    assert torch.isfinite(c).all()

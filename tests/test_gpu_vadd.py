@@ -13,8 +13,15 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
-def _bits(t):
-    return t.cpu().view(torch.int16).numpy().view(np.uint16) if t.element_size() == 2 else t.cpu().numpy()
+def _np(t):
+    """numpy view of a tensor: bfloat16 as uint16 bit patterns, other dtypes as themselves."""
+    t = t.cpu()
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+
+def _bits(a):
+    """Bit patterns for a bit-exact comparison (NaN-safe)."""
+    return a.view(np.uint16) if a.dtype in (np.float16, np.uint16) else a.view(np.uint32)
 
 
 def test_reference_recipe_fixture(device):
@@ -53,9 +60,8 @@ def test_vadd_vs_oracle(device, size, tile, tpb, grid, dtype):
     out = sentinel.to(device)
     kernels.vadd(x.to(device), y.to(device), out, size, tile, tpb, grid)
     torch.cuda.synchronize()
-    xn, yn, sn = _bits(x), _bits(y), _bits(sentinel)
-    expected = O.vadd(xn, yn, sn, size, tile, tpb, grid, dtype)
-    np.testing.assert_array_equal(_bits(out), expected)
+    expected = O.vadd(_np(x), _np(y), _np(sentinel), size, tile, tpb, grid, dtype)
+    np.testing.assert_array_equal(_bits(_np(out)), _bits(expected))
 
 
 def test_unaligned_views(device):
