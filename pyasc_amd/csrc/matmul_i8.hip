@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
         if constexpr (kMode == 0) {
           static_cast<int32_t*>(p.c)[off] = acc[i][j][r];
         } else {
-          const float v = static_cast<float>(acc[i][j][r]) * s;
+          const float v = asc::materialize(static_cast<float>(acc[i][j][r]) * s);
           static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
         }
       }

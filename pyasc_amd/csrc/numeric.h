@@ -24,4 +24,13 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   return __builtin_bit_cast(uint16_t, v);
 }
 
+// Forces `v` to be rounded to fp32 and held in a register.  Without it the
+// compiler may fuse a following fp32 -> fp16 conversion into the producing
+// multiply (v_fma_mixlo_f16), rounding the exact product once instead of
+// rounding to fp32 first -- a different result in rare ties.
+__device__ __forceinline__ float materialize(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 }  // namespace asc

@@ -5,8 +5,8 @@
 // over the row's first L columns (row stride S).
 //
 // HBM-bound (one read + one write of every element).  Rows up to 8192 columns
-// stay in registers: a wave per row up to 4096 columns (no barrier, 16 float4
-// loads in flight per lane), a 256-thread block per row above that.  Max and sum reduce in-thread, then by wave butterfly
+// stay in registers: a wave per row up to 1024 columns, a 256-thread block per
+// row above that (measured faster at 4096 columns than a wave per row).  Max and sum reduce in-thread, then by wave butterfly
 // (__shfl_xor), then across waves through LDS.  exp is the accurate libm expf
 // and the normalisation is a true division, as the reference's DivL2
 // (lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116).
@@ -172,9 +172,9 @@ int32_t launch_rows(const RowView& p, hipStream_t stream, const char* who) {
   } else if (L <= 1024) {
     hipLaunchKernelGGL(softmax_wave_kernel<4>, wave_grid, block, 0, stream, p);
   } else if (L <= 2048) {
-    hipLaunchKernelGGL(softmax_wave_kernel<8>, wave_grid, block, 0, stream, p);
+    hipLaunchKernelGGL(softmax_block_kernel<2>, row_grid, block, 0, stream, p);
   } else if (L <= 4096) {
-    hipLaunchKernelGGL(softmax_wave_kernel<16>, wave_grid, block, 0, stream, p);
+    hipLaunchKernelGGL(softmax_block_kernel<4>, row_grid, block, 0, stream, p);
   } else if (L <= 8192) {
     hipLaunchKernelGGL(softmax_block_kernel<8>, row_grid, block, 0, stream, p);
   } else {
