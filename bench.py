@@ -208,6 +208,35 @@ class MatmulI8(Workload):
                 "epilogue": "fp16(fp32(acc) * scale[n])", "input": "int8 uniform[-127,127], seed 3"}
 
 
+class FlashAttention(Workload):
+    bound, unit, dtype, kernel_hint = "mfma", "TFLOP/s", "bf16", "fa_fwd"
+    peak = BF16_PEAK_TFLOPS
+
+    def __init__(self, B: int, H: int, S: int, D: int, causal: bool):
+        self.B, self.H, self.S, self.D, self.causal = B, H, S, D, causal
+        self.name = f"flash_attn_fwd_b{B}h{H}s{S}d{D}_{'causal' if causal else 'noncausal'}"
+
+    def setup(self, dev):
+        import torch
+        g = torch.Generator(device=dev).manual_seed(4)
+        shape = (self.B, self.H, self.S, self.D)
+        self.q, self.k, self.v = [torch.randn(*shape, device=dev, generator=g).to(torch.bfloat16) for _ in range(3)]
+        self.o = torch.empty_like(self.q)
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        kernels.flash_attention_fwd(self.q, self.k, self.v, self.o, 1 / math.sqrt(self.D), self.causal)
+
+    def work(self) -> float:
+        full = 4.0 * self.B * self.H * self.S * self.S * self.D
+        return full / 2 if self.causal else full  # causal counted as half of the dense work
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": self.B, "heads": self.H, "seq_len": self.S, "head_dim": self.D,
+                "causal": self.causal, "sm_scale": 1 / math.sqrt(self.D), "input": "bf16 randn, seed 4",
+                "flop_convention": "4*B*H*S^2*D, halved for causal"}
+
+
 WORKLOADS = {
     "softmax_4096x4096": lambda: Softmax(4096, 4096),
     "softmax_16384x1024": lambda: Softmax(16384, 1024),
@@ -216,9 +245,12 @@ WORKLOADS = {
     "matmul_bf16_8192": lambda: Matmul(8192, "bfloat16"),
     "matmul_f16_8192": lambda: Matmul(8192, "float16"),
     "matmul_i8_4096x11008x4096": lambda: MatmulI8(4096, 11008, 4096),
+    "fa_fwd_noncausal": lambda: FlashAttention(4, 32, 4096, 128, False),
+    "fa_fwd_causal": lambda: FlashAttention(4, 32, 4096, 128, True),
 }
 HEADLINE = "softmax_4096x4096"
-SUITE = ["softmax_16384x1024", "vadd_268435456", "matmul_bf16_8192", "matmul_f16_8192", "matmul_i8_4096x11008x4096"]
+SUITE = ["softmax_16384x1024", "vadd_268435456", "matmul_bf16_8192", "matmul_f16_8192", "matmul_i8_4096x11008x4096",
+         "fa_fwd_noncausal", "fa_fwd_causal"]
 
 
 def _time_cpu(fn, budget_s: float) -> float:
