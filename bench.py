@@ -38,6 +38,7 @@ FP16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0
 METRIC = "HBM GB/s (vadd, softmax); TFLOP/s or TOPS (matmul, FA-fwd); % of MI355X peak"
 ROTATE_BYTES = 640 << 20  # > 2x the 256 MiB Infinity Cache
+COPY_BYTES = 256 << 20    # calibration copy: reads and writes exactly this many bytes
 
 
 class Workload:
@@ -308,6 +309,9 @@ def main() -> int:
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); every kernel here runs on a single "
@@ -336,6 +340,13 @@ def main() -> int:
             suite[name] = r
             del w
             torch.cuda.empty_cache()
+    if args.copy_calibration:
+        src = torch.empty(COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cpu = None if args.no_cpu else head.cpu_baseline()
     line = {
         "metric": METRIC,
