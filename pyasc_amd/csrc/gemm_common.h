@@ -11,11 +11,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // LDS tiles are stored as rows of 8 chunks of 16 bytes (128 bytes per row, K
 // contiguous).  The chunk index is XOR-swizzled with
-//   g(row) = ((row >> 1) ^ (row >> 3)) & 7
-// which makes both access patterns conflict-free within a 16-lane LDS phase:
-//  - MFMA operand reads: 16 consecutive rows, one chunk each,
-//  - transposed B writes: rows 8 apart (one 8x8 block per lane).
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (((row >> 1) ^ (row >> 3)) & 7); }
+//   g(row) = (row ^ (row >> 3)) & 7.
+// A 128-bit LDS access is serviced 8 lanes (128 bytes) at a time, so each
+// group of 8 lanes must touch 8 distinct chunk positions:
+//  - MFMA operand reads: 8 consecutive rows, one chunk each -> row & 7 differs;
+//  - transposed B writes: rows 8*nc + e for 8 values of nc -> (row >> 3) differs;
+//  - A writes: one row, chunks 0..7.
+// (Enumerated: conflict-free for all three; the previous ((row>>1)^(row>>3))
+// form measured as many LDS bank-conflict cycles as active LDS cycles.)
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
 
 __device__ __forceinline__ uint32_t lds_offset(int row, int chunk) {
   return static_cast<uint32_t>(row * 128 + swz(row, chunk) * 16);

@@ -1,0 +1,223 @@
+// Direct-to-LDS MFMA GEMM main loop for tile-aligned shapes (the fast path of
+// matmul.hip and matmul_i8.hip; ragged shapes use gemm_core.h).
+//
+//   - 256x256 output tile per 256-thread workgroup; 4 waves in 2x2, each wave
+//     128x128 = 4x4 blocks of 32x32 MFMA accumulators (256 AGPRs).
+//   - A k-tile is 64 bytes of K (32 fp16/bf16 or 64 int8 elements): 2 MFMA
+//     k-steps.  Operands go from HBM straight into LDS (buffer_load ... lds,
+//     16 bytes per lane, 1 KiB per wave instruction): no staging registers, no
+//     ds_write.  Four LDS stages of 32 KiB (A 16 KiB + B 16 KiB); the loads of
+//     k-tile kt+3 are issued while k-tile kt is computed, so each tile has two
+//     to three tiles of MFMA work to arrive.
+//   - One s_barrier per k-tile with no drain: before it a wave only waits for
+//     its own loads of tile kt+2 (vmcnt counts the one newer tile), and the
+//     first operand fragments of tile kt+1 are already read.
+//   - A tile: 256 rows x 64 bytes (K contiguous); 16-byte chunks swizzled by
+//     gA(row) = ((row >> 1) ^ (row >> 3)) & 3; MFMA operands are ds_read_b128.
+//   - B tile: kBK rows (K) x 256 columns, row-major as in HBM (N contiguous);
+//     the K-contiguous MFMA operand is read with the gfx950 LDS transpose
+//     reads (ds_read_b64_tr_b16 / ds_read_b64_tr_b8).  16-byte chunks are
+//     swizzled per row so those reads are conflict-free (tables found by
+//     enumerating both 128- and 256-byte-per-cycle bank models).
+//   - Lane layouts of the transpose reads (measured on the device): in each
+//     16-lane group, b16: lane i receives element i%4 of lane 4j + i/4's 8-byte
+//     read (j = 0..3); b8: lane i receives byte i%8 of lane 2j + i/8's read
+//     (j = 0..7).
+//   - The four stages are distinct __shared__ objects and every access names
+//     its stage at compile time (the loop is unrolled by four), so the compiler
+//     can tell that loads into one stage do not alias reads of another.
+#pragma once
+
+#include "gemm_common.h"
+
+namespace asc {
+namespace gemm {
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((vector_size(8)));
+
+constexpr int kDirectStages = 4;
+constexpr int kDirectStageBytes = 32768;
+
+template <class Tr>
+struct GemmDirectLoop {
+  using Elem = typename Tr::Elem;
+  using Acc = typename Tr::Acc;
+  static constexpr int kES = sizeof(Elem);
+  static constexpr int kBK = 64 / kES;          // K elements per k-tile (64 bytes)
+  static constexpr int kBRowBytes = 256 * kES;  // one B tile row (256 columns)
+  static constexpr int kBRowsPerLoad = 1024 / kBRowBytes;
+  static constexpr int kBOff = 16384;
+
+  // A chunk swizzle (4 chunks per 64-byte row)
+  __device__ __forceinline__ static int ga(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+  // B chunk swizzle: position p of row r holds logical chunk p ^ fb(r)
+  __device__ __forceinline__ static int fb(int row) {
+    if constexpr (kES == 2) return (0xCA60u >> (4 * (row & 3))) & 15;   // {0, 6, 10, 12}
+    else return (0xE5CB2097u >> (4 * (row & 7))) & 15;                  // {7, 9, 0, 2, 11, 12, 5, 14}
+  }
+
+  const Elem* a;
+  const Elem* b;
+  int m0, n0;
+  int lane, wave, wm, wn;
+  int lda_bytes, ldb_bytes;
+  uint8_t* lds[kDirectStages];
+  __amdgpu_buffer_rsrc_t rsrc_a, rsrc_b;
+  int voff_a[4];  // per A load instruction (the swizzle depends on the 16-row block)
+  int voff_b[2];  // per parity of the B load instruction
+
+  __device__ __forceinline__ void init(int64_t lda, int64_t ldb) {
+    lda_bytes = static_cast<int>(lda) * kES;
+    ldb_bytes = static_cast<int>(ldb) * kES;
+    const Elem* a_panel = a + static_cast<int64_t>(m0) * lda;
+    const Elem* b_cols = b + n0;
+    rsrc_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<Elem*>(a_panel), static_cast<short>(0), 0x7fffffff,
+                                               0x00020000);
+    rsrc_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<Elem*>(b_cols), static_cast<short>(0), 0x7fffffff,
+                                               0x00020000);
+    // A: instruction i of wave w loads rows 16R .. 16R+15, R = 4w + i; lane l ->
+    // row 16R + l/4, LDS position l%4 holding logical chunk (l%4) ^ ga(row).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int R = wave * 4 + i;
+      const int row = 16 * R + (lane >> 2);
+      const int c = (lane & 3) ^ ga(row);
+      voff_a[i] = (lane >> 2) * lda_bytes + c * 16;
+    }
+    // B: instruction R loads rows kBRowsPerLoad*R + lane / (64 / kBRowsPerLoad);
+    // the row's swizzle only depends on R's parity.
+    constexpr int kLanesPerRow = 64 / kBRowsPerLoad;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int rr = lane / kLanesPerRow;
+      const int row = kBRowsPerLoad * par + rr;
+      const int c = (lane % kLanesPerRow) ^ fb(row);
+      voff_b[par] = rr * ldb_bytes + c * 16;
+    }
+  }
+
+  template <int kS>
+  __device__ __forceinline__ void issue_loads(int k0) {
+    uint8_t* base = lds[kS];
+    const int kb = k0 * kES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int R = wave * 4 + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) void*)(base + R * 1024),
+                                               16, voff_a[i], 16 * R * lda_bytes + kb, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int R = wave * 4 + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b,
+                                               (__attribute__((address_space(3))) void*)(base + kBOff + R * 1024), 16,
+                                               voff_b[i & 1], (k0 + kBRowsPerLoad * R) * ldb_bytes, 0, 0);
+    }
+  }
+
+  // byte offset of element (row, col) in the swizzled B tile
+  __device__ __forceinline__ static int b_off(int row, int col) {
+    const int byte = col * kES;
+    return row * kBRowBytes + (((byte >> 4) ^ fb(row)) << 4) + (byte & 15);
+  }
+
+  template <int kS>
+  __device__ __forceinline__ void read_frags(int step, u32x4 (&fa)[4], u32x4 (&fbv)[4]) const {
+    const uint8_t* as = lds[kS];
+    const uint8_t* bs = as + kBOff;
+    const int h = lane >> 5;
+    const int chunk = step * 2 + h;
+    const int arow = wm * 128 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = arow + i * 32;
+      fa[i] = *reinterpret_cast<const u32x4*>(as + row * 64 + ((chunk ^ ga(row)) << 4));
+    }
+    const int g = (lane >> 4) & 1, t = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int nb = wn * 128 + j * 32 + 16 * g;
+      if constexpr (kES == 2) {
+        // k = 16*step + 8h + e; read e = 0..3 then 4..7; lane 4jj+q -> row +jj, col +4q
+        const int row = step * 16 + 8 * h + (t >> 2);
+        const int col = nb + 4 * (t & 3);
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(bs + b_off(row, col)));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(bs + b_off(row + 4, col)));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        fbv[j] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+      } else {
+        // k = 32*step + 16h + e; read e = 0..7 then 8..15; lane 2jj+sub -> row +jj, col +8sub
+        const int row = step * 32 + 16 * h + (t >> 1);
+        const int col = nb + 8 * (t & 1);
+        const i32x2_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) i32x2_t*)(bs + b_off(row, col)));
+        const i32x2_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) i32x2_t*)(bs + b_off(row + 8, col)));
+        fbv[j] = u32x4{static_cast<uint32_t>(lo[0]), static_cast<uint32_t>(lo[1]), static_cast<uint32_t>(hi[0]),
+                       static_cast<uint32_t>(hi[1])};
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void mma(Acc (&acc)[4][4], const u32x4 (&fa)[4], const u32x4 (&fbv)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = Tr::mfma(fa[i], fbv[j], acc[i][j]);
+  }
+
+  // Workgroup barrier that does not wait for outstanding loads (unlike
+  // __syncthreads, whose fence drains vmcnt).
+  __device__ __forceinline__ static void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+  // k-tile kt, held in stage kS.  On entry the k-step-0 fragments of tile kt
+  // are in fa0/fb0, and tiles kt and kt+1 are visible in LDS.
+  template <int kS>
+  __device__ __forceinline__ void iteration(int kt, int k_tiles, Acc (&acc)[4][4], u32x4 (&fa0)[4],
+                                            u32x4 (&fb0)[4], u32x4 (&fa1)[4], u32x4 (&fb1)[4]) {
+    constexpr int kNext = (kS + 1) % kDirectStages;
+    constexpr int kAhead = (kS + 3) % kDirectStages;
+    // tile kt+3 (clamped: the tail re-loads the last tile into a free stage)
+    issue_loads<kAhead>((kt + 3 < k_tiles ? kt + 3 : k_tiles - 1) * kBK);
+    read_frags<kS>(1, fa1, fb1);
+    mma(acc, fa0, fb0);
+    read_frags<kNext>(0, fa0, fb0);
+    mma(acc, fa1, fb1);
+    // own loads of tile kt+2 done (only tile kt+3's eight may still run), and
+    // this wave's reads of stage kS complete before anyone reloads it
+    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    barrier();
+  }
+
+  __device__ __forceinline__ void run(int K, Acc (&acc)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
+    const int k_tiles = K / kBK;
+    issue_loads<0>(0);
+    issue_loads<1>((k_tiles > 1 ? 1 : 0) * kBK);
+    issue_loads<2>((k_tiles > 2 ? 2 : k_tiles - 1) * kBK);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // tiles 0 and 1 landed
+    barrier();
+    u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
+    read_frags<0>(0, fa0, fb0);
+    int kt = 0;
+    for (; kt + 3 < k_tiles; kt += 4) {
+      iteration<0>(kt, k_tiles, acc, fa0, fb0, fa1, fb1);
+      iteration<1>(kt + 1, k_tiles, acc, fa0, fb0, fa1, fb1);
+      iteration<2>(kt + 2, k_tiles, acc, fa0, fb0, fa1, fb1);
+      iteration<3>(kt + 3, k_tiles, acc, fa0, fb0, fa1, fb1);
+    }
+    if (kt < k_tiles) iteration<0>(kt, k_tiles, acc, fa0, fb0, fa1, fb1);
+    if (kt + 1 < k_tiles) iteration<1>(kt + 1, k_tiles, acc, fa0, fb0, fa1, fb1);
+    if (kt + 2 < k_tiles) iteration<2>(kt + 2, k_tiles, acc, fa0, fb0, fa1, fb1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load may outlive the kernel
+  }
+};
+
+}  // namespace gemm
+}  // namespace asc

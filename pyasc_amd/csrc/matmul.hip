@@ -6,9 +6,8 @@
 // accumulation:
 //   - 256x256 output tile per 256-thread workgroup, 4 waves in 2x2, each wave
 //     owns 128x128 = 4x4 MFMA blocks (256 fp32 accumulators per lane);
-//   - K advances 64 at a time through two LDS stages (2 x 64 KiB): while one
-//     stage feeds the MFMAs, the next k-tile is fetched from HBM into registers
-//     and written to the other stage;
+//   - K advances 64 at a time through two LDS stages (2 x 64 KiB) in the
+//     software-pipelined main loop of gemm_core.h;
 //   - A (row-major, K contiguous) is copied as is; B (row-major, N contiguous)
 //     is transposed in registers (8x8 blocks of 16-bit, v_perm_b32) so both LDS
 //     tiles are K-contiguous and every MFMA operand is one ds_read_b128;
@@ -21,6 +20,8 @@
 // FMA kernel.
 #include "common.h"
 #include "gemm_common.h"
+#include "gemm_core.h"
+#include "gemm_direct.h"
 #include "numeric.h"
 
 namespace {
@@ -30,12 +31,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256;
-constexpr int BN = 256;
-constexpr int BK = 64;             // 16-bit elements per LDS row = 128 bytes
-constexpr int kThreads = 256;
-constexpr int kStageBytes = (BM + BN) * 128;
-constexpr int kGroupM = 8;
+constexpr int BM = asc::gemm::kTileM;
+constexpr int BN = asc::gemm::kTileN;
+constexpr int BK = 64;  // 16-bit elements per LDS row = 128 bytes
+constexpr int kThreads = asc::gemm::kGemmThreads;
+constexpr int kStageBytes = asc::gemm::kStageBytes;
 
 enum OutKind { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
 
@@ -49,19 +49,8 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
-template <bool kBf16>
-__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (kBf16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                  0, 0);
-  }
-}
-
-// 8 consecutive 16-bit elements p[0..7] of row `row`, columns col..col+7 of a
-// row-major [rows x cols] matrix; out-of-range elements read as 0.
+// 8 consecutive 16-bit elements of row `row`, columns col..col+7 of a row-major
+// [rows x cols] matrix; out-of-range elements read as 0.
 template <bool kChecked>
 __device__ __forceinline__ u32x4 load_chunk(const uint16_t* base, int64_t ld, int row, int col, int rows, int cols,
                                             bool vec_ok) {
@@ -76,91 +65,85 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t* base, int64_t ld, in
   return v;
 }
 
+template <bool kBf16>
+struct Tr16 {
+  using Elem = uint16_t;
+  using Acc = f32x16;
+  using BReg = u32x4;
+  static constexpr int kBK = BK;
+  static constexpr int kBRows = 8;
+  template <bool kChecked>
+  __device__ __forceinline__ static u32x4 load_a(const uint16_t* base, int64_t ld, int row, int col, int rows,
+                                                 int cols, bool vec_ok) {
+    return load_chunk<kChecked>(base, ld, row, col, rows, cols, vec_ok);
+  }
+  template <bool kChecked>
+  __device__ __forceinline__ static u32x4 load_b(const uint16_t* base, int64_t ld, int row, int col, int rows,
+                                                 int cols, bool vec_ok) {
+    return load_chunk<kChecked>(base, ld, row, col, rows, cols, vec_ok);
+  }
+  __device__ __forceinline__ static void transpose_b(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+    asc::gemm::transpose8x8_b16(in, out);
+  }
+  __device__ __forceinline__ static f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    if constexpr (kBf16) {
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                     c, 0, 0, 0);
+    } else {
+      return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                    0, 0, 0);
+    }
+  }
+};
+
 template <bool kBf16, bool kChecked, int kOut>
 __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
   int tm, tn;
-  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, asc::gemm::kGroupM, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-
-  // vector loads need 16-byte aligned chunks
-  const bool a_vec = ((reinterpret_cast<uintptr_t>(p.a) | (p.lda * 2)) & 15) == 0;
-  const bool b_vec = ((reinterpret_cast<uintptr_t>(p.b) | (p.ldb * 2)) & 15) == 0;
-
-  // A loader: chunk c = tid + 256*i -> row c/8, k-chunk c%8
-  // B loader: one 8(k) x 8(n) block per thread: n-chunk tid%32, k-group tid/32
-  const int b_nc = tid & 31, b_kg = tid >> 5;
-
-  u32x4 ra[8], rb[8];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + kThreads * i;
-      ra[i] = load_chunk<kChecked>(p.a, p.lda, m0 + (c >> 3), k0 + (c & 7) * 8, p.M, p.K, a_vec);
-    }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      rb[r] = load_chunk<kChecked>(p.b, p.ldb, k0 + b_kg * 8 + r, n0 + b_nc * 8, p.K, p.N, b_vec);
-    }
-  };
-  auto stash = [&](int stage) {
-    uint8_t* as = smem + stage * kStageBytes;
-    uint8_t* bs = as + BM * 128;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + kThreads * i;
-      *reinterpret_cast<u32x4*>(as + asc::gemm::lds_offset(c >> 3, c & 7)) = ra[i];
-    }
-    u32x4 tb[8];
-    asc::gemm::transpose8x8_b16(rb, tb);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      *reinterpret_cast<u32x4*>(bs + asc::gemm::lds_offset(b_nc * 8 + e, b_kg)) = tb[e];
-    }
-  };
-
+  const int lane = threadIdx.x & 63;
+  const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
   f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  const int k_tiles = (p.K + BK - 1) / BK;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-
-  const int arow = wm * 128 + (lane & 31);
-  const int brow = wn * 128 + (lane & 31);
-  const int khalf = lane >> 5;
-
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    const int stage = kt & 1;
-    if (kt + 1 < k_tiles) fetch((kt + 1) * BK);
-    const uint8_t* as = smem + stage * kStageBytes;
-    const uint8_t* bs = as + BM * 128;
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      const int chunk = s * 2 + khalf;
-      u32x4 fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const u32x4*>(as + asc::gemm::lds_offset(arow + i * 32, chunk));
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const u32x4*>(bs + asc::gemm::lds_offset(brow + j * 32, chunk));
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<kBf16>(fa[i], fb[j], acc[i][j]);
-    }
-    if (kt + 1 < k_tiles) stash(stage ^ 1);
-    __syncthreads();
+  if constexpr (kChecked) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kStageBytes];
+    asc::gemm::GemmMainLoop<Tr16<kBf16>, true> L;
+    L.a = p.a;
+    L.b = p.b;
+    L.s = asc::gemm::GemmShape{p.M, p.N, p.K, p.lda, p.ldb, p.tiles_m, p.tiles_n};
+    L.m0 = m0;
+    L.n0 = n0;
+    L.tid = threadIdx.x;
+    L.lane = lane;
+    L.wm = wm;
+    L.wn = wn;
+    // vector loads need 16-byte aligned chunks
+    L.a_vec = ((reinterpret_cast<uintptr_t>(p.a) | (p.lda * 2)) & 15) == 0;
+    L.b_vec = ((reinterpret_cast<uintptr_t>(p.b) | (p.ldb * 2)) & 15) == 0;
+    L.lds[0] = lds0;
+    L.lds[1] = lds1;
+    L.run(acc);
+  } else {
+    // four LDS stages as distinct objects (see gemm_direct.h)
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
+    asc::gemm::GemmDirectLoop<Tr16<kBf16>> L;
+    L.a = p.a;
+    L.b = p.b;
+    L.m0 = m0;
+    L.n0 = n0;
+    L.lane = lane;
+    L.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
+    L.wm = wm;
+    L.wn = wn;
+    L.lds[0] = lds0;
+    L.lds[1] = lds1;
+    L.lds[2] = lds2;
+    L.lds[3] = lds3;
+    L.init(p.lda, p.ldb);
+    L.run(p.K, acc);
   }
 
   // Epilogue.  MFMA 32x32 result layout: lane holds column lane%32 of the block,
@@ -235,17 +218,8 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__
 
 template <bool kBf16, bool kChecked, int kOut>
 int32_t launch_mfma(const GemmArgs& p, hipStream_t stream) {
-  auto kern = gemm_mfma_kernel<kBf16, kChecked, kOut>;
-  static bool configured = false;  // per instantiation; the attribute is idempotent
-  if (!configured) {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
-    if (err != hipSuccess)
-      return asc::set_error(static_cast<int32_t>(err), "asc_matmul: hipFuncSetAttribute: %s", hipGetErrorString(err));
-    configured = true;
-  }
   const int blocks = p.tiles_m * p.tiles_n;
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), 2 * kStageBytes, stream, p);
+  hipLaunchKernelGGL((gemm_mfma_kernel<kBf16, kChecked, kOut>), dim3(blocks), dim3(kThreads), 0, stream, p);
   return asc::check_launch("asc_matmul");
 }
 
@@ -315,7 +289,9 @@ extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a
   p.tiles_n = static_cast<int>((N + BN - 1) / BN);
   const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
                        (lda % 8) == 0 && (ldb % 8) == 0;
-  const bool fast = aligned && (M % BM) == 0 && (N % BN) == 0 && (K % BK) == 0 && K > 0;
+  // the direct-to-LDS path addresses each operand with 31-bit buffer offsets
+  const bool offsets_fit = (BM * lda + K) * 2 < (int64_t{1} << 31) && (K + 64) * ldb * 2 < (int64_t{1} << 31);
+  const bool fast = aligned && offsets_fit && (M % BM) == 0 && (N % BN) == 0 && (K % 32) == 0 && K > 0;
   // K == 0 takes the checked kernel: no k-tile runs and C receives cast(0).
   return in_dtype == ASC_DT_BFLOAT16 ? dispatch_out<true>(p, out_dtype, fast, s)
                                      : dispatch_out<false>(p, out_dtype, fast, s);

@@ -3,15 +3,17 @@
 // (python/test/generalization/adv/test_matmul_quant.py:23-51,94-106;
 //  lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:116-117).
 //
-// Same structure as the fp16/bf16 kernel (matmul.hip) on v_mfma_i32_32x32x32_i8:
-// 256x256 output tile, 4 waves of 128x128, K advancing 128 bytes per LDS stage
-// (128-byte LDS rows, swizzled chunks), B transposed in registers as 16(k) x
-// 8(n) byte blocks (64 v_perm_b32 per block).  The epilogue either stores the
+// Same pipelined main loop as the fp16/bf16 kernel (gemm_core.h) on
+// v_mfma_i32_32x32x32_i8: 256x256 output tile, 4 waves of 128x128, K advancing
+// 128 bytes per LDS stage, B transposed in registers as 16(k) x 8(n) byte blocks
+// (64 v_perm_b32 per block).  The epilogue either stores the
 // int32 accumulators or out = fp16_rne(fp32_rne(acc) * s[n]) with s[n] the
 // fp32 scale (optionally with its low 13 mantissa bits cleared, the reference
 // golden's trunc-19 form).
 #include "common.h"
 #include "gemm_common.h"
+#include "gemm_core.h"
+#include "gemm_direct.h"
 #include "numeric.h"
 
 namespace {
@@ -21,12 +23,11 @@ using asc::gemm::u32x4;
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256;
-constexpr int BN = 256;
+constexpr int BM = asc::gemm::kTileM;
+constexpr int BN = asc::gemm::kTileN;
 constexpr int BK = 128;  // int8 elements per LDS row = 128 bytes
-constexpr int kThreads = 256;
-constexpr int kStageBytes = (BM + BN) * 128;
-constexpr int kGroupM = 8;
+constexpr int kThreads = asc::gemm::kGemmThreads;
+constexpr int kStageBytes = asc::gemm::kStageBytes;
 
 struct I8Args {
   const int8_t* a;
@@ -66,93 +67,79 @@ __device__ __forceinline__ u32x2 load8(const int8_t* base, int64_t ld, int row, 
   return v;
 }
 
+struct TrI8 {
+  using Elem = int8_t;
+  using Acc = i32x16;
+  using BReg = u32x2;
+  static constexpr int kBK = BK;
+  static constexpr int kBRows = 16;
+  template <bool kChecked>
+  __device__ __forceinline__ static u32x4 load_a(const int8_t* base, int64_t ld, int row, int col, int rows, int cols,
+                                                 bool vec_ok) {
+    return load16<kChecked>(base, ld, row, col, rows, cols, vec_ok);
+  }
+  template <bool kChecked>
+  __device__ __forceinline__ static u32x2 load_b(const int8_t* base, int64_t ld, int row, int col, int rows, int cols,
+                                                 bool vec_ok) {
+    return load8<kChecked>(base, ld, row, col, rows, cols, vec_ok);
+  }
+  __device__ __forceinline__ static void transpose_b(const u32x2 (&in)[16], u32x4 (&out)[8]) {
+    asc::gemm::transpose16x8_b8(in, out);
+  }
+  __device__ __forceinline__ static i32x16 mfma(u32x4 a, u32x4 b, i32x16 c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
+                                                 0);
+  }
+};
+
 // kMode: 0 = int32 accumulators, 1 = fp16 dequant
 template <bool kChecked, int kMode>
 __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
   int tm, tn;
-  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, asc::gemm::kGroupM, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int64_t lda = p.K, ldb = p.N;
-  const bool a_vec = ((reinterpret_cast<uintptr_t>(p.a) | static_cast<uintptr_t>(lda)) & 15) == 0;
-  const bool b_vec = ((reinterpret_cast<uintptr_t>(p.b) | static_cast<uintptr_t>(ldb)) & 7) == 0;
-
-  // B loader: one 16(k) x 8(n) byte block per thread: n-chunk tid%32, k-group tid/32
-  const int b_nc = tid & 31, b_kg = tid >> 5;
-
-  u32x4 ra[8];
-  u32x2 rb[16];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + kThreads * i;
-      ra[i] = load16<kChecked>(p.a, lda, m0 + (c >> 3), k0 + (c & 7) * 16, p.M, p.K, a_vec);
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      rb[r] = load8<kChecked>(p.b, ldb, k0 + b_kg * 16 + r, n0 + b_nc * 8, p.K, p.N, b_vec);
-    }
-  };
-  auto stash = [&](int stage) {
-    uint8_t* as = smem + stage * kStageBytes;
-    uint8_t* bs = as + BM * 128;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + kThreads * i;
-      *reinterpret_cast<u32x4*>(as + asc::gemm::lds_offset(c >> 3, c & 7)) = ra[i];
-    }
-    u32x4 tb[8];
-    asc::gemm::transpose16x8_b8(rb, tb);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      *reinterpret_cast<u32x4*>(bs + asc::gemm::lds_offset(b_nc * 8 + e, b_kg)) = tb[e];
-    }
-  };
-
+  const int lane = threadIdx.x & 63;
+  const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
   i32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = i32x16{};
-
-  const int k_tiles = (p.K + BK - 1) / BK;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-
-  const int arow = wm * 128 + (lane & 31);
-  const int brow = wn * 128 + (lane & 31);
-  const int khalf = lane >> 5;
-
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    const int stage = kt & 1;
-    if (kt + 1 < k_tiles) fetch((kt + 1) * BK);
-    const uint8_t* as = smem + stage * kStageBytes;
-    const uint8_t* bs = as + BM * 128;
-#pragma unroll
-    for (int s = 0; s < BK / 32; ++s) {
-      const int chunk = s * 2 + khalf;
-      u32x4 fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const u32x4*>(as + asc::gemm::lds_offset(arow + i * 32, chunk));
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const u32x4*>(bs + asc::gemm::lds_offset(brow + j * 32, chunk));
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fa[i]),
-                                                            __builtin_bit_cast(i32x4, fb[j]), acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < k_tiles) stash(stage ^ 1);
-    __syncthreads();
+  if constexpr (kChecked) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kStageBytes];
+    asc::gemm::GemmMainLoop<TrI8, true> L;
+    L.a = p.a;
+    L.b = p.b;
+    L.s = asc::gemm::GemmShape{p.M, p.N, p.K, p.K, p.N, p.tiles_m, p.tiles_n};
+    L.m0 = m0;
+    L.n0 = n0;
+    L.tid = threadIdx.x;
+    L.lane = lane;
+    L.wm = wm;
+    L.wn = wn;
+    L.a_vec = ((reinterpret_cast<uintptr_t>(p.a) | static_cast<uintptr_t>(p.K)) & 15) == 0;
+    L.b_vec = ((reinterpret_cast<uintptr_t>(p.b) | static_cast<uintptr_t>(p.N)) & 7) == 0;
+    L.lds[0] = lds0;
+    L.lds[1] = lds1;
+    L.run(acc);
+  } else {
+    // four LDS stages as distinct objects (see gemm_direct.h)
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
+    asc::gemm::GemmDirectLoop<TrI8> L;
+    L.a = p.a;
+    L.b = p.b;
+    L.m0 = m0;
+    L.n0 = n0;
+    L.lane = lane;
+    L.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
+    L.wm = wm;
+    L.wn = wn;
+    L.lds[0] = lds0;
+    L.lds[1] = lds1;
+    L.lds[2] = lds2;
+    L.lds[3] = lds3;
+    L.init(p.K, p.N);
+    L.run(p.K, acc);
   }
 
   // Epilogue: lane holds column lane%32 of each 32x32 block, register r row
@@ -189,16 +176,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
 
 template <bool kChecked, int kMode>
 int32_t launch(const I8Args& p, hipStream_t stream, const char* who) {
-  auto kern = gemm_i8_kernel<kChecked, kMode>;
-  static bool configured = false;
-  if (!configured) {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
-    if (err != hipSuccess)
-      return asc::set_error(static_cast<int32_t>(err), "%s: hipFuncSetAttribute: %s", who, hipGetErrorString(err));
-    configured = true;
-  }
-  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), 2 * kStageBytes, stream, p);
+  hipLaunchKernelGGL((gemm_i8_kernel<kChecked, kMode>), dim3(p.tiles_m * p.tiles_n), dim3(kThreads), 0, stream, p);
   return asc::check_launch(who);
 }
 
@@ -222,8 +200,10 @@ int32_t run(const int8_t* a, const int8_t* b, const float* scale, void* c, int64
   p.trunc19 = trunc19;
   p.tiles_m = static_cast<int>((M + BM - 1) / BM);
   p.tiles_n = static_cast<int>((N + BN - 1) / BN);
-  const bool fast = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
-                    (M % BM) == 0 && (N % BN) == 0 && (K % BK) == 0 && K > 0;
+  // the direct-to-LDS path addresses each operand with 31-bit buffer offsets
+  const bool offsets_fit = (BM * K + K) < (int64_t{1} << 31) && (K + 128) * N < (int64_t{1} << 31);
+  const bool fast = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 && offsets_fit &&
+                    (M % BM) == 0 && (N % BN) == 0 && (K % 64) == 0 && K > 0;
   if (mode == 0) return fast ? launch<false, 0>(p, stream, who) : launch<true, 0>(p, stream, who);
   return fast ? launch<false, 1>(p, stream, who) : launch<true, 1>(p, stream, who);
 }
