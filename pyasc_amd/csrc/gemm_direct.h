@@ -13,12 +13,13 @@
 //     its own loads of tile kt+2 (vmcnt counts the one newer tile), and the
 //     first operand fragments of tile kt+1 are already read.
 //   - A tile: 256 rows x 64 bytes (K contiguous); 16-byte chunks swizzled by
-//     gA(row) = ((row >> 1) ^ (row >> 3)) & 3; MFMA operands are ds_read_b128.
+//     gA(row) = (row >> 2) & 3; MFMA operands are ds_read_b128.
 //   - B tile: kBK rows (K) x 256 columns, row-major as in HBM (N contiguous);
 //     the K-contiguous MFMA operand is read with the gfx950 LDS transpose
 //     reads (ds_read_b64_tr_b16 / ds_read_b64_tr_b8).  16-byte chunks are
 //     swizzled per row so those reads are conflict-free (tables found by
-//     enumerating both 128- and 256-byte-per-cycle bank models).
+//     enumerating bank models, confirmed with SQ_LDS_BANK_CONFLICT = 0 on the
+//     device).
 //   - Lane layouts of the transpose reads (measured on the device): in each
 //     16-lane group, b16: lane i receives element i%4 of lane 4j + i/4's 8-byte
 //     read (j = 0..3); b8: lane i receives byte i%8 of lane 2j + i/8's read
@@ -49,8 +50,10 @@ struct GemmDirectLoop {
   static constexpr int kBRowsPerLoad = 1024 / kBRowBytes;
   static constexpr int kBOff = 16384;
 
-  // A chunk swizzle (4 chunks per 64-byte row)
-  __device__ __forceinline__ static int ga(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+  // A chunk swizzle (4 chunks per 64-byte row).  Chosen by measurement
+  // (SQ_LDS_BANK_CONFLICT on the operand-read pattern): (row >> 2) & 3 reads
+  // conflict-free, ((row >> 1) ^ (row >> 3)) & 3 costs 4 conflict cycles per read.
+  __device__ __forceinline__ static int ga(int row) { return (row >> 2) & 3; }
   // B chunk swizzle: position p of row r holds logical chunk p ^ fb(r)
   __device__ __forceinline__ static int fb(int row) {
     if constexpr (kES == 2) return (0xCA60u >> (4 * (row & 3))) & 15;   // {0, 6, 10, 12}
@@ -180,12 +183,32 @@ struct GemmDirectLoop {
                                             u32x4 (&fb0)[4], u32x4 (&fa1)[4], u32x4 (&fb1)[4]) {
     constexpr int kNext = (kS + 1) % kDirectStages;
     constexpr int kAhead = (kS + 3) % kDirectStages;
-    // tile kt+3 (clamped: the tail re-loads the last tile into a free stage)
+    // k-step 0: tile kt+3's loads (clamped: the tail re-loads the last tile
+    // into a free stage) and k-step 1's operand reads, one per MFMA.
     issue_loads<kAhead>((kt + 3 < k_tiles ? kt + 3 : k_tiles - 1) * kBK);
     read_frags<kS>(1, fa1, fb1);
     mma(acc, fa0, fb0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (LDS DMA)
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    // k-step 1: the next tile's k-step-0 operands, one read per MFMA
     read_frags<kNext>(0, fa0, fb0);
     mma(acc, fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     // own loads of tile kt+2 done (only tile kt+3's eight may still run), and
     // this wave's reads of stage kS complete before anyone reloads it
     asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
