@@ -10,8 +10,10 @@ matmul 8192^3, int8 matmul 4096x11008x4096 + dequant, flash-attention forward)
 are measured the same way and reported under "suite".
 
 Timing: W untimed warm-up steps, then exactly K steps bracketed by
-torch.cuda.synchronize(), timed with HIP events recorded on the stream the
-kernels are launched on (torch's current stream).  HBM-bound workloads rotate
+torch.cuda.synchronize().  The K launches are captured into one HIP graph and
+one replay is timed with HIP events on the replay stream (the kernels run back
+to back, without host launch overhead); --no-graph times each launch with its
+own event pair instead.  HBM-bound workloads rotate
 through enough input/output sets (> 512 MiB) that the 256 MiB Infinity Cache
 cannot serve them.  The CPU baseline is the reference test's torch CPU golden
 expression (oracle/cpu_golden.py), timed on the host cores on a bounded sample.
@@ -267,29 +269,54 @@ def _time_cpu(fn, budget_s: float) -> float:
     return statistics.median(times)
 
 
-def measure(w: Workload, steps: int, warmup: int, dev) -> dict:
-    """Times exactly ``steps`` launches.  Each launch is bracketed by its own pair of
-    HIP events on the launch stream, so ``kernel_ms`` is the GPU duration of the
-    kernel itself (the figure the roofline uses) and ``ms_per_step`` the wall time of
-    the whole timed region divided by ``steps``."""
+def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True) -> dict:
+    """Times exactly ``steps`` launches on the launch stream with HIP events.
+
+    Default: the ``steps`` launches are captured once into a HIP graph and the
+    graph is replayed between two events, so the kernels run back to back with
+    no host launch overhead in the timed region (``kernel_ms`` = region / steps).
+    ``graph=False``: each launch is bracketed by its own event pair instead and
+    ``kernel_ms`` is their mean (adds about 2 us of event overhead per launch)."""
     import torch
     w.setup(dev)
     for i in range(warmup):
         w.launch(i)
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    torch.cuda.synchronize()
-    for i in range(steps):
-        ev[i][0].record(stream)
-        w.launch(warmup + i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    ms = ev[0][0].elapsed_time(ev[-1][1]) / steps
-    kernel_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for i in range(steps):
+                    w.launch(warmup + i)
+        torch.cuda.synchronize()
+        g.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        kernel_ms = ms
+        del g
+    else:
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        for i in range(steps):
+            ev[i][0].record(stream)
+            w.launch(warmup + i)
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        ms = ev[0][0].elapsed_time(ev[-1][1]) / steps
+        kernel_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
     rate = w.rate(kernel_ms / 1e3)
     return {"workload": w.name, "ms_per_step": ms, "kernel_ms": kernel_ms, "value": rate, "unit": w.unit,
-            "frac_of_peak": rate / w.peak, "bound": w.bound, "config": w.config()}
+            "frac_of_peak": rate / w.peak, "bound": w.bound, "config": w.config(),
+            "timing": "hip-graph replay" if graph else "per-launch events"}
 
 
 def traffic_for(name: str):
@@ -309,6 +336,7 @@ def main() -> int:
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time with per-launch event pairs, no HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -327,14 +355,14 @@ def main() -> int:
     dev = torch.device("cuda", 0)
 
     head = WORKLOADS[args.workload]()
-    res = measure(head, args.steps, args.warmup, dev)
+    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph)
     suite = {}
     if not args.no_suite:
         for name in SUITE:
             if name == args.workload:
                 continue
             w = WORKLOADS[name]()
-            r = measure(w, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+            r = measure(w, max(5, args.steps // 2), max(2, args.warmup // 2), dev, graph=not args.no_graph)
             r["roofline"] = {"bound": w.bound, "achieved": r["value"], "peak": w.peak, "unit": w.unit,
                              "frac": r["value"] / w.peak, "traffic": traffic_for(w.name)}
             suite[name] = r
@@ -357,6 +385,7 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": res["ms_per_step"],
         "kernel_ms": res["kernel_ms"],
+        "timing": res["timing"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -16,6 +16,8 @@
 
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 struct RowView {
   const float* x;
   float* out;
@@ -28,7 +30,11 @@ struct RowView {
 // Loads vector q (elements 4q..4q+3) of a row, padding with -inf past `len`.
 __device__ __forceinline__ float4 load_vec(const float* row, int q, int len, bool vec_ok) {
   const int e = q * 4;
-  if (vec_ok && e + 3 < len) return *reinterpret_cast<const float4*>(row + e);
+  if (vec_ok && e + 3 < len) {
+    // streamed once: non-temporal so the rows do not displace other cached data
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + e));
+    return make_float4(v.x, v.y, v.z, v.w);
+  }
   float4 v;
   v.x = e + 0 < len ? row[e + 0] : -INFINITY;
   v.y = e + 1 < len ? row[e + 1] : -INFINITY;
@@ -40,7 +46,7 @@ __device__ __forceinline__ float4 load_vec(const float* row, int q, int len, boo
 __device__ __forceinline__ void store_vec(float* row, int q, int len, bool vec_ok, float4 v) {
   const int e = q * 4;
   if (vec_ok && e + 3 < len) {
-    *reinterpret_cast<float4*>(row + e) = v;
+    __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(row + e));
     return;
   }
   if (e + 0 < len) row[e + 0] = v.x;
@@ -59,70 +65,94 @@ __device__ __forceinline__ float4 exp_shift(float4 v, float m) {
   return r;
 }
 
-// One wave per row; each lane holds VPL float4 vectors in registers.
-template <int VPL>
+// One wave per row; each lane holds VPL float4 vectors of each of kRows rows
+// (all rows' loads are issued before any reduction, so more bytes are in flight).
+template <int VPL, int kRows>
 __global__ void __launch_bounds__(256) softmax_wave_kernel(RowView p) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (r >= p.rows) return;
-  const float* row = p.x + r * p.stride;
-  float4 v[VPL];
-  float m = -INFINITY;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kRows;
+  float4 v[kRows][VPL];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    v[j] = load_vec(row, lane + 64 * j, p.len, p.vec_ok);
-    m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+  for (int k = 0; k < kRows; ++k) {
+    if (r0 + k >= p.rows) continue;
+    const float* row = p.x + (r0 + k) * p.stride;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) v[k][j] = load_vec(row, lane + 64 * j, p.len, p.vec_ok);
   }
-  m = asc::wave_max(m);
-  float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    v[j] = exp_shift(v[j], m);
-    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-  }
-  s = asc::wave_sum(s);
-  float* orow = p.out + r * p.stride;
+  for (int k = 0; k < kRows; ++k) {
+    if (r0 + k >= p.rows) continue;
+    float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    float4 o = make_float4(v[j].x / s, v[j].y / s, v[j].z / s, v[j].w / s);
-    store_vec(orow, lane + 64 * j, p.len, p.vec_ok, o);
+    for (int j = 0; j < VPL; ++j) m = fmaxf(m, fmaxf(fmaxf(v[k][j].x, v[k][j].y), fmaxf(v[k][j].z, v[k][j].w)));
+    m = asc::wave_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      v[k][j] = exp_shift(v[k][j], m);
+      s += (v[k][j].x + v[k][j].y) + (v[k][j].z + v[k][j].w);
+    }
+    s = asc::wave_sum(s);
+    float* orow = p.out + (r0 + k) * p.stride;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float4 o = make_float4(v[k][j].x / s, v[k][j].y / s, v[k][j].z / s, v[k][j].w / s);
+      store_vec(orow, lane + 64 * j, p.len, p.vec_ok, o);
+    }
   }
 }
 
-// One 256-thread block per row; each thread holds VPT float4 vectors.
-template <int VPT>
+// One 256-thread block per kRows rows; each thread holds VPT float4 vectors of
+// each row.  All rows are loaded first; the cross-wave max and sum of all rows
+// share one barrier each.
+template <int VPT, int kRows>
 __global__ void __launch_bounds__(256) softmax_block_kernel(RowView p) {
   constexpr int kWaves = 256 / 64;
-  __shared__ float red[2][kWaves];
+  __shared__ float red[2][kRows][kWaves];
   const int t = threadIdx.x;
-  const int64_t r = blockIdx.x;
-  const float* row = p.x + r * p.stride;
-  float4 v[VPT];
-  float m = -INFINITY;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  float4 v[kRows][VPT];
+  float m[kRows], s[kRows];
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    v[j] = load_vec(row, t + 256 * j, p.len, p.vec_ok);
-    m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+  for (int k = 0; k < kRows; ++k) {
+    const bool live = r0 + k < p.rows;
+    const float* row = p.x + (live ? r0 + k : r0) * p.stride;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) v[k][j] = load_vec(row, t + 256 * j, live ? p.len : 0, p.vec_ok);
   }
-  m = asc::wave_max(m);
-  if ((t & 63) == 0) red[0][t >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    v[j] = exp_shift(v[j], m);
-    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  for (int k = 0; k < kRows; ++k) {
+    m[k] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      m[k] = fmaxf(m[k], fmaxf(fmaxf(v[k][j].x, v[k][j].y), fmaxf(v[k][j].z, v[k][j].w)));
+    m[k] = asc::wave_max(m[k]);
+    if ((t & 63) == 0) red[0][k][t >> 6] = m[k];
   }
-  s = asc::wave_sum(s);
-  if ((t & 63) == 0) red[1][t >> 6] = s;
   __syncthreads();
-  s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-  float* orow = p.out + r * p.stride;
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    float4 o = make_float4(v[j].x / s, v[j].y / s, v[j].z / s, v[j].w / s);
-    store_vec(orow, t + 256 * j, p.len, p.vec_ok, o);
+  for (int k = 0; k < kRows; ++k) {
+    m[k] = fmaxf(fmaxf(red[0][k][0], red[0][k][1]), fmaxf(red[0][k][2], red[0][k][3]));
+    s[k] = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      v[k][j] = exp_shift(v[k][j], m[k]);
+      s[k] += (v[k][j].x + v[k][j].y) + (v[k][j].z + v[k][j].w);
+    }
+    s[k] = asc::wave_sum(s[k]);
+    if ((t & 63) == 0) red[1][k][t >> 6] = s[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kRows; ++k) {
+    if (r0 + k >= p.rows) continue;
+    const float sum = (red[1][k][0] + red[1][k][1]) + (red[1][k][2] + red[1][k][3]);
+    float* orow = p.out + (r0 + k) * p.stride;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      float4 o = make_float4(v[k][j].x / sum, v[k][j].y / sum, v[k][j].z / sum, v[k][j].w / sum);
+      store_vec(orow, t + 256 * j, p.len, p.vec_ok, o);
+    }
   }
 }
 
@@ -163,22 +193,24 @@ int32_t launch_rows(const RowView& p, hipStream_t stream, const char* who) {
   if (p.rows == 0 || p.len == 0) return ASC_OK;
   const int64_t L = p.len;
   const dim3 block(256);
-  const dim3 wave_grid(static_cast<uint32_t>(asc::ceil_div(p.rows, 4)));
-  const dim3 row_grid(static_cast<uint32_t>(p.rows));
+  // 2 rows per wave (measured faster at 1024 columns than 1)
+  const dim3 wave_grid(static_cast<uint32_t>(asc::ceil_div(p.rows, 8)));
   if (L <= 256) {
-    hipLaunchKernelGGL(softmax_wave_kernel<1>, wave_grid, block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_wave_kernel<1, 2>), wave_grid, block, 0, stream, p);
   } else if (L <= 512) {
-    hipLaunchKernelGGL(softmax_wave_kernel<2>, wave_grid, block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_wave_kernel<2, 2>), wave_grid, block, 0, stream, p);
   } else if (L <= 1024) {
-    hipLaunchKernelGGL(softmax_wave_kernel<4>, wave_grid, block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_wave_kernel<4, 2>), wave_grid, block, 0, stream, p);
   } else if (L <= 2048) {
-    hipLaunchKernelGGL(softmax_block_kernel<2>, row_grid, block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_block_kernel<2, 1>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else if (L <= 4096) {
-    hipLaunchKernelGGL(softmax_block_kernel<4>, row_grid, block, 0, stream, p);
+    // one row per block measured fastest here (2 rows per block, or persistent
+    // blocks streaming rows, lose occupancy or add a launch round)
+    hipLaunchKernelGGL((softmax_block_kernel<4, 1>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else if (L <= 8192) {
-    hipLaunchKernelGGL(softmax_block_kernel<8>, row_grid, block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_block_kernel<8, 1>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else {
-    hipLaunchKernelGGL(softmax_long_kernel, row_grid, block, 0, stream, p);
+    hipLaunchKernelGGL(softmax_long_kernel, dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   }
   return asc::check_launch(who);
 }
