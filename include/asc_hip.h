@@ -149,8 +149,8 @@ int32_t asc_matmul_i8_dequant_f16(const int8_t* a, const int8_t* b,
  *   flash_attention_fwd_kernel(q_ptr, k_ptr, v_ptr, o_ptr, batch, heads,
  *       seq_len, head_dim: ConstExpr[int], sm_scale: float,
  *       causal: ConstExpr[bool], block_m: ConstExpr[int], block_n: ConstExpr[int])
- * O = softmax(Q K^T * sm_scale + mask) V per (batch, head); q, k, v, o are
- * contiguous bf16 [batch, heads, seq_len, head_dim]; fp32 online-softmax
+ * O = softmax(Q K^T * sm_scale + mask) V per (batch, head), sm_scale > 0;
+ * q, k, v, o are contiguous bf16 [batch, heads, seq_len, head_dim]; fp32 online-softmax
  * statistics; causal masks keys j > query i.  lse (optional, may be NULL)
  * receives fp32 log-sum-exp per row [batch, heads, seq_len] in natural log. */
 int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k,

@@ -14,9 +14,12 @@
 //    data movement; A and B agree on which key each operand slot holds), V^T is
 //    read from the row-major V tile with ds_read_b64_tr_b16 (gfx950 LDS
 //    transpose read).  Q^T stays in registers for the whole kernel.
-//  - Online softmax in the exp2 domain with scale*log2(e) folded into one
-//    multiply; causal tiles above the diagonal are skipped and the diagonal
-//    tile is masked; heavy (late) query blocks are scheduled first.
+//  - Online softmax in the exp2 domain: the max is taken on raw scores and
+//    scale*log2(e) and the shift fold into one FMA before exp2; the reference
+//    point only moves when a tile max exceeds it by more than 8 (exact
+//    arithmetic either way, O and l are rescaled rarely); causal tiles above
+//    the diagonal are skipped and the diagonal tile is masked; heavy (late)
+//    query blocks are scheduled first.
 // LDS tiles use XOR-swizzled 16-byte chunks so that both the MFMA operand
 // reads and the transpose reads are free of bank conflicts.
 #include <math.h>
@@ -77,102 +80,73 @@ __device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
                                                  0, 0);
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 pair, RNE (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return static_cast<uint32_t>(asc::f32_to_bf16_rne(lo)) | (static_cast<uint32_t>(asc::f32_to_bf16_rne(hi)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
+// Largest exponent (log2 domain) an unnormalised probability may reach before
+// the running max is moved; bounds exp2 values by 2^8.
+constexpr float kRescaleSlack = 8.0f;
+
+// Per-workgroup state of the attention kernel.
 template <int D>
-__global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
-  constexpr int kChunks = D / 8;              // 16-byte chunks per row
-  constexpr int kTileBytes = BKV * D * 2;     // one K or V tile
-  constexpr int kKSteps = D / 16;             // MFMA k-steps over head_dim
-  constexpr int kDBlocks = D / 32;            // 32-wide d blocks of O^T
-  constexpr int kLoads = BKV * kChunks / kThreads;  // 16-byte loads per thread per tile
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * kTileBytes];
+struct FaState {
+  static constexpr int kChunks = D / 8;           // 16-byte chunks per row
+  static constexpr int kTileBytes = BKV * D * 2;  // one K or V tile
+  static constexpr int kKSteps = D / 16;          // MFMA k-steps over head_dim
+  static constexpr int kDBlocks = D / 32;         // 32-wide d blocks of O^T
+  static constexpr int kRowsPerLoad = 1024 / (D * 2);     // tile rows per 1 KiB wave load
+  static constexpr int kLoadsPerWave = BKV / kRowsPerLoad / kWaves;  // per operand per tile
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int col = lane & 31;  // query column within the wave's 32
-  const int h = lane >> 5;    // lane half
-
-  // heavy-first order for causal: all (batch, head) of the last query block first
-  const int64_t bid = blockIdx.x;
-  const int64_t bh = bid % p.heads_total;
-  int qb = static_cast<int>(bid / p.heads_total);
-  if (p.causal) qb = p.n_qblocks - 1 - qb;
-  const int q0 = qb * BQ;
-  const int S = p.seq;
-  const int64_t head_off = bh * static_cast<int64_t>(S) * D;
-  const uint16_t* Qh = p.q + head_off;
-  const uint16_t* Kh = p.k + head_off;
-  const uint16_t* Vh = p.v + head_off;
-
-  const int my_q = q0 + wave * 32 + col;
-  const int wave_qmax = q0 + wave * 32 + 31;
-
-  // Q^T operand: lane (query col, half h) holds Q[my_q][16*ks + 8h .. +8]
+  int lane, wave, col, h;
+  int q0, S, my_q, wave_qmax, causal;
+  float scale_log2;
+  __amdgpu_buffer_rsrc_t rsrc_k, rsrc_v;
+  int voff_k[4], voff_v;
   u32x4 qreg[kKSteps];
+  f32x16 acc_o[kDBlocks];
+  float m_run, l_run;
+
+  // K/V tile rows go straight from HBM into LDS (buffer_load ... lds, 1 KiB per
+  // wave instruction, lane l -> row kRowsPerLoad*R + l/(64/kRowsPerLoad)).  The
+  // lane loads the logical chunk that the row's swizzle puts at its position;
+  // keys >= S read as zero through the descriptor's byte bound.
+  __device__ __forceinline__ void init_loads(const uint16_t* Kh, const uint16_t* Vh) {
+    const int bytes = S * D * 2;
+    rsrc_k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Kh), static_cast<short>(0), bytes, 0x00020000);
+    rsrc_v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Vh), static_cast<short>(0), bytes, 0x00020000);
+    constexpr int kLanesPerRow = 64 / kRowsPerLoad;
+    const int rr = lane / kLanesPerRow, pos = lane % kLanesPerRow;
 #pragma unroll
-  for (int ks = 0; ks < kKSteps; ++ks) {
-    if (my_q < S) {
-      qreg[ks] = *reinterpret_cast<const u32x4*>(Qh + static_cast<int64_t>(my_q) * D + ks * 16 + h * 8);
-    } else {
-      qreg[ks] = u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 4; ++i) {  // the K swizzle depends on (row mod 16) = kRowsPerLoad*(R mod 4) + rr
+      const int row = kRowsPerLoad * i + rr;
+      voff_k[i] = rr * (D * 2) + ((pos ^ kswz<D>(row)) << 4);
+    }
+    voff_v = rr * (D * 2) + ((pos ^ vswz<D>(rr)) << 4);
+  }
+
+  __device__ __forceinline__ void issue_loads(uint8_t* ks_, uint8_t* vs_, int k0) const {
+#pragma unroll
+    for (int i = 0; i < kLoadsPerWave; ++i) {
+      const int R = wave * kLoadsPerWave + i;
+      // the row offset goes into the per-lane offset, not the SGPR offset: the
+      // buffer range check (keys >= S read as zero) only covers the former
+      const int roff = (k0 + kRowsPerLoad * R) * (D * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_k, (__attribute__((address_space(3))) void*)(ks_ + R * 1024),
+                                               16, voff_k[R & 3] + roff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_v, (__attribute__((address_space(3))) void*)(vs_ + R * 1024),
+                                               16, voff_v + roff, 0, 0, 0);
     }
   }
 
-  int kv_end = S;
-  if (p.causal) kv_end = min(S, q0 + BQ);
-  const int n_tiles = (kv_end + BKV - 1) / BKV;
-
-  u32x4 rk[kLoads], rv[kLoads];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c / kChunks, ch = c % kChunks;
-      const int key = k0 + row;
-      if (key < S) {
-        rk[i] = *reinterpret_cast<const u32x4*>(Kh + static_cast<int64_t>(key) * D + ch * 8);
-        rv[i] = *reinterpret_cast<const u32x4*>(Vh + static_cast<int64_t>(key) * D + ch * 8);
-      } else {
-        rk[i] = u32x4{0, 0, 0, 0};
-        rv[i] = u32x4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto stash = [&](int stage) {
-    uint8_t* ks_ = smem + stage * 2 * kTileBytes;
-    uint8_t* vs_ = ks_ + kTileBytes;
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c / kChunks, ch = c % kChunks;
-      *reinterpret_cast<u32x4*>(ks_ + k_off<D>(row, ch)) = rk[i];
-      *reinterpret_cast<u32x4*>(vs_ + v_off<D>(row, ch * 8)) = rv[i];
-    }
-  };
-
-  f32x16 acc_o[kDBlocks];
-#pragma unroll
-  for (int i = 0; i < kDBlocks; ++i) acc_o[i] = f32x16{};
-  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
-  float l_run = 0.f;        // running sum of exp2(s - m_run)
-
-  fetch(0);
-  stash(0);
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int stage = t & 1;
-    const int k0 = t * BKV;
-    if (t + 1 < n_tiles) fetch(k0 + BKV);
-    const uint8_t* ks_ = smem + stage * 2 * kTileBytes;
-    const uint8_t* vs_ = ks_ + kTileBytes;
-
+  // One K/V tile from LDS (ks_, vs_): S^T, online softmax, O^T += V^T P^T.
+  __device__ __forceinline__ void tile(const uint8_t* ks_, const uint8_t* vs_, int k0) {
     // causal: a wave whose queries all precede the tile skips it
-    const bool active = !(p.causal && k0 > wave_qmax);
+    const bool active = !(causal && k0 > wave_qmax);
     if (active) {
       // ---- S^T = K Q^T for keys k0 .. k0+63 (two 32-key blocks)
       f32x16 s[2];
@@ -186,42 +160,51 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
           s[kb] = mfma_bf16(a, qreg[kk], s[kb]);
         }
       }
-      // ---- scale, mask, tile max.  Register r of block kb holds key
-      //      k0 + 32*kb + 8*(r/4) + 4*h + r%4 for query my_q.
-      const bool need_mask = (k0 + BKV > S) || (p.causal && k0 + BKV - 1 > q0 + wave * 32);
-      float mt = -INFINITY;
+      // ---- mask and tile max on the raw scores (sm_scale > 0, so the max of
+      //      the scaled scores is the scaled max).  Register r of block kb
+      //      holds key k0 + 32*kb + 8*(r/4) + 4*h + r%4 for query my_q.
+      const bool need_mask = (k0 + BKV > S) || (causal && k0 + BKV - 1 > q0 + wave * 32);
+      if (need_mask) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[kb][r] * p.scale_log2;
-          if (need_mask) {
+          for (int r = 0; r < 16; ++r) {
             const int key = k0 + kb * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-            if (key >= S || (p.causal && key > my_q)) x = -INFINITY;
+            if (key >= S || (causal && key > my_q)) s[kb][r] = -INFINITY;
           }
-          s[kb][r] = x;
-          mt = fmaxf(mt, x);
         }
       }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m_run, mt);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
+      // Lazy rescale: the reference point m_run only moves when the tile max
+      // exceeds it by more than kRescaleSlack (log2 units), so exp2 values stay
+      // below 2^kRescaleSlack and O / l are rescaled rarely.  The branch is
+      // wave-uniform (any lane that needs it).
+      const bool upd = mt > m_run + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(upd) != 0) {
+        const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
+        if (upd) m_run = mt;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < kDBlocks; ++db) acc_o[db] *= alpha;
+      }
+      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
       float rs = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(s[kb][r] - m_use);
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale_log2, neg_m));
           s[kb][r] = e;
           rs += e;
         }
       }
       rs += __shfl_xor(rs, 32, 64);
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < kDBlocks; ++db) acc_o[db] *= alpha;
+      l_run += rs;
 
       // ---- P^T operands: block kb, step u uses registers 8u..8u+7, i.e. keys
       //      32kb + 16u + 4h + {0..3} and 32kb + 16u + 8 + 4h + {0..3}.
@@ -262,9 +245,94 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
         }
       }
     }
-    if (t + 1 < n_tiles) stash(stage ^ 1);
-    __syncthreads();
   }
+};
+
+template <int D>
+__global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
+  constexpr int kTileBytes = FaState<D>::kTileBytes;
+  constexpr int kChunks = FaState<D>::kChunks;
+  constexpr int kKSteps = FaState<D>::kKSteps;
+  constexpr int kDBlocks = FaState<D>::kDBlocks;
+  // two LDS stages (K and V tile each) as distinct objects, so the compiler can
+  // tell that loads into one stage do not alias reads of the other
+  __shared__ __attribute__((aligned(16))) uint8_t stage0[2 * kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t stage1[2 * kTileBytes];
+
+  FaState<D> st;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  st.lane = lane;
+  st.wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  st.col = lane & 31;  // query column within the wave's 32
+  st.h = lane >> 5;    // lane half
+  const int wave = st.wave, col = st.col, h = st.h;
+
+  // Block order: query-block major, all (batch, head) of one query block
+  // together; causal runs the heavy (late) query blocks first.  (Block b lands
+  // on XCD b % 8, so all query blocks of a head share one XCD.  A head-major
+  // order measured no faster non-causal and slower causal.)
+  const int64_t bid = blockIdx.x;
+  const int64_t bh = bid % p.heads_total;
+  int qb = static_cast<int>(bid / p.heads_total);
+  if (p.causal) qb = p.n_qblocks - 1 - qb;
+  const int q0 = qb * BQ;
+  const int S = p.seq;
+  const int64_t head_off = bh * static_cast<int64_t>(S) * D;
+  const uint16_t* Qh = p.q + head_off;
+  st.q0 = q0;
+  st.S = S;
+  st.causal = p.causal;
+  st.scale_log2 = p.scale_log2;
+  st.my_q = q0 + wave * 32 + col;
+  st.wave_qmax = q0 + wave * 32 + 31;
+  const int my_q = st.my_q;
+
+  // Q^T operand: lane (query col, half h) holds Q[my_q][16*ks + 8h .. +8]
+#pragma unroll
+  for (int ks = 0; ks < kKSteps; ++ks) {
+    if (my_q < S) {
+      st.qreg[ks] = *reinterpret_cast<const u32x4*>(Qh + static_cast<int64_t>(my_q) * D + ks * 16 + h * 8);
+    } else {
+      st.qreg[ks] = u32x4{0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDBlocks; ++i) st.acc_o[i] = f32x16{};
+  st.m_run = -INFINITY;  // reference point of the scaled scores (log2 domain), <= running max
+  st.l_run = 0.f;        // running sum of exp2(s*scale_log2 - m_run)
+
+  int kv_end = S;
+  if (p.causal) kv_end = min(S, q0 + BQ);
+  const int n_tiles = (kv_end + BKV - 1) / BKV;
+
+  st.init_loads(p.k + head_off, p.v + head_off);
+  st.issue_loads(stage0, stage0 + kTileBytes, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+  // Tile t lives in stage t % 2; tile t+1 streams into the other stage while
+  // tile t is computed.  Before the barrier a wave waits for its own loads and
+  // its own LDS reads only (a plain s_barrier, not __syncthreads, whose fence
+  // would also drain unrelated counters).
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    st.issue_loads(stage1, stage1 + kTileBytes, (t + 1) * BKV);
+    st.tile(stage0, stage0 + kTileBytes, t * BKV);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (t + 2 < n_tiles) st.issue_loads(stage0, stage0 + kTileBytes, (t + 2) * BKV);
+    st.tile(stage1, stage1 + kTileBytes, (t + 1) * BKV);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+  }
+  if (t < n_tiles) {
+    st.tile(stage0, stage0 + kTileBytes, t * BKV);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+  }
+  const float m_run = st.m_run, l_run = st.l_run;
+  f32x16 (&acc_o)[kDBlocks] = st.acc_o;
+  uint8_t* smem = stage0;  // reused for the O transpose (the loop ended with a barrier)
 
   // ---- epilogue: O = O^T / l, transposed through LDS into row-major bf16.
   //      Lane holds query my_q and, for d block db and register r,
@@ -316,7 +384,11 @@ extern "C" int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k, co
               "asc_flash_attention_fwd_bf16: negative shape");
   ASC_REQUIRE(head_dim == 64 || head_dim == 128, ASC_ERR_UNSUPPORTED,
               "asc_flash_attention_fwd_bf16: head_dim %d not supported (64, 128)", head_dim);
-  ASC_REQUIRE(seq_len < (1 << 30), ASC_ERR_UNSUPPORTED, "asc_flash_attention_fwd_bf16: seq_len too large");
+  // K/V of one head are addressed with 32-bit buffer offsets (one tile past the end included)
+  ASC_REQUIRE((seq_len + BKV) * head_dim * 2 < (int64_t{1} << 31), ASC_ERR_UNSUPPORTED,
+              "asc_flash_attention_fwd_bf16: seq_len %lld too large for head_dim %d",
+              static_cast<long long>(seq_len), head_dim);
+  ASC_REQUIRE(sm_scale > 0.f, ASC_ERR_INVALID_ARG, "asc_flash_attention_fwd_bf16: sm_scale must be positive");
   if (batch == 0 || heads == 0 || seq_len == 0) return ASC_OK;
   ASC_REQUIRE(q && k && v && o, ASC_ERR_INVALID_ARG, "asc_flash_attention_fwd_bf16: null buffer");
   ASC_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |

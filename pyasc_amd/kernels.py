@@ -194,6 +194,8 @@ def flash_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: to
         if t.dim() != 4 or tuple(t.shape) != tuple(q.shape):
             raise ValueError(f"'{n}' must be [batch, heads, seq_len, head_dim] like q {tuple(q.shape)}")
     batch, heads, seq_len, head_dim = q.shape
+    if not sm_scale > 0:
+        raise ValueError(f"sm_scale must be positive, got {sm_scale}")
     if head_dim not in FA_HEAD_DIMS:
         raise ValueError(f"head_dim {head_dim} not supported (supported: {FA_HEAD_DIMS})")
     lse_ptr = 0
