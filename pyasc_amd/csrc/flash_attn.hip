@@ -88,11 +88,20 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
+// Value of lane l^32 (v_permlane32_swap: lanes 32..63 of the first operand trade
+// places with lanes 0..31 of the second; the lane half picks the result that
+// holds the partner's value).
+__device__ __forceinline__ float other_half(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // Largest exponent (log2 domain) an unnormalised probability may reach before
 // the running max is moved; bounds exp2 values by 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-// Per-workgroup state of the attention kernel.
+// Per-wave state of the attention kernel (a wave owns 32 queries).
 template <int D>
 struct FaState {
   static constexpr int kChunks = D / 8;           // 16-byte chunks per row
@@ -100,16 +109,22 @@ struct FaState {
   static constexpr int kKSteps = D / 16;          // MFMA k-steps over head_dim
   static constexpr int kDBlocks = D / 32;         // 32-wide d blocks of O^T
   static constexpr int kRowsPerLoad = 1024 / (D * 2);     // tile rows per 1 KiB wave load
-  static constexpr int kLoadsPerWave = BKV / kRowsPerLoad / kWaves;  // per operand per tile
+  static constexpr int kLoadsPerWave = BKV / kRowsPerLoad / kWaves;  // per tile
 
   int lane, wave, col, h;
   int q0, S, my_q, wave_qmax, causal;
   float scale_log2;
   __amdgpu_buffer_rsrc_t rsrc_k, rsrc_v;
   int voff_k[4], voff_v;
+  // Per-lane LDS read offsets, loop-invariant: the K swizzle of row kb*32+col
+  // equals that of row col, and the V swizzle of row r0+j (r0 % 4 == 0) equals
+  // that of row j, so every other term of a read address is an immediate.
+  uint32_t kaddr[kKSteps];   // K row col, chunk 2*kk+h
+  uint32_t vaddr[kDBlocks];  // V transpose read of d block db, rows 4h+j
   u32x4 qreg[kKSteps];
   f32x16 acc_o[kDBlocks];
-  float m_run, l_run;
+  float m_run;   // reference point of the scaled scores (log2 domain), <= running max
+  float l_part;  // this lane half's share of the running sum of exp2(s*scale_log2 - m_run)
 
   // K/V tile rows go straight from HBM into LDS (buffer_load ... lds, 1 KiB per
   // wave instruction, lane l -> row kRowsPerLoad*R + l/(64/kRowsPerLoad)).  The
@@ -127,126 +142,162 @@ struct FaState {
       voff_k[i] = rr * (D * 2) + ((pos ^ kswz<D>(row)) << 4);
     }
     voff_v = rr * (D * 2) + ((pos ^ vswz<D>(rr)) << 4);
+#pragma unroll
+    for (int kk = 0; kk < kKSteps; ++kk) kaddr[kk] = k_off<D>(col, kk * 2 + h);
+    // ds_read_b64_tr_b16: in each 16-lane group, lane 4j+q addresses row
+    // (rowstart + j), columns 4q..4q+3 of the group's 16 columns; lane i of the
+    // group receives column i, rows rowstart..+3.
+    const int g_lane = lane & 15;
+    const int tr_col = ((lane >> 4) & 1) * 16 + (g_lane & 3) * 4;
+#pragma unroll
+    for (int db = 0; db < kDBlocks; ++db) vaddr[db] = v_off<D>(h * 4 + (g_lane >> 2), db * 32 + tr_col);
   }
 
-  __device__ __forceinline__ void issue_loads(uint8_t* ks_, uint8_t* vs_, int k0) const {
+  // Keys k0 .. k0+63 of K (kIsV false) or V into one LDS stage.
+  template <bool kIsV>
+  __device__ __forceinline__ void load_tile(uint8_t* dst, int k0) const {
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i) {
       const int R = wave * kLoadsPerWave + i;
       // the row offset goes into the per-lane offset, not the SGPR offset: the
       // buffer range check (keys >= S read as zero) only covers the former
       const int roff = (k0 + kRowsPerLoad * R) * (D * 2);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_k, (__attribute__((address_space(3))) void*)(ks_ + R * 1024),
-                                               16, voff_k[R & 3] + roff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_v, (__attribute__((address_space(3))) void*)(vs_ + R * 1024),
-                                               16, voff_v + roff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kIsV ? rsrc_v : rsrc_k,
+                                               (__attribute__((address_space(3))) void*)(dst + R * 1024), 16,
+                                               (kIsV ? voff_v : voff_k[R & 3]) + roff, 0, 0, 0);
     }
   }
 
-  // One K/V tile from LDS (ks_, vs_): S^T, online softmax, O^T += V^T P^T.
-  __device__ __forceinline__ void tile(const uint8_t* ks_, const uint8_t* vs_, int k0) {
-    // causal: a wave whose queries all precede the tile skips it
-    const bool active = !(causal && k0 > wave_qmax);
-    if (active) {
-      // ---- S^T = K Q^T for keys k0 .. k0+63 (two 32-key blocks)
-      f32x16 s[2];
+  // causal: a wave whose queries all precede the tile skips it
+  __device__ __forceinline__ bool active(int k0) const { return !(causal && k0 > wave_qmax); }
+
+  // S^T = K Q^T for keys k0 .. k0+63 (two 32-key blocks).  Register r of block
+  // kb then holds key k0 + 32*kb + 8*(r/4) + 4*h + r%4 for query my_q.
+  __device__ __forceinline__ void scores(const uint8_t* ks_, f32x16 (&s)[2]) const {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = f32x16{};
-        const int row = kb * 32 + col;
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < kKSteps; ++kk) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(ks_ + k_off<D>(row, kk * 2 + h));
-          s[kb] = mfma_bf16(a, qreg[kk], s[kb]);
-        }
+      for (int kk = 0; kk < kKSteps; ++kk) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(ks_ + kb * 32 * (D * 2) + kaddr[kk]);
+        s[kb] = mfma_bf16(a, qreg[kk], s[kb]);
       }
-      // ---- mask and tile max on the raw scores (sm_scale > 0, so the max of
-      //      the scaled scores is the scaled max).  Register r of block kb
-      //      holds key k0 + 32*kb + 8*(r/4) + 4*h + r%4 for query my_q.
-      const bool need_mask = (k0 + BKV > S) || (causal && k0 + BKV - 1 > q0 + wave * 32);
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + kb * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-            if (key >= S || (causal && key > my_q)) s[kb][r] = -INFINITY;
-          }
-        }
-      }
-      float mt = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
-      // Lazy rescale: the reference point m_run only moves when the tile max
-      // exceeds it by more than kRescaleSlack (log2 units), so exp2 values stay
-      // below 2^kRescaleSlack and O / l are rescaled rarely.  The branch is
-      // wave-uniform (any lane that needs it).
-      const bool upd = mt > m_run + kRescaleSlack;
-      if (__builtin_amdgcn_ballot_w64(upd) != 0) {
-        const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
-        if (upd) m_run = mt;
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < kDBlocks; ++db) acc_o[db] *= alpha;
-      }
-      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
-      float rs = 0.f;
+    }
+  }
+
+  // Keys >= S and (causal) keys after the query score -inf.
+  __device__ __forceinline__ void mask(f32x16 (&s)[2], int k0) const {
+    const bool need_mask = (k0 + BKV > S) || (causal && k0 + BKV - 1 > q0 + wave * 32);
+    if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale_log2, neg_m));
-          s[kb][r] = e;
-          rs += e;
+          const int key = k0 + kb * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          if (key >= S || (causal && key > my_q)) s[kb][r] = -INFINITY;
         }
       }
-      rs += __shfl_xor(rs, 32, 64);
-      l_run += rs;
+    }
+  }
 
-      // ---- P^T operands: block kb, step u uses registers 8u..8u+7, i.e. keys
-      //      32kb + 16u + 4h + {0..3} and 32kb + 16u + 8 + 4h + {0..3}.
-      u32x4 pb[2][2];
+  // Tile max of the raw scores over both lane halves, times scale_log2
+  // (sm_scale > 0, so the max of the scaled scores is the scaled max).
+  __device__ __forceinline__ float tile_max(const f32x16 (&s)[2]) const {
+    float mt = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+    return fmaxf(mt, other_half(mt)) * scale_log2;
+  }
+
+  // Lazy rescale: the reference point m_run only moves when the tile max
+  // exceeds it by more than kRescaleSlack (log2 units), so exp2 values stay
+  // below 2^kRescaleSlack and O / l are rescaled rarely.  The branch is
+  // wave-uniform (any lane that needs it).
+  __device__ __forceinline__ void rebase(float mt) {
+    const bool upd = mt > m_run + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(upd) != 0) {
+      const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
+      if (upd) m_run = mt;
+      l_part *= alpha;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) acc_o[db] *= alpha;
+    }
+  }
+
+  // P^T operands: exp2(s * scale_log2 - m_run) rounded to bf16.  Block kb, step
+  // u uses registers 8u..8u+7, i.e. keys 32kb + 16u + 4h + {0..3} and
+  // 32kb + 16u + 8 + 4h + {0..3}.
+  __device__ __forceinline__ void probs(const f32x16 (&s)[2], u32x4 (&pb)[2][2]) {
+    const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * u + 2 * w], scale_log2, neg_m));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * u + 2 * w + 1], scale_log2, neg_m));
+          rs += e0;
+          rs += e1;
+          pb[kb][u][w] = pack_bf16(e0, e1);
+        }
+    l_part += rs;
+  }
+
+  // O^T += V^T P^T; V^T comes from transpose reads of the row-major V tile.
+  __device__ __forceinline__ void pv(const uint8_t* vs_, const u32x4 (&pb)[2][2]) {
+#pragma unroll
+    for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          pb[kb][u][0] = pack_bf16(s[kb][8 * u + 0], s[kb][8 * u + 1]);
-          pb[kb][u][1] = pack_bf16(s[kb][8 * u + 2], s[kb][8 * u + 3]);
-          pb[kb][u][2] = pack_bf16(s[kb][8 * u + 4], s[kb][8 * u + 5]);
-          pb[kb][u][3] = pack_bf16(s[kb][8 * u + 6], s[kb][8 * u + 7]);
-        }
-
-      // ---- O^T += V^T P^T.  ds_read_b64_tr_b16: in each 16-lane group, lane
-      //      4j+q addresses row (rowstart + j), columns 4q..4q+3 of the group's
-      //      16 columns; lane i of the group receives column i, rows rowstart..+3.
-      const int g_lane = lane & 15;
-      const int tr_row = g_lane >> 2;            // j
-      const int tr_col = ((lane >> 4) & 1) * 16 + (g_lane & 3) * 4;
-#pragma unroll
-      for (int db = 0; db < kDBlocks; ++db) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int r0 = kb * 32 + u * 16 + h * 4;
-            const int cc = db * 32 + tr_col;
-            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4*)(vs_ + v_off<D>(r0 + tr_row, cc)));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4*)(vs_ + v_off<D>(r0 + 8 + tr_row, cc)));
-            const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
-            const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
-            const u32x4 a = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
-            acc_o[db] = mfma_bf16(a, pb[kb][u], acc_o[db]);
-          }
+          const uint8_t* base = vs_ + (kb * 32 + u * 16) * (D * 2) + vaddr[db];
+          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(base));
+          const i16x4 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(base + 8 * (D * 2)));
+          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+          const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+          const u32x4 a = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+          acc_o[db] = mfma_bf16(a, pb[kb][u], acc_o[db]);
         }
       }
     }
   }
 };
+
+// One pipeline step for key tile j.  On entry LDS holds K_{j+1} (k_next) and
+// V_j (v_cur), and sc holds the masked scores of tile j with m_run already
+// rebased for them.  The step streams V_{j+1} and K_{j+2} into the stages freed
+// by the previous step, then overlaps the exp2 of tile j with the S^T MFMAs of
+// tile j+1, and the P.V MFMAs of tile j with the max of tile j+1.  kGuard
+// false (a clean step): tile j+1 exists, every wave is active for tiles j and
+// j+1, and tile j+1 needs no mask -- the caller guarantees it.
+template <int D, bool kGuard>
+__device__ __forceinline__ void fa_step(FaState<D>& st, int j, int n_tiles, uint8_t* k_load, uint8_t* v_load,
+                                        const uint8_t* k_next, const uint8_t* v_cur, f32x16 (&sc)[2],
+                                        f32x16 (&sn)[2]) {
+  const int k1 = (j + 1) * BKV;
+  const bool has_next = !kGuard || j + 1 < n_tiles;
+  const bool act = !kGuard || st.active(j * BKV);
+  const bool act_next = !kGuard || (has_next && st.active(k1));
+  if (has_next) st.template load_tile<true>(v_load, k1);
+  if (j + 2 < n_tiles) st.template load_tile<false>(k_load, k1 + BKV);
+  u32x4 pb[2][2];
+  if (act) st.probs(sc, pb);
+  if (act_next) st.scores(k_next, sn);
+  if (kGuard && act_next) st.mask(sn, k1);
+  if (act) st.pv(v_cur, pb);
+  const float mt = act_next ? st.tile_max(sn) : -INFINITY;
+  // a wave waits for its own loads and LDS reads only, then the workgroup
+  // meets (a plain s_barrier: __syncthreads' fence would drain more)
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+  if (act_next) st.rebase(mt);
+}
 
 template <int D>
 __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
@@ -254,10 +305,13 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   constexpr int kChunks = FaState<D>::kChunks;
   constexpr int kKSteps = FaState<D>::kKSteps;
   constexpr int kDBlocks = FaState<D>::kDBlocks;
-  // two LDS stages (K and V tile each) as distinct objects, so the compiler can
-  // tell that loads into one stage do not alias reads of the other
-  __shared__ __attribute__((aligned(16))) uint8_t stage0[2 * kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t stage1[2 * kTileBytes];
+  // K and V rings of two stages each, as distinct objects, so the compiler can
+  // tell that loads into one stage do not alias reads of another.  K runs one
+  // tile ahead of V.
+  __shared__ __attribute__((aligned(16))) uint8_t kst0[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t kst1[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vst0[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vst1[kTileBytes];
 
   FaState<D> st;
   const int tid = threadIdx.x;
@@ -299,56 +353,58 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   }
 #pragma unroll
   for (int i = 0; i < kDBlocks; ++i) st.acc_o[i] = f32x16{};
-  st.m_run = -INFINITY;  // reference point of the scaled scores (log2 domain), <= running max
-  st.l_run = 0.f;        // running sum of exp2(s*scale_log2 - m_run)
+  st.m_run = -INFINITY;
+  st.l_part = 0.f;
 
   int kv_end = S;
   if (p.causal) kv_end = min(S, q0 + BQ);
   const int n_tiles = (kv_end + BKV - 1) / BKV;
 
   st.init_loads(p.k + head_off, p.v + head_off);
-  st.issue_loads(stage0, stage0 + kTileBytes, 0);
+  st.template load_tile<false>(kst0, 0);
+  st.template load_tile<true>(vst0, 0);
+  if (n_tiles > 1) st.template load_tile<false>(kst1, BKV);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   asm volatile("s_barrier" ::: "memory");
-  // Tile t lives in stage t % 2; tile t+1 streams into the other stage while
-  // tile t is computed.  Before the barrier a wave waits for its own loads and
-  // its own LDS reads only (a plain s_barrier, not __syncthreads, whose fence
-  // would also drain unrelated counters).
-  int t = 0;
-  for (; t + 1 < n_tiles; t += 2) {
-    st.issue_loads(stage1, stage1 + kTileBytes, (t + 1) * BKV);
-    st.tile(stage0, stage0 + kTileBytes, t * BKV);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    asm volatile("s_barrier" ::: "memory");
-    if (t + 2 < n_tiles) st.issue_loads(stage0, stage0 + kTileBytes, (t + 2) * BKV);
-    st.tile(stage1, stage1 + kTileBytes, (t + 1) * BKV);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    asm volatile("s_barrier" ::: "memory");
+  f32x16 sa[2], sb[2];
+  st.scores(kst0, sa);  // tile 0 is active for every wave
+  st.mask(sa, 0);
+  st.rebase(st.tile_max(sa));
+  // Clean tiles need no mask and are active for every wave: all their keys are
+  // < S and, for causal, precede the block's first query q0.  Step j is clean
+  // when tile j+1 is; the clean steps run as pairs, the rest (at most four:
+  // n_tiles - n_clean <= 2) guarded.  Tile j lives in stage j % 2 of each ring.
+  const int n_clean = p.causal ? min(q0 / BKV, S / BKV) : S / BKV;
+  int j = 0;
+  for (; j + 2 < n_clean; j += 2) {
+    fa_step<D, false>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
+    fa_step<D, false>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
   }
-  if (t < n_tiles) {
-    st.tile(stage0, stage0 + kTileBytes, t * BKV);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    asm volatile("s_barrier" ::: "memory");
+  for (; j < n_tiles; j += 2) {
+    fa_step<D, true>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
+    if (j + 1 < n_tiles) fa_step<D, true>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
   }
-  const float m_run = st.m_run, l_run = st.l_run;
-  f32x16 (&acc_o)[kDBlocks] = st.acc_o;
-  uint8_t* smem = stage0;  // reused for the O transpose (the loop ended with a barrier)
 
-  // ---- epilogue: O = O^T / l, transposed through LDS into row-major bf16.
-  //      Lane holds query my_q and, for d block db and register r,
-  //      d = 32*db + 8*(r/4) + 4*h + r%4.
+  // ---- epilogue: O = O^T / l, transposed through LDS (the K ring, free after
+  //      the last step's barrier) into row-major bf16.  Lane holds query my_q
+  //      and, for d block db and register r, d = 32*db + 8*(r/4) + 4*h + r%4.
+  //      Rows 0..63 of the block go to kst0, rows 64..127 to kst1.
+  const float l_run = st.l_part + other_half(st.l_part);
+  const float m_run = st.m_run;
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
-  uint8_t* os_ = smem;  // [BQ][D] bf16, row stride D*2, chunk swizzle like K
+  {
+    uint8_t* os_ = wave < 2 ? kst0 : kst1;
+    const int row = (wave & 1) * 32 + col;
 #pragma unroll
-  for (int db = 0; db < kDBlocks; ++db) {
+    for (int db = 0; db < kDBlocks; ++db) {
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int d = db * 32 + rq * 8 + h * 4;
-      u32x2 w;
-      w[0] = pack_bf16(acc_o[db][rq * 4 + 0] * inv_l, acc_o[db][rq * 4 + 1] * inv_l);
-      w[1] = pack_bf16(acc_o[db][rq * 4 + 2] * inv_l, acc_o[db][rq * 4 + 3] * inv_l);
-      const int row = wave * 32 + col;
-      *reinterpret_cast<u32x2*>(os_ + k_off<D>(row, d >> 3) + (d & 7) * 2) = w;
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + rq * 8 + h * 4;
+        u32x2 w;
+        w[0] = pack_bf16(st.acc_o[db][rq * 4 + 0] * inv_l, st.acc_o[db][rq * 4 + 1] * inv_l);
+        w[1] = pack_bf16(st.acc_o[db][rq * 4 + 2] * inv_l, st.acc_o[db][rq * 4 + 3] * inv_l);
+        *reinterpret_cast<u32x2*>(os_ + k_off<D>(row, d >> 3) + (d & 7) * 2) = w;
+      }
     }
   }
   if (p.lse != nullptr && h == 0 && my_q < S) {
@@ -360,10 +416,11 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   for (int i = 0; i < BQ * kChunks / kThreads; ++i) {
     const int c = tid + kThreads * i;
     const int row = c / kChunks, ch = c % kChunks;
+    const uint8_t* os_ = row < 64 ? kst0 : kst1;
     const int q = q0 + row;
     if (q < S) {
       *reinterpret_cast<u32x4*>(Oh + static_cast<int64_t>(q) * D + ch * 8) =
-          *reinterpret_cast<const u32x4*>(os_ + k_off<D>(row, ch));
+          *reinterpret_cast<const u32x4*>(os_ + k_off<D>(row & 63, ch));
     }
   }
 }
