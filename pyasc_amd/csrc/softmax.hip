@@ -5,11 +5,16 @@
 // over the row's first L columns (row stride S).
 //
 // HBM-bound (one read + one write of every element).  Rows up to 8192 columns
-// stay in registers: a wave per row up to 1024 columns, a 256-thread block per
-// row above that (measured faster at 4096 columns than a wave per row).  Max and sum reduce in-thread, then by wave butterfly
-// (__shfl_xor), then across waves through LDS.  exp is the accurate libm expf
-// and the normalisation is a true division, as the reference's DivL2
-// (lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116).
+// stay in registers: a wave per row (two rows per wave) up to 1024 columns, a
+// 128-thread block per row up to 4096 (measured faster there than one wave or
+// four waves per row), 256 threads above.  Max, min and sum reduce in-thread,
+// then across the wave with DPP and permlane swaps (no LDS round trips), then
+// across waves through LDS.  x - max is rounded to fp32 as in the reference
+// (test_softmax.py:22-24); exp of it is accurate to ~2 ulp (the row's min picks
+// a shorter exp when no result can fall below 2^-126) and the
+// normalisation multiplies by one correctly rounded reciprocal per row, which
+// stays within 2 ulp of the reference's true division (DivL2,
+// lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116).
 #include <math.h>
 
 #include "common.h"
@@ -55,14 +60,120 @@ __device__ __forceinline__ void store_vec(float* row, int q, int len, bool vec_o
   if (e + 3 < len) row[e + 3] = v.w;
 }
 
-// exp(v - m) with masked (-inf) lanes giving exactly 0.
+constexpr float kL2E = 1.44269504088896340736f;   // log2(e) rounded to fp32
+constexpr float kL2ELo = 1.925963033500011e-08f;  // log2(e) - kL2E
+constexpr float kLn2 = 0.69314718055994530942f;
+constexpr float kMinNormalLog2 = -126.0f;
+
+// Vectors q0 + kStride*j (j < N) of a row, where q0 < kStride is the thread's
+// index in its group.  The test that a vector lies inside the row for every
+// thread of the group depends on kernel arguments only (uniform branch), so
+// full vectors are plain 16-byte loads issued back to back; only a ragged
+// tail takes the per-lane path.  (A per-lane choice between the two load
+// forms would run both and serialise the loads on their shared registers.)
+template <int N, int kStride>
+__device__ __forceinline__ void load_row(float4 (&v)[N], const float* row, int q0, int len, bool vec_ok) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int q = q0 + kStride * j;
+    if (vec_ok && kStride * (j + 1) * 4 <= len) {
+      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row) + q);
+      v[j] = make_float4(t.x, t.y, t.z, t.w);
+    } else {
+      v[j] = load_vec(row, q, len, vec_ok);
+    }
+  }
+}
+
+template <int N, int kStride>
+__device__ __forceinline__ void store_row(const float4 (&v)[N], float* row, int q0, int len, bool vec_ok, float rs) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int q = q0 + kStride * j;
+    const float4 o = make_float4(v[j].x * rs, v[j].y * rs, v[j].z * rs, v[j].w * rs);
+    if (vec_ok && kStride * (j + 1) * 4 <= len) {
+      __builtin_nontemporal_store(f32x4{o.x, o.y, o.z, o.w}, reinterpret_cast<f32x4*>(row) + q);
+    } else {
+      store_vec(row, q, len, vec_ok, o);
+    }
+  }
+}
+
+// exp(y) for finite y <= 0 with y*log2(e) >= -126 (the caller checks the row's
+// range), within ~2 ulp: t = y*log2(e) rounded, v_exp_f32 of t, and a
+// first-order correction by the rounding residual, taken from a two-term split
+// of log2(e) (Cody-Waite).
+__device__ __forceinline__ float exp_plain(float y) {
+  const float t = y * kL2E;
+  const float err = fmaf(y, kL2ELo, fmaf(y, kL2E, -t));
+  const float e = __builtin_amdgcn_exp2f(t);
+  return fmaf(e, err * kLn2, e);
+}
+
+// exp(y) for any y <= 0 (-inf gives 0, NaN stays NaN).  v_exp_f32 flushes
+// results below 2^-126, so those are evaluated 64 octaves up (t + 64 is exact
+// for t <= -126) and scaled back by an exact power of two, which rounds once
+// into the denormal range.
+__device__ __forceinline__ float exp_nonpos(float y) {
+  const float t = y * kL2E;
+  const float yc = fmaxf(y, -104.0f);  // keeps the residual finite for y = -inf
+  const float err = fmaf(yc, kL2ELo, fmaf(yc, kL2E, -(yc * kL2E)));
+  const bool tiny = t < kMinNormalLog2;
+  const float e = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t);
+  const float r = fmaf(e, err * kLn2, e);
+  return tiny ? r * 0x1p-64f : r;
+}
+
+// True when every exp(x - m) of a row with maximum m and minimum mn is a
+// normal number reached by exp_plain: RN(RN(mn - m) * log2 e) >= -126 bounds
+// RN(RN(x - m) * log2 e) for every x of the row (rounding is monotonic).
+// mn = -inf (a -inf element or padding) selects the general path.
+__device__ __forceinline__ bool plain_range(float m, float mn) { return (mn - m) * kL2E >= kMinNormalLog2; }
+
+// exp(v - m) per lane of a vector
+template <bool kPlain>
 __device__ __forceinline__ float4 exp_shift(float4 v, float m) {
   float4 r;
-  r.x = expf(v.x - m);
-  r.y = expf(v.y - m);
-  r.z = expf(v.z - m);
-  r.w = expf(v.w - m);
+  if constexpr (kPlain) {
+    r.x = exp_plain(v.x - m);
+    r.y = exp_plain(v.y - m);
+    r.z = exp_plain(v.z - m);
+    r.w = exp_plain(v.w - m);
+  } else {
+    r.x = exp_nonpos(v.x - m);
+    r.y = exp_nonpos(v.y - m);
+    r.z = exp_nonpos(v.z - m);
+    r.w = exp_nonpos(v.w - m);
+  }
   return r;
+}
+
+__device__ __forceinline__ float max4(float4 v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
+__device__ __forceinline__ float min4(float4 v) { return fminf(fminf(v.x, v.y), fminf(v.z, v.w)); }
+
+// Replaces the vectors of one row by exp(v - m) and returns their sum.  One
+// vector at a time (scheduling fence): with many waves per SIMD resident,
+// overlapping the exps of several vectors buys nothing and its temporaries
+// would cost occupancy.
+template <int N>
+__device__ __forceinline__ float exp_row(float4 (&v)[N], float m, float mn) {
+  float s = 0.f;
+  if (plain_range(m, mn)) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      v[j] = exp_shift<true>(v[j], m);
+      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      v[j] = exp_shift<false>(v[j], m);
+      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  return s;
 }
 
 // One wave per row; each lane holds VPL float4 vectors of each of kRows rows
@@ -75,117 +186,100 @@ __global__ void __launch_bounds__(256) softmax_wave_kernel(RowView p) {
 #pragma unroll
   for (int k = 0; k < kRows; ++k) {
     if (r0 + k >= p.rows) continue;
-    const float* row = p.x + (r0 + k) * p.stride;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) v[k][j] = load_vec(row, lane + 64 * j, p.len, p.vec_ok);
+    load_row<VPL, 64>(v[k], p.x + (r0 + k) * p.stride, lane, p.len, p.vec_ok);
   }
 #pragma unroll
   for (int k = 0; k < kRows; ++k) {
     if (r0 + k >= p.rows) continue;
-    float m = -INFINITY;
+    float m = -INFINITY, mn = INFINITY;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) m = fmaxf(m, fmaxf(fmaxf(v[k][j].x, v[k][j].y), fmaxf(v[k][j].z, v[k][j].w)));
+    for (int j = 0; j < VPL; ++j) {
+      m = fmaxf(m, max4(v[k][j]));
+      mn = fminf(mn, min4(v[k][j]));
+    }
     m = asc::wave_max(m);
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      v[k][j] = exp_shift(v[k][j], m);
-      s += (v[k][j].x + v[k][j].y) + (v[k][j].z + v[k][j].w);
-    }
-    s = asc::wave_sum(s);
-    float* orow = p.out + (r0 + k) * p.stride;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      float4 o = make_float4(v[k][j].x / s, v[k][j].y / s, v[k][j].z / s, v[k][j].w / s);
-      store_vec(orow, lane + 64 * j, p.len, p.vec_ok, o);
-    }
+    mn = asc::wave_min(mn);
+    const float rs = 1.0f / asc::wave_sum(exp_row(v[k], m, mn));
+    store_row<VPL, 64>(v[k], p.out + (r0 + k) * p.stride, lane, p.len, p.vec_ok, rs);
   }
 }
 
-// One 256-thread block per kRows rows; each thread holds VPT float4 vectors of
-// each row.  All rows are loaded first; the cross-wave max and sum of all rows
-// share one barrier each.
-template <int VPT, int kRows>
-__global__ void __launch_bounds__(256) softmax_block_kernel(RowView p) {
-  constexpr int kWaves = 256 / 64;
-  __shared__ float red[2][kRows][kWaves];
+// One kThreads-thread block per row; each thread holds VPT float4 vectors.
+// The cross-wave max/min and sum go through LDS, one barrier each.
+template <int VPT, int kThreads>
+__global__ void __launch_bounds__(kThreads) softmax_block_kernel(RowView p) {
+  constexpr int kWaves = kThreads / 64;
+  __shared__ float red[3][kWaves];  // max, min, sum per wave
   const int t = threadIdx.x;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
-  float4 v[kRows][VPT];
-  float m[kRows], s[kRows];
+  const int64_t r = blockIdx.x;
+  float4 v[VPT];
+  load_row<VPT, kThreads>(v, p.x + r * p.stride, t, p.len, p.vec_ok);
+  float m = -INFINITY, mn = INFINITY;
 #pragma unroll
-  for (int k = 0; k < kRows; ++k) {
-    const bool live = r0 + k < p.rows;
-    const float* row = p.x + (live ? r0 + k : r0) * p.stride;
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) v[k][j] = load_vec(row, t + 256 * j, live ? p.len : 0, p.vec_ok);
+  for (int j = 0; j < VPT; ++j) {
+    m = fmaxf(m, max4(v[j]));
+    mn = fminf(mn, min4(v[j]));
   }
-#pragma unroll
-  for (int k = 0; k < kRows; ++k) {
-    m[k] = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      m[k] = fmaxf(m[k], fmaxf(fmaxf(v[k][j].x, v[k][j].y), fmaxf(v[k][j].z, v[k][j].w)));
-    m[k] = asc::wave_max(m[k]);
-    if ((t & 63) == 0) red[0][k][t >> 6] = m[k];
+  m = asc::wave_max(m);
+  mn = asc::wave_min(mn);
+  if ((t & 63) == 0) {
+    red[0][t >> 6] = m;
+    red[1][t >> 6] = mn;
   }
   __syncthreads();
+  m = red[0][0];
+  mn = red[1][0];
 #pragma unroll
-  for (int k = 0; k < kRows; ++k) {
-    m[k] = fmaxf(fmaxf(red[0][k][0], red[0][k][1]), fmaxf(red[0][k][2], red[0][k][3]));
-    s[k] = 0.f;
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      v[k][j] = exp_shift(v[k][j], m[k]);
-      s[k] += (v[k][j].x + v[k][j].y) + (v[k][j].z + v[k][j].w);
-    }
-    s[k] = asc::wave_sum(s[k]);
-    if ((t & 63) == 0) red[1][k][t >> 6] = s[k];
+  for (int w = 1; w < kWaves; ++w) {
+    m = fmaxf(m, red[0][w]);
+    mn = fminf(mn, red[1][w]);
   }
+  const float s = asc::wave_sum(exp_row(v, m, mn));
+  if ((t & 63) == 0) red[2][t >> 6] = s;
   __syncthreads();
+  float sum = red[2][0];
 #pragma unroll
-  for (int k = 0; k < kRows; ++k) {
-    if (r0 + k >= p.rows) continue;
-    const float sum = (red[1][k][0] + red[1][k][1]) + (red[1][k][2] + red[1][k][3]);
-    float* orow = p.out + (r0 + k) * p.stride;
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      float4 o = make_float4(v[k][j].x / sum, v[k][j].y / sum, v[k][j].z / sum, v[k][j].w / sum);
-      store_vec(orow, t + 256 * j, p.len, p.vec_ok, o);
-    }
-  }
+  for (int w = 1; w < kWaves; ++w) sum += red[2][w];
+  store_row<VPT, kThreads>(v, p.out + r * p.stride, t, p.len, p.vec_ok, 1.0f / sum);
 }
 
 // Rows longer than the register-resident variants: three passes over the row.
 __global__ void __launch_bounds__(256) softmax_long_kernel(RowView p) {
   constexpr int kWaves = 256 / 64;
-  __shared__ float red[2][kWaves];
+  __shared__ float red[3][kWaves];
   const int t = threadIdx.x;
   const int64_t r = blockIdx.x;
   const float* row = p.x + r * p.stride;
   const int nvec = (p.len + 3) / 4;
-  float m = -INFINITY;
+  float m = -INFINITY, mn = INFINITY;
   for (int q = t; q < nvec; q += 256) {
-    float4 v = load_vec(row, q, p.len, p.vec_ok);
-    m = fmaxf(m, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    const float4 v = load_vec(row, q, p.len, p.vec_ok);
+    m = fmaxf(m, max4(v));
+    mn = fminf(mn, min4(v));
   }
   m = asc::wave_max(m);
-  if ((t & 63) == 0) red[0][t >> 6] = m;
+  mn = asc::wave_min(mn);
+  if ((t & 63) == 0) {
+    red[0][t >> 6] = m;
+    red[1][t >> 6] = mn;
+  }
   __syncthreads();
   m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  mn = fminf(fminf(red[1][0], red[1][1]), fminf(red[1][2], red[1][3]));
   float s = 0.f;
   for (int q = t; q < nvec; q += 256) {
-    float4 v = exp_shift(load_vec(row, q, p.len, p.vec_ok), m);
-    s += (v.x + v.y) + (v.z + v.w);
+    float4 v[1] = {load_vec(row, q, p.len, p.vec_ok)};
+    s += exp_row(v, m, mn);
   }
   s = asc::wave_sum(s);
-  if ((t & 63) == 0) red[1][t >> 6] = s;
+  if ((t & 63) == 0) red[2][t >> 6] = s;
   __syncthreads();
-  s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  const float rs = 1.0f / ((red[2][0] + red[2][1]) + (red[2][2] + red[2][3]));
   float* orow = p.out + r * p.stride;
   for (int q = t; q < nvec; q += 256) {
-    float4 v = exp_shift(load_vec(row, q, p.len, p.vec_ok), m);
-    store_vec(orow, q, p.len, p.vec_ok, make_float4(v.x / s, v.y / s, v.z / s, v.w / s));
+    float4 v[1] = {load_vec(row, q, p.len, p.vec_ok)};
+    exp_row(v, m, mn);
+    store_vec(orow, q, p.len, p.vec_ok, make_float4(v[0].x * rs, v[0].y * rs, v[0].z * rs, v[0].w * rs));
   }
 }
 
@@ -202,13 +296,13 @@ int32_t launch_rows(const RowView& p, hipStream_t stream, const char* who) {
   } else if (L <= 1024) {
     hipLaunchKernelGGL((softmax_wave_kernel<4, 2>), wave_grid, block, 0, stream, p);
   } else if (L <= 2048) {
-    hipLaunchKernelGGL((softmax_block_kernel<2, 1>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_block_kernel<4, 128>), dim3(static_cast<uint32_t>(p.rows)), dim3(128), 0, stream, p);
   } else if (L <= 4096) {
-    // one row per block measured fastest here (2 rows per block, or persistent
-    // blocks streaming rows, lose occupancy or add a launch round)
-    hipLaunchKernelGGL((softmax_block_kernel<4, 1>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
+    // two waves per row: 32 values per lane keep 8 waves per SIMD resident, so
+    // a 4096-row launch is in flight at once
+    hipLaunchKernelGGL((softmax_block_kernel<8, 128>), dim3(static_cast<uint32_t>(p.rows)), dim3(128), 0, stream, p);
   } else if (L <= 8192) {
-    hipLaunchKernelGGL((softmax_block_kernel<8, 1>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
+    hipLaunchKernelGGL((softmax_block_kernel<8, 256>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else {
     hipLaunchKernelGGL(softmax_long_kernel, dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   }
