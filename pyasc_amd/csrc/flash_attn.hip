@@ -322,13 +322,24 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   st.h = lane >> 5;    // lane half
   const int wave = st.wave, col = st.col, h = st.h;
 
-  // Block order: query-block major, all (batch, head) of one query block
-  // together; causal runs the heavy (late) query blocks first.  (Block b lands
-  // on XCD b % 8, so all query blocks of a head share one XCD.  A head-major
-  // order measured no faster non-causal and slower causal.)
+  // Block order.  Workgroup b runs on XCD b % 8, and each XCD starts its
+  // workgroups in order of b / 8.  When the (batch, head) count divides by 8,
+  // XCD x takes heads x, x+8, x+16, ... and runs all query blocks of one head
+  // back to back, so the workgroups resident on an XCD at once stream the same
+  // head's K/V through that XCD's L2 (fetched from HBM about once per head,
+  // instead of once per round of resident query blocks).  Otherwise: query-block
+  // major.  Causal runs a head's heavy (late) query blocks first.
   const int64_t bid = blockIdx.x;
-  const int64_t bh = bid % p.heads_total;
-  int qb = static_cast<int>(bid / p.heads_total);
+  int64_t bh;
+  int qb;
+  if (p.heads_total % 8 == 0) {
+    const int64_t slot = bid >> 3;
+    bh = (bid & 7) + 8 * (slot / p.n_qblocks);
+    qb = static_cast<int>(slot % p.n_qblocks);
+  } else {
+    bh = bid % p.heads_total;
+    qb = static_cast<int>(bid / p.heads_total);
+  }
   if (p.causal) qb = p.n_qblocks - 1 - qb;
   const int q0 = qb * BQ;
   const int S = p.seq;
