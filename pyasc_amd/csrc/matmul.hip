@@ -3,18 +3,17 @@
 // python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py).
 //
 // fp16/bf16 inputs run on MFMA (v_mfma_f32_32x32x16_{bf16,f16}) with fp32
-// accumulation:
-//   - 256x256 output tile per 256-thread workgroup, 4 waves in 2x2, each wave
-//     owns 128x128 = 4x4 MFMA blocks (256 fp32 accumulators per lane);
-//   - K advances 64 at a time through two LDS stages (2 x 64 KiB) in the
-//     software-pipelined main loop of gemm_core.h;
-//   - A (row-major, K contiguous) is copied as is; B (row-major, N contiguous)
-//     is transposed in registers (8x8 blocks of 16-bit, v_perm_b32) so both LDS
-//     tiles are K-contiguous and every MFMA operand is one ds_read_b128;
+// accumulation, 256x256 output tile per 256-thread workgroup, 4 waves in 2x2,
+// each wave 128x128 = 4x4 MFMA blocks (256 fp32 accumulators per lane):
+//   - tile-aligned shapes (M, N multiples of 256, K of 32, offsets within
+//     32 bits): the direct-to-LDS loop of gemm_direct.h -- operands go from HBM
+//     straight into four 32 KiB LDS stages, B stays row-major and its
+//     K-contiguous MFMA operand comes from LDS transpose reads;
+//   - other shapes: the register-staged loop of gemm_core.h with bounds-checked
+//     loads (zero fill), B transposed in registers, masked stores;
 //   - XCD-aware, grouped tile order (gemm_common.h).
 // The epilogue applies the fixpipe relu and the RNE cast to fp16/bf16, or
-// stores fp32 as is.  Shapes that are not multiples of the tile run the same
-// kernel with bounds-checked loads (zero fill) and masked stores.
+// stores fp32 as is.
 //
 // fp32 inputs (test_matmul_fixpipe.py's float32 case) use a plain LDS-tiled
 // FMA kernel.

@@ -3,12 +3,13 @@
 // (python/test/generalization/adv/test_matmul_quant.py:23-51,94-106;
 //  lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:116-117).
 //
-// Same pipelined main loop as the fp16/bf16 kernel (gemm_core.h) on
-// v_mfma_i32_32x32x32_i8: 256x256 output tile, 4 waves of 128x128, K advancing
-// 128 bytes per LDS stage, B transposed in registers as 16(k) x 8(n) byte blocks
-// (64 v_perm_b32 per block).  The epilogue either stores the
-// int32 accumulators or out = fp16_rne(fp32_rne(acc) * s[n]) with s[n] the
-// fp32 scale (optionally with its low 13 mantissa bits cleared, the reference
+// Same structure as the fp16/bf16 kernel on v_mfma_i32_32x32x32_i8: 256x256
+// output tile, 4 waves of 128x128; tile-aligned shapes take the direct-to-LDS
+// loop of gemm_direct.h (64-byte k-tiles, B read with ds_read_b64_tr_b8),
+// others the register-staged loop of gemm_core.h (B transposed in registers as
+// 16(k) x 8(n) byte blocks).  The epilogue either stores the int32
+// accumulators or out = fp16_rne(fp32_rne(acc) * s[n]) with s[n] the fp32
+// scale (optionally with its low 13 mantissa bits cleared, the reference
 // golden's trunc-19 form).
 #include "common.h"
 #include "gemm_common.h"
