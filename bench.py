@@ -154,6 +154,121 @@ class Vadd(Workload):
                 "kind": "port", "sample": f"x + y on {n} fp32 elements (README.md:53)", "seconds_per_call": secs}
 
 
+class LeakyRelu(Workload):
+    """test_leaky_relu.py's kernel at a bandwidth size: bf16, alpha a 0-dim bf16 tensor (0.1)."""
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "bf16", "map_vec_kernel"
+
+    def __init__(self, n: int):
+        self.n = n
+        self.name = f"leaky_relu_{n}_bf16"
+
+    def setup(self, dev):
+        import torch
+        g = torch.Generator(device=dev).manual_seed(0)
+        self.sets = [((torch.rand(self.n, device=dev, generator=g) * 10.0 - 5.0).to(torch.bfloat16),
+                      torch.empty(self.n, device=dev, dtype=torch.bfloat16)) for _ in range(_sets_for(4 * self.n))]
+        self.alpha = float(torch.tensor(0.1, dtype=torch.bfloat16).item())
+        self.tpb = ((self.n + 127) // 128 + 15) // 16  # leaky_relu_launch (test_leaky_relu.py:29-37)
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        x, out = self.sets[i % len(self.sets)]
+        kernels.leaky_relu(x, self.alpha, out, self.n, 128, self.tpb, 16)
+
+    def work(self) -> float:
+        return 4.0 * self.n
+
+    def config(self) -> dict:
+        return {"workload": self.name, "size": self.n, "tile_size": 128, "tile_per_block": self.tpb, "grid": 16,
+                "alpha": "bf16 0.1", "input": "rand*10-5 bf16", "rotating_sets": len(self.sets)}
+
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        n = min(self.n, 1 << 26)
+        x = torch.rand(n).to(torch.bfloat16) * 10.0 - 5.0
+        alpha = torch.tensor(0.1, dtype=torch.bfloat16)
+        secs = _time_cpu(lambda: cpu_golden.leaky_relu(x, alpha), budget_s=10.0)
+        return {"value": round(4.0 * n / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port", "sample": f"torch.where(x >= 0, x, x * alpha) on {n} bf16 elements "
+                "(test_leaky_relu.py:47)", "seconds_per_call": secs}
+
+
+class VMulAdd(Workload):
+    """test_vmuladd.py's kernel at a bandwidth size (fp32, tile 32 as in vmuladd_launch)."""
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "map_vec_kernel"
+
+    def __init__(self, n: int):
+        self.n = n
+        self.name = f"vmuladd_{n}_f32"
+
+    def setup(self, dev):
+        import torch
+        self.sets = [tuple(torch.rand(self.n, device=dev) * 10 for _ in range(3)) + (torch.empty(self.n, device=dev),)
+                     for _ in range(_sets_for(16 * self.n))]
+        self.tpb = ((self.n + 31) // 32 + 15) // 16  # vmuladd_launch (test_vmuladd.py:34-40)
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        x, y, z, out = self.sets[i % len(self.sets)]
+        kernels.vmuladd(x, y, z, out, self.n, 32, self.tpb, 16)
+
+    def work(self) -> float:
+        return 16.0 * self.n
+
+    def config(self) -> dict:
+        return {"workload": self.name, "size": self.n, "tile_size": 32, "tile_per_block": self.tpb, "grid": 16,
+                "input": "rand*10 fp32", "rotating_sets": len(self.sets)}
+
+    def cpu_baseline(self):
+        import numpy as np
+        import torch
+        from oracle import cpu_golden
+        n = min(self.n, 1 << 25)
+        rng = np.random.default_rng(seed=2026)
+        x, y, z = (rng.random(n, dtype=np.float32) * 10 for _ in range(3))
+        secs = _time_cpu(lambda: cpu_golden.vmuladd(x, y, z), budget_s=10.0)
+        return {"value": round(16.0 * n / secs / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"numpy x * y + z on {n} fp32 elements (test_vmuladd.py:52)", "seconds_per_call": secs}
+
+
+class Gelu(Workload):
+    """test_gelu.py's kernel at softmax's second shape (fp32 rows, tile = row length)."""
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "gelu_rows_kernel"
+
+    def __init__(self, rows: int, cols: int, approximate: bool):
+        self.rows, self.cols, self.approximate = rows, cols, approximate
+        self.name = f"gelu_{'tanh' if approximate else 'erf'}_{rows}x{cols}_f32"
+
+    def setup(self, dev):
+        import torch
+        g = torch.Generator(device=dev).manual_seed(1)
+        self.sets = [(torch.randn(self.rows, self.cols, device=dev, generator=g) * 2.0,
+                      torch.empty(self.rows, self.cols, device=dev))
+                     for _ in range(_sets_for(8 * self.rows * self.cols))]
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        x, out = self.sets[i % len(self.sets)]
+        kernels.gelu_rows(x, out, self.rows, self.cols, self.cols, self.approximate, 16)
+
+    def work(self) -> float:
+        return 8.0 * self.rows * self.cols
+
+    def config(self) -> dict:
+        return {"workload": self.name, "rows": self.rows, "cols": self.cols, "tile_size": self.cols, "grid": 16,
+                "approximate": self.approximate, "input": "randn*2 fp32", "rotating_sets": len(self.sets)}
+
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        x = torch.randn(self.rows, self.cols) * 2.0
+        secs = _time_cpu(lambda: cpu_golden.gelu(x, self.approximate), budget_s=10.0)
+        return {"value": round(self.work() / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port", "sample": f"test_gelu.py:44-48 golden on the full {self.rows}x{self.cols} input",
+                "seconds_per_call": secs}
+
+
 class Matmul(Workload):
     bound, unit, kernel_hint = "mfma", "TFLOP/s", "gemm_mfma"
 
@@ -250,10 +365,15 @@ WORKLOADS = {
     "matmul_i8_4096x11008x4096": lambda: MatmulI8(4096, 11008, 4096),
     "fa_fwd_noncausal": lambda: FlashAttention(4, 32, 4096, 128, False),
     "fa_fwd_causal": lambda: FlashAttention(4, 32, 4096, 128, True),
+    "leaky_relu_268435456": lambda: LeakyRelu(1 << 28),
+    "vmuladd_268435456": lambda: VMulAdd(1 << 28),
+    "gelu_tanh_16384x1024": lambda: Gelu(16384, 1024, True),
+    "gelu_erf_16384x1024": lambda: Gelu(16384, 1024, False),
 }
 HEADLINE = "softmax_4096x4096"
 SUITE = ["softmax_16384x1024", "vadd_268435456", "matmul_bf16_8192", "matmul_f16_8192", "matmul_i8_4096x11008x4096",
-         "fa_fwd_noncausal", "fa_fwd_causal"]
+         "fa_fwd_noncausal", "fa_fwd_causal", "leaky_relu_268435456", "vmuladd_268435456", "gelu_tanh_16384x1024",
+         "gelu_erf_16384x1024"]
 
 
 def _time_cpu(fn, budget_s: float) -> float:

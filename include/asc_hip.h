@@ -81,6 +81,42 @@ int32_t asc_vadd(int32_t dtype, const void* x, const void* y, void* out,
                  int64_t size, int32_t tile_size, int32_t tile_per_block,
                  int32_t grid, asc_stream_t stream);
 
+/* ---- leaky_relu / vmuladd ------------------------------------------------------
+ * asc2 leaky_relu_kernel(x_ptr, alpha: float, out_ptr, size: int,
+ *                        tile_size: ConstExpr[int], tile_per_block: ConstExpr[int])
+ *   python/test/asc2/kernels/test_leaky_relu.py:16-26:
+ *   out = where(x >= 0, x, x * alpha); x * alpha is formed in fp32 and rounded
+ *   once to the element type (RNE).
+ * asc2 vmuladd_kernel(x_ptr, y_ptr, z_ptr, out_ptr, size: int,
+ *                     tile_size: ConstExpr[int], tile_per_block: ConstExpr[int],
+ *                     buffer_factor: ConstExpr[int])
+ *   python/test/asc2/kernels/test_vmuladd.py:16-31:
+ *   out = x * y + z, the product rounded to the element type before the add
+ *   (no fused multiply-add).
+ * Coverage as vadd: out[j] for j < min(size, grid*tpb*tile); the rest of out is
+ * untouched.  dtype: ASC_DT_FLOAT32 / FLOAT16 / BFLOAT16. */
+int32_t asc_leaky_relu(int32_t dtype, const void* x, float alpha, void* out,
+                       int64_t size, int32_t tile_size, int32_t tile_per_block,
+                       int32_t grid, asc_stream_t stream);
+int32_t asc_vmuladd(int32_t dtype, const void* x, const void* y, const void* z,
+                    void* out, int64_t size, int32_t tile_size,
+                    int32_t tile_per_block, int32_t grid, asc_stream_t stream);
+
+/* ---- gelu ---------------------------------------------------------------------
+ * asc2 gelu_kernel(x_ptr, out_ptr, num_rows: ConstExpr, num_columns: ConstExpr,
+ *                  tile_size: ConstExpr, approximate: ConstExpr)
+ *   python/test/asc2/kernels/test_gelu.py:19-33.
+ * fp32 [num_rows, num_cols]; each row's first tile_size columns get
+ *   approximate != 0: x - x / (exp(x * (x*x*k2 + k1)) + 1),
+ *                     k1 = 2*sqrt(2/pi), k2 = k1 * 0.044715
+ *   approximate == 0: x * (erf(x * sqrt(0.5)) + 1) * 0.5
+ * (the reference body's expressions and order).  tile_size must be <=
+ * num_cols (ASC_ERR_UNSUPPORTED otherwise, as for the row softmax). */
+int32_t asc_gelu_rows_f32(const float* x, float* out, int64_t num_rows,
+                          int64_t num_cols, int32_t tile_size,
+                          int32_t approximate, int32_t grid,
+                          asc_stream_t stream);
+
 /* ---- row softmax -----------------------------------------------------------
  * asc2 softmax_kernel(x_ptr, out_ptr, num_rows: int, num_cols: int,
  *                     tile_size: ConstExpr[int])

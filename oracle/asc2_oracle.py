@@ -20,6 +20,14 @@ How each function is pinned (tests/test_oracle.py):
                   (gen_golden) where |acc| <= 2048.
   attention       causal row 0 == v[0], q = 0 -> (prefix) means of v, torch's
                   scaled_dot_product_attention in fp32.
+  leaky_relu      a literal per-element loop of the kernel body, sign / -0 / NaN
+                  known answers, torch.where(x >= 0, x, x * alpha) in bfloat16
+                  (the reference's golden).
+  vmuladd         per-element fp32 known answers (rounding of the product shows),
+                  numpy's unfused x * y + z (the reference's golden), torch float16
+                  / bfloat16 mul-then-add.
+  gelu            torch.nn.functional.gelu in float64 (both forms; same function,
+                  different expression), gelu(0) = 0, gelu(x) - gelu(-x) = x.
 Every function here has at least one such check; none is "parity unpinned".
 """
 from __future__ import annotations
@@ -70,6 +78,80 @@ def vadd(x: np.ndarray, y: np.ndarray, out: np.ndarray, size: int, tile_size: in
     res = out.copy()
     n = vadd_covered(size, tile_size, tile_per_block, grid)
     res[:n] = add_elements(x[:n], y[:n], dtype)
+    return res
+
+
+# -------------------------------------------------------------------------- leaky_relu / vmuladd / gelu
+
+def _to_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    return bf16_bits_to_f32(x) if dtype == "bfloat16" else np.asarray(x).astype(np.float32)
+
+
+def _from_f32(v: np.ndarray, dtype: str) -> np.ndarray:
+    """RNE from float32 to the element type (bfloat16 as uint16 bit patterns)."""
+    if dtype == "bfloat16":
+        return f32_to_bf16_bits(v)
+    return np.asarray(v, dtype=np.float32).astype(np.float16 if dtype == "float16" else np.float32)
+
+
+def leaky_relu_elements(x: np.ndarray, alpha: float, dtype: str) -> np.ndarray:
+    """python/test/asc2/kernels/test_leaky_relu.py:24 ``where(x >= 0, x, x * alpha)``: the
+    product in float32, rounded once to the element type; x >= 0 (also -0) passes unchanged."""
+    xf = _to_f32(x, dtype)
+    with np.errstate(over="ignore", invalid="ignore"):
+        prod = _from_f32(xf * np.float32(alpha), dtype)
+    return np.where(xf >= 0, x, prod)
+
+
+def leaky_relu(x: np.ndarray, alpha: float, out: np.ndarray, size: int, tile_size: int, tile_per_block: int,
+               grid: int, dtype: str = "float32") -> np.ndarray:
+    """test_leaky_relu.py:16-26: vadd-style tiles, coverage [0, min(size, grid*tpb*tile))."""
+    res = out.copy()
+    n = vadd_covered(size, tile_size, tile_per_block, grid)
+    res[:n] = leaky_relu_elements(x[:n], alpha, dtype)
+    return res
+
+
+def muladd_elements(x: np.ndarray, y: np.ndarray, z: np.ndarray, dtype: str) -> np.ndarray:
+    """python/test/asc2/kernels/test_vmuladd.py:29 ``x * y + z``: two tile ops, each rounded to
+    the element type (the golden at :52 is numpy's unfused ``x * y + z``)."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        prod = _from_f32(_to_f32(x, dtype) * _to_f32(y, dtype), dtype)
+        return _from_f32(_to_f32(prod, dtype) + _to_f32(z, dtype), dtype)
+
+
+def vmuladd(x: np.ndarray, y: np.ndarray, z: np.ndarray, out: np.ndarray, size: int, tile_size: int,
+            tile_per_block: int, grid: int, dtype: str = "float32") -> np.ndarray:
+    """test_vmuladd.py:16-31: vadd-style tiles, coverage [0, min(size, grid*tpb*tile))."""
+    res = out.copy()
+    n = vadd_covered(size, tile_size, tile_per_block, grid)
+    res[:n] = muladd_elements(x[:n], y[:n], z[:n], dtype)
+    return res
+
+
+def gelu_values(x: np.ndarray, approximate: bool) -> np.ndarray:
+    """python/test/asc2/kernels/test_gelu.py:24-31 in float64 on float32 inputs:
+    tanh form x - x / (exp(x*(x*x*k2 + k1)) + 1) with k1 = 2*sqrt(2/pi), k2 = k1*0.044715;
+    erf form x * (erf(x*sqrt(0.5)) + 1) * 0.5."""
+    xd = np.asarray(x, dtype=np.float32).astype(np.float64)
+    if approximate:
+        k1 = 2.0 * np.sqrt(2.0 / np.pi)
+        k2 = k1 * 0.044715
+        with np.errstate(over="ignore"):
+            return xd - xd / (np.exp(xd * (xd * xd * k2 + k1)) + 1.0)
+    from scipy.special import erf
+    return xd * (erf(xd * np.sqrt(0.5)) + 1.0) * 0.5
+
+
+def gelu_rows(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, tile_size: int,
+              approximate: bool) -> np.ndarray:
+    """test_gelu.py:19-33: every row's first ``tile_size`` columns (grid-stride rows cover all
+    rows); ``tile_size > num_cols`` is rejected like the row softmax."""
+    if tile_size > num_cols:
+        raise ValueError("tile_size > num_cols is not supported")
+    x2 = np.asarray(x, dtype=np.float32).reshape(num_rows, num_cols)
+    res = np.array(out, dtype=np.float64).reshape(num_rows, num_cols)
+    res[:, :tile_size] = gelu_values(x2[:, :tile_size], approximate)
     return res
 
 

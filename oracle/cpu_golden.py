@@ -9,8 +9,13 @@ with torch on the host cores:
   int8        a.to(int32) @ b.to(int32)               python/test/generalization/adv/test_matmul_iterate_all.py:116
   dequant     (acc.float() * scale).half()            build definition of DEQF16 (test_matmul_quant.py:94-106)
   attention   softmax(q k^T * scale + mask) v in fp32 (no reference golden; build-defined)
+  leaky_relu  torch.where(x >= 0, x, x * alpha)       python/test/asc2/kernels/test_leaky_relu.py:47
+  vmuladd     x * y + z                               python/test/asc2/kernels/test_vmuladd.py:52
+  gelu        0.5 x (1 + tanh(...)) / 0.5 x (1 + erf(x / sqrt 2))   python/test/asc2/kernels/test_gelu.py:44-48
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -42,3 +47,17 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float
         n = s.shape[0]
         s = s.masked_fill(torch.ones(n, s.shape[1], dtype=torch.bool).triu(1), float("-inf"))
     return torch.softmax(s, dim=-1) @ v.float()
+
+
+def leaky_relu(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
+    return torch.where(x >= 0, x, x * alpha)
+
+
+def vmuladd(x, y, z):
+    return x * y + z
+
+
+def gelu(x: torch.Tensor, approximate: bool) -> torch.Tensor:
+    if approximate:
+        return 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * torch.pow(x, 3))))
+    return 0.5 * x * (1 + torch.erf(x / math.sqrt(2)))

@@ -38,6 +38,9 @@ SIGNATURES = {
                         ctypes.c_char_p],
     "asc_stream_synchronize": [_c_p],
     "asc_vadd": [_c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
+    "asc_leaky_relu": [_c_i32, _c_p, _c_f32, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
+    "asc_vmuladd": [_c_i32, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
+    "asc_gelu_rows_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
     "asc_softmax_rows_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
     "asc_softmax_blocks_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
     "asc_matmul": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],

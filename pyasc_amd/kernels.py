@@ -77,6 +77,70 @@ def vadd(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, size: int, tile_si
                  grid, _stream(stream))
 
 
+# -------------------------------------------------------------------------- leaky_relu / vmuladd / gelu
+
+def _check_stream_operands(tensors, covered: int) -> int:
+    """Common checks of the tiled elementwise kernels: contiguous device tensors of one
+    float dtype, each holding at least the covered elements.  Returns the dtype code."""
+    for t, n in tensors:
+        _contiguous(_device_tensor(t, n), n)
+    first = tensors[0][0]
+    code = _code(first, tensors[0][1], (torch.float32, torch.float16, torch.bfloat16))
+    for t, n in tensors:
+        if t.dtype != first.dtype:
+            raise TypeError(f"operands must share one dtype, got {first.dtype} and {t.dtype} ('{n}')")
+        if t.numel() < covered:
+            raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {covered}")
+    return code
+
+
+def _check_tiling(size: int, tile_size: int, tile_per_block: int, grid: int, what: str) -> None:
+    if tile_size <= 0 or tile_per_block < 0 or grid <= 0 or size < 0:
+        raise ValueError(f"invalid {what} launch: size={size}, tile_size={tile_size}, "
+                         f"tile_per_block={tile_per_block}, grid={grid}")
+
+
+def leaky_relu(x: torch.Tensor, alpha: float, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
+               grid: int, stream: Any = None) -> None:
+    """asc2 leaky_relu_kernel (python/test/asc2/kernels/test_leaky_relu.py:16-26):
+    out = where(x >= 0, x, x * alpha) over the vadd-style covered range; ``alpha`` is
+    used at its float value (a 0-dim bf16 tensor's exact value)."""
+    _check_tiling(size, tile_size, tile_per_block, grid, "leaky_relu")
+    covered = vadd_covered(size, tile_size, tile_per_block, grid)
+    code = _check_stream_operands(((x, "x"), (out, "out")), covered)
+    _native.call("asc_leaky_relu", code, x.data_ptr(), float(alpha), out.data_ptr(), size, tile_size,
+                 tile_per_block, grid, _stream(stream))
+
+
+def vmuladd(x: torch.Tensor, y: torch.Tensor, z: torch.Tensor, out: torch.Tensor, size: int, tile_size: int,
+            tile_per_block: int, grid: int, stream: Any = None) -> None:
+    """asc2 vmuladd_kernel (python/test/asc2/kernels/test_vmuladd.py:16-31): out = x * y + z,
+    multiply and add rounded separately."""
+    _check_tiling(size, tile_size, tile_per_block, grid, "vmuladd")
+    covered = vadd_covered(size, tile_size, tile_per_block, grid)
+    code = _check_stream_operands(((x, "x"), (y, "y"), (z, "z"), (out, "out")), covered)
+    _native.call("asc_vmuladd", code, x.data_ptr(), y.data_ptr(), z.data_ptr(), out.data_ptr(), size, tile_size,
+                 tile_per_block, grid, _stream(stream))
+
+
+def gelu_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, approximate: bool,
+              grid: int, stream: Any = None) -> None:
+    """asc2 gelu_kernel (python/test/asc2/kernels/test_gelu.py:19-33) on fp32 rows."""
+    if tile_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
+        raise ValueError(f"invalid gelu launch: rows={num_rows}, cols={num_cols}, tile={tile_size}, grid={grid}")
+    if tile_size > num_cols:
+        raise ValueError(f"tile_size {tile_size} > num_cols {num_cols}: the reference kernel's row store would "
+                         "spill into the next row")
+    for t, n in ((x, "x"), (out, "out")):
+        _contiguous(_device_tensor(t, n), n)
+        if t.dtype != torch.float32:
+            raise TypeError(f"gelu supports float32 only, '{n}' is {t.dtype}")
+        if t.numel() < num_rows * num_cols:
+            raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {num_rows}x{num_cols}")
+    _native.call("asc_gelu_rows_f32", x.data_ptr(), out.data_ptr(), num_rows, num_cols, tile_size,
+                 int(bool(approximate)), grid, _stream(stream))
+
+
 # ------------------------------------------------------------------------------------------- softmax
 
 def _check_softmax(x: torch.Tensor, out: torch.Tensor, rows: int, num_cols: int) -> None:

@@ -55,6 +55,43 @@ def _vadd(call: KernelCall) -> None:
                  int(call.consts["tile_size"]), int(call.consts["tile_per_block"]), call.grid, call.stream)
 
 
+# ------------------------------------------------------------------ leaky_relu / vmuladd / gelu
+
+def _scalar(v) -> float:
+    """A by-value float argument: a python number or a 0-dim tensor (its exact value)."""
+    if isinstance(v, torch.Tensor):
+        if v.dim() != 0:
+            raise TypeError("a scalar argument must be a python number or a 0-dim tensor")
+        return float(v.item())
+    return float(v)
+
+
+@register("leaky_relu_kernel", ("x_ptr", "alpha", "out_ptr", "size", "tile_size", "tile_per_block"),
+          "python/test/asc2/kernels/test_leaky_relu.py:16-26")
+def _leaky_relu(call: KernelCall) -> None:
+    kernels.leaky_relu(call.args["x_ptr"], _scalar(call.args["alpha"]), call.args["out_ptr"],
+                       int(call.args["size"]), int(call.consts["tile_size"]), int(call.consts["tile_per_block"]),
+                       call.grid, call.stream)
+
+
+@register("vmuladd_kernel", ("x_ptr", "y_ptr", "z_ptr", "out_ptr", "size", "tile_size", "tile_per_block",
+                             "buffer_factor"),
+          "python/test/asc2/kernels/test_vmuladd.py:16-31")
+def _vmuladd(call: KernelCall) -> None:
+    # buffer_factor is the reference loop's unroll/double-buffer hint; it does not change the result
+    kernels.vmuladd(call.args["x_ptr"], call.args["y_ptr"], call.args["z_ptr"], call.args["out_ptr"],
+                    int(call.args["size"]), int(call.consts["tile_size"]), int(call.consts["tile_per_block"]),
+                    call.grid, call.stream)
+
+
+@register("gelu_kernel", ("x_ptr", "out_ptr", "num_rows", "num_columns", "tile_size", "approximate"),
+          "python/test/asc2/kernels/test_gelu.py:19-33")
+def _gelu(call: KernelCall) -> None:
+    kernels.gelu_rows(call.args["x_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
+                      int(call.get("num_columns")), int(call.get("tile_size")), bool(call.get("approximate")),
+                      call.grid, call.stream)
+
+
 # ------------------------------------------------------------------------------------------- softmax
 
 @register("softmax_kernel", ("x_ptr", "out_ptr", "num_rows", "num_cols", "tile_size"),

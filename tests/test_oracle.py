@@ -266,3 +266,74 @@ def test_attention_matches_torch_sdpa(causal):
     for h in range(2):
         got = O.attention(q[0, h].numpy(), k[0, h].numpy(), v[0, h].numpy(), 0.2, causal)
         np.testing.assert_allclose(got, ref[0, h].numpy(), rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------------------------ leaky_relu / vmuladd / gelu
+
+def _leaky_body_loop(x, alpha, size, tile, tpb, grid):
+    """Literal per-element loop of test_leaky_relu.py:19-26 in float32."""
+    out = np.full(x.shape, 7.0, np.float32)
+    for b in range(grid):
+        for i in range(tpb):
+            off = (b * tpb + i) * tile
+            for j in range(off, min(off + tile, size)):
+                v = np.float32(x[j])
+                out[j] = v if v >= 0 else np.float32(v * np.float32(alpha))
+    return out
+
+
+@pytest.mark.parametrize("size,tile,tpb,grid", [(1000, 32, 2, 8), (300, 7, 3, 4), (64, 128, 1, 1)])
+def test_leaky_relu_matches_kernel_body_loop(size, tile, tpb, grid):
+    x = np.random.default_rng(size).standard_normal(size).astype(np.float32) * 3
+    got = O.leaky_relu(x, 0.1, np.full(size, 7.0, np.float32), size, tile, tpb, grid)
+    np.testing.assert_array_equal(got, _leaky_body_loop(x, 0.1, size, tile, tpb, grid))
+
+
+def test_leaky_relu_known_answers_and_torch_bf16_golden():
+    x = np.array([2.0, -2.0, -0.0, 0.0, np.nan, -np.inf], np.float32)
+    got = O.leaky_relu_elements(x, 0.25, "float32")
+    assert got[0] == 2.0 and got[1] == -0.5 and got[4] != got[4] and got[5] == -np.inf
+    assert np.signbit(got[2]) and not np.signbit(got[3])  # -0 >= 0 passes through unchanged
+    # the reference test's recipe and golden (test_leaky_relu.py:41-47), bfloat16
+    g = torch.Generator().manual_seed(0)
+    xt = torch.rand(8192, dtype=torch.bfloat16, generator=g) * 10.0 - 5.0
+    alpha = torch.tensor(0.1, dtype=torch.bfloat16)
+    golden = torch.where(xt >= 0, xt, xt * alpha)
+    bits = xt.view(torch.int16).numpy().view(np.uint16)
+    ours = O.leaky_relu_elements(bits, float(alpha.item()), "bfloat16")
+    np.testing.assert_array_equal(ours, golden.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_vmuladd_unfused_known_answer_and_goldens():
+    one = np.float32(1.0 + 2.0 ** -12)
+    # x*y = 1 + 2^-11 + 2^-24 rounds (tie to even) to 1 + 2^-11, so the sum is 0; a fused
+    # multiply-add would give 2^-24
+    got = O.muladd_elements(np.array([one]), np.array([one]), np.array([-(1.0 + 2.0 ** -11)], np.float32),
+                            "float32")
+    assert got[0] == 0.0
+    rng = np.random.default_rng(seed=2026)  # test_vmuladd.py:43-52
+    x, y, z = (rng.random(8192, dtype=np.float32) * 10 for _ in range(3))
+    np.testing.assert_array_equal(O.muladd_elements(x, y, z, "float32"), x * y + z)
+    for dt, name in ((torch.float16, "float16"), (torch.bfloat16, "bfloat16")):
+        g = torch.Generator().manual_seed(3)
+        xt, yt, zt = (torch.randn(4096, generator=g).to(dt) * 4 for _ in range(3))
+        golden = xt * yt + zt
+        if name == "bfloat16":
+            conv = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        else:
+            conv = lambda t: t.numpy()  # noqa: E731
+        ours = O.muladd_elements(conv(xt), conv(yt), conv(zt), name)
+        np.testing.assert_array_equal(np.asarray(ours).view(np.uint16), conv(golden).view(np.uint16))
+
+
+@pytest.mark.parametrize("approximate", [True, False])
+def test_gelu_matches_torch_and_identities(approximate):
+    x = np.linspace(-8, 8, 2001).astype(np.float32)
+    ours = O.gelu_values(x, approximate)
+    ref = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="tanh" if approximate else "none")
+    np.testing.assert_allclose(ours, ref.numpy(), rtol=1e-12, atol=1e-14)
+    assert O.gelu_values(np.zeros(1, np.float32), approximate)[0] == 0.0
+    # gelu(x) - gelu(-x) = x for both forms (x*Phi(x) and x*sigmoid(2u) are odd-complemented)
+    np.testing.assert_allclose(ours - O.gelu_values(-x, approximate), x.astype(np.float64), rtol=0, atol=1e-12)
+    out = O.gelu_rows(np.tile(x[:64], 3), np.full(192, 5.0), 3, 64, 40, approximate)
+    assert (out[:, 40:] == 5.0).all()

@@ -136,6 +136,33 @@ def test_registry_contents():
     assert sum(1 for n, _ in names if n == "matmul_kernel") == 4
     assert ("flash_attention_fwd_kernel", "block_n") in names
     assert ("matmul_dequant_kernel", "c_shape") in names
+    assert ("leaky_relu_kernel", "tile_per_block") in names and ("vmuladd_kernel", "buffer_factor") in names
+    assert ("gelu_kernel", "approximate") in names
+
+
+@asc2.jit(always_compile=True)
+def leaky_relu_kernel(x_ptr: asc.GlobalAddress, alpha: float, out_ptr: asc.GlobalAddress, size: int,
+                      tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+    pass
+
+
+@asc2.jit(always_compile=True)
+def gelu_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: asc.ConstExpr,
+                num_columns: asc.ConstExpr, tile_size: asc.ConstExpr, approximate: asc.ConstExpr):
+    pass
+
+
+def test_scalar_and_bare_constexpr_arguments(recorded):
+    # test_leaky_relu.py passes alpha as a 0-dim bf16 tensor to an `alpha: float` parameter (by value);
+    # test_gelu.py annotates with bare asc.ConstExpr
+    x = torch.zeros(256, dtype=torch.bfloat16)
+    alpha = torch.tensor(0.1, dtype=torch.bfloat16)
+    leaky_relu_kernel[16](x, alpha, x, 256, 128, 1)
+    entry, name, rt, ce, _ = recorded[0]
+    assert entry.params[1] == "alpha" and rt["alpha"] is alpha and ce == {"tile_size": 128, "tile_per_block": 1}
+    assert launcher_mod.Launcher.scalar_value(rt["alpha"]) == float(alpha.item())
+    gelu_kernel[16](torch.zeros(2, 8), torch.zeros(2, 8), 2, 8, 8, True)
+    assert recorded[1][3] == {"num_rows": 2, "num_columns": 8, "tile_size": 8, "approximate": True}
 
 
 def test_set_platform_surface():
