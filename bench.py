@@ -272,11 +272,12 @@ class Gelu(Workload):
 class Matmul(Workload):
     bound, unit, kernel_hint = "mfma", "TFLOP/s", "gemm_mfma"
 
-    def __init__(self, n: int, dtype: str):
-        self.n, self.dt = n, dtype
+    def __init__(self, n: int, dtype: str, bias_leaky: bool = False):
+        self.n, self.dt, self.bias_leaky = n, dtype, bias_leaky
         self.dtype = {"bfloat16": "bf16", "float16": "f16"}[dtype]
         self.peak = BF16_PEAK_TFLOPS if dtype == "bfloat16" else FP16_PEAK_TFLOPS
-        self.name = f"matmul_{n}x{n}x{n}_{self.dtype}"
+        # the 05_matmul_leakyrelu tutorial's epilogue: fp32 C = leaky_relu(A B + bias, 0.001)
+        self.name = f"matmul_{n}x{n}x{n}_{self.dtype}" + ("_bias_leakyrelu_f32out" if bias_leaky else "")
 
     def setup(self, dev):
         import torch
@@ -284,18 +285,25 @@ class Matmul(Workload):
         g = torch.Generator(device=dev).manual_seed(2)
         self.a = (torch.randn(self.n, self.n, device=dev, generator=g) / math.sqrt(self.n)).to(td)
         self.b = (torch.randn(self.n, self.n, device=dev, generator=g) / math.sqrt(self.n)).to(td)
-        self.c = torch.empty(self.n, self.n, device=dev, dtype=td)
+        self.c = torch.empty(self.n, self.n, device=dev, dtype=torch.float32 if self.bias_leaky else td)
+        self.bias = torch.randn(self.n, device=dev, generator=g) if self.bias_leaky else None
 
     def launch(self, i: int) -> None:
         from pyasc_amd import kernels
-        kernels.matmul(self.a, self.b, self.c)
+        if self.bias_leaky:
+            kernels.matmul(self.a, self.b, self.c, bias=self.bias, leaky_alpha=0.001)
+        else:
+            kernels.matmul(self.a, self.b, self.c)
 
     def work(self) -> float:
         return 2.0 * self.n ** 3
 
     def config(self) -> dict:
-        return {"workload": self.name, "M": self.n, "N": self.n, "K": self.n, "layout": "A row-major, B row-major",
-                "input": "randn/sqrt(K), seed 2", "accumulate": "fp32", "out": self.dtype}
+        cfg = {"workload": self.name, "M": self.n, "N": self.n, "K": self.n, "layout": "A row-major, B row-major",
+               "input": "randn/sqrt(K), seed 2", "accumulate": "fp32", "out": self.dtype}
+        if self.bias_leaky:
+            cfg.update({"out": "f32", "epilogue": "leaky_relu(acc + bias[n], 0.001)"})
+        return cfg
 
 
 class MatmulI8(Workload):
@@ -362,6 +370,7 @@ WORKLOADS = {
     "vadd_8192": lambda: Vadd(8192),
     "matmul_bf16_8192": lambda: Matmul(8192, "bfloat16"),
     "matmul_f16_8192": lambda: Matmul(8192, "float16"),
+    "matmul_f16_8192_bias_leakyrelu": lambda: Matmul(8192, "float16", bias_leaky=True),
     "matmul_i8_4096x11008x4096": lambda: MatmulI8(4096, 11008, 4096),
     "fa_fwd_noncausal": lambda: FlashAttention(4, 32, 4096, 128, False),
     "fa_fwd_causal": lambda: FlashAttention(4, 32, 4096, 128, True),
@@ -372,7 +381,7 @@ WORKLOADS = {
 }
 HEADLINE = "softmax_4096x4096"
 SUITE = ["softmax_16384x1024", "vadd_268435456", "matmul_bf16_8192", "matmul_f16_8192", "matmul_i8_4096x11008x4096",
-         "fa_fwd_noncausal", "fa_fwd_causal", "leaky_relu_268435456", "vmuladd_268435456", "gelu_tanh_16384x1024",
+         "matmul_f16_8192_bias_leakyrelu", "fa_fwd_noncausal", "fa_fwd_causal", "leaky_relu_268435456", "vmuladd_268435456", "gelu_tanh_16384x1024",
          "gelu_erf_16384x1024"]
 
 

@@ -122,9 +122,10 @@ int32_t asc_gelu_rows_f32(const float* x, float* out, int64_t num_rows,
  *                     tile_size: ConstExpr[int])
  *   python/test/asc2/kernels/test_softmax.py:16-27.
  * Rows i = b, b+grid, ... cover every row; each row's first `tile_size`
- * columns are replaced by exp(x - max) / sum(exp(x - max)) (true division,
- * lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116); columns >= tile_size
- * are untouched.  tile_size must be <= num_cols: with tile_size > num_cols the
+ * columns are replaced by exp(x - max) / sum(exp(x - max)) (the reference
+ * divides, lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116; here one
+ * correctly rounded reciprocal per row and a multiply, within 2 ulp of the
+ * quotient); columns >= tile_size are untouched.  tile_size must be <= num_cols: with tile_size > num_cols the
  * reference's reduction counts the zero padding and its store spills into the
  * next row, which is rejected here (ASC_ERR_UNSUPPORTED). */
 int32_t asc_softmax_rows_f32(const float* x, float* out, int64_t num_rows,
@@ -157,6 +158,20 @@ int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a,
                    const void* b, void* c, int64_t M, int64_t N, int64_t K,
                    int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,
                    asc_stream_t stream);
+
+/* ---- matmul with bias and activation epilogue -------------------------------
+ * asc1 matmul_leakyrelu_kernel(a, b, c, bias, alpha: float, tiling, workspace)
+ *   python/tutorials/05_matmul_leakyrelu/matmul_leakyrelu.py:27-70: the Matmul
+ *   API with set_bias (fp32 bias[n] added to the fp32 accumulator) followed by
+ *   asc.leaky_relu (python/asc/language/basic/vec_binary_scalar.py:63-66).
+ * C[m,n] = cast(act(acc[m,n] + bias[n])) with acc as in asc_matmul; bias may be
+ * NULL (no add); act: 0 none, 1 relu, 2 leaky relu (v >= 0 ? v : v * alpha).
+ * asc_matmul(..., relu) equals asc_matmul_bias_act(..., NULL, ..., relu, 0). */
+int32_t asc_matmul_bias_act(int32_t in_dtype, int32_t out_dtype, const void* a,
+                            const void* b, void* c, const float* bias,
+                            int64_t M, int64_t N, int64_t K, int64_t lda,
+                            int64_t ldb, int64_t ldc, int32_t act, float alpha,
+                            asc_stream_t stream);
 
 /* ---- int8 matmul with per-channel dequant -----------------------------------
  * asc1 matmul_kernel(a, b, c, tiling, workspace, quant_vector) with

@@ -28,6 +28,8 @@ How each function is pinned (tests/test_oracle.py):
                   / bfloat16 mul-then-add.
   gelu            torch.nn.functional.gelu in float64 (both forms; same function,
                   different expression), gelu(0) = 0, gelu(x) - gelu(-x) = x.
+  matmul + bias   the tutorial's golden (torch fp32 matmul + bias, then where) on
+  + leaky_relu    its integer-valued recipe (exact), a hand-computed 2x2 case.
 Every function here has at least one such check; none is "parity unpinned".
 """
 from __future__ import annotations
@@ -218,6 +220,16 @@ def matmul(a: np.ndarray, b: np.ndarray, relu: bool = False, out_dtype: str = "f
     if out_dtype == "bfloat16":
         return f32_to_bf16_bits(acc)
     raise ValueError(out_dtype)
+
+
+def matmul_bias_leaky_relu(a: np.ndarray, b: np.ndarray, bias: np.ndarray, alpha: float) -> np.ndarray:
+    """python/tutorials/05_matmul_leakyrelu/matmul_leakyrelu.py:27-70: the Matmul API's fp32
+    result with set_bias (bias[n] added to the fp32 accumulator), then asc.leaky_relu
+    (vec_binary_scalar.py:63-66, v >= 0 ? v : v * alpha in fp32).  Products exact in fp64,
+    the fp64 sum standing in for the fp32 accumulator as in ``matmul``."""
+    acc = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    v = (acc + np.asarray(bias, dtype=np.float32).reshape(1, -1)).astype(np.float32)
+    return np.where(v >= 0, v, (v * np.float32(alpha)).astype(np.float32))
 
 
 def mnblock_rectangles(M: int, N: int, grid: int, m_tile: int, m_tiles_per_block: int, n_tile: int,

@@ -36,7 +36,7 @@ class ArgType:
     """Classification of one runtime argument: pointer or by-value, with its dtype name."""
 
     def __init__(self, kind: str, dtype: DataType):
-        self.kind = kind  # "pointer" | "plain"
+        self.kind = kind  # "pointer" | "plain" | "struct"
         self.dtype = dtype
 
     def __repr__(self) -> str:
@@ -105,6 +105,10 @@ class JITFunction:
             return ArgType("pointer", DataType(str(np.dtype(value.dtype))))
         if isinstance(value, np.generic):
             return ArgType("plain", DataType(str(value.dtype)))
+        from ..adv import TCubeTiling
+        if isinstance(value, TCubeTiling):
+            # passed by value as a struct on the reference (python/asc/runtime/launcher.py:156-184)
+            return ArgType("struct", DataType("void"))
         try:
             import torch
             if isinstance(value, torch.Tensor):

@@ -38,13 +38,32 @@ constexpr int kStageBytes = asc::gemm::kStageBytes;
 
 enum OutKind { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
 
+// Epilogue on the fp32 accumulator, before the output cast: optional
+// per-column bias (fp32 add), then an activation -- 0 none, 1 relu (fixpipe
+// relu), 2 leaky relu v >= 0 ? v : v * alpha.
+struct Epilogue {
+  const float* bias;  // [N] or null
+  int act;
+  float alpha;
+  __device__ __forceinline__ float operator()(float v, float bias_n) const {
+    if (bias != nullptr) v += bias_n;
+    if (act == 1) {
+      v = fmaxf(v, 0.0f);
+    } else if (act == 2) {
+      v = v >= 0.0f ? v : v * alpha;
+    }
+    return v;
+  }
+  __device__ __forceinline__ float bias_at(int n) const { return bias != nullptr ? bias[n] : 0.0f; }
+};
+
 struct GemmArgs {
   const uint16_t* a;
   const uint16_t* b;
   void* c;
   int M, N, K;
   int64_t lda, ldb, ldc;
-  int relu;
+  Epilogue epi;
   int tiles_m, tiles_n;
 };
 
@@ -149,6 +168,12 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
   // register r holds row 8*(r/4) + 4*(lane/32) + r%4.
   const int col_in = lane & 31;
   const int row_q = (lane >> 5) * 4;
+  float bias_n[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 128 + j * 32 + col_in;
+    bias_n[j] = (!kChecked || n < p.N) ? p.epi.bias_at(n) : 0.0f;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -158,8 +183,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
         if (kChecked && (m >= p.M || n >= p.N)) continue;
-        float v = acc[i][j][r];
-        if (p.relu) v = fmaxf(v, 0.0f);
+        const float v = p.epi(acc[i][j][r], bias_n[j]);
         const int64_t off = static_cast<int64_t>(m) * p.ldc + n;
         if constexpr (kOut == kOutF32) {
           static_cast<float*>(p.c)[off] = v;
@@ -177,7 +201,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
 template <int kOut>
 __global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                        void* c, int M, int N, int K, int64_t lda, int64_t ldb,
-                                                       int64_t ldc, int relu) {
+                                                       int64_t ldc, Epilogue epi) {
   __shared__ float as[16][64 + 1];
   __shared__ float bs[16][64 + 1];
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -206,7 +230,7 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__
     for (int j = 0; j < 4; ++j) {
       const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
       if (m >= M || n >= N) continue;
-      float v = relu ? fmaxf(acc[i][j], 0.f) : acc[i][j];
+      const float v = epi(acc[i][j], epi.bias_at(n));
       const int64_t off = static_cast<int64_t>(m) * ldc + n;
       if constexpr (kOut == kOutF32) static_cast<float*>(c)[off] = v;
       else if constexpr (kOut == kOutF16) static_cast<uint16_t*>(c)[off] = asc::f32_to_f16_rne(v);
@@ -239,9 +263,10 @@ int32_t dispatch_out(const GemmArgs& p, int out_dtype, bool fast, hipStream_t st
 
 }  // namespace
 
-extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M,
-                              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,
-                              asc_stream_t stream) {
+namespace {
+
+int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
+                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi, asc_stream_t stream) {
   ASC_REQUIRE(M >= 0 && N >= 0 && K >= 0, ASC_ERR_INVALID_ARG, "asc_matmul: negative shape");
   ASC_REQUIRE(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), ASC_ERR_UNSUPPORTED, "asc_matmul: shape too large");
   ASC_REQUIRE(lda >= K && ldb >= N && ldc >= N, ASC_ERR_INVALID_ARG,
@@ -257,15 +282,15 @@ extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a
     switch (out_dtype) {
       case ASC_DT_FLOAT32:
         hipLaunchKernelGGL(gemm_f32_kernel<kOutF32>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
-                           ldb, ldc, relu);
+                           ldb, ldc, epi);
         break;
       case ASC_DT_FLOAT16:
         hipLaunchKernelGGL(gemm_f32_kernel<kOutF16>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
-                           ldb, ldc, relu);
+                           ldb, ldc, epi);
         break;
       case ASC_DT_BFLOAT16:
         hipLaunchKernelGGL(gemm_f32_kernel<kOutBF16>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
-                           ldb, ldc, relu);
+                           ldb, ldc, epi);
         break;
       default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
     }
@@ -283,7 +308,7 @@ extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a
   p.lda = lda;
   p.ldb = ldb;
   p.ldc = ldc;
-  p.relu = relu;
+  p.epi = epi;
   p.tiles_m = static_cast<int>((M + BM - 1) / BM);
   p.tiles_n = static_cast<int>((N + BN - 1) / BN);
   const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
@@ -294,4 +319,20 @@ extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a
   // K == 0 takes the checked kernel: no k-tile runs and C receives cast(0).
   return in_dtype == ASC_DT_BFLOAT16 ? dispatch_out<true>(p, out_dtype, fast, s)
                                      : dispatch_out<false>(p, out_dtype, fast, s);
+}
+
+}  // namespace
+
+extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M,
+                              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,
+                              asc_stream_t stream) {
+  return matmul_impl(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{nullptr, relu ? 1 : 0, 0.0f},
+                     stream);
+}
+
+extern "C" int32_t asc_matmul_bias_act(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c,
+                                       const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                       int64_t ldc, int32_t act, float alpha, asc_stream_t stream) {
+  ASC_REQUIRE(act >= 0 && act <= 2, ASC_ERR_INVALID_ARG, "asc_matmul_bias_act: act must be 0, 1 or 2, got %d", act);
+  return matmul_impl(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{bias, act, alpha}, stream);
 }

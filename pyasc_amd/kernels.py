@@ -194,9 +194,14 @@ def _row_major_2d(t: torch.Tensor, name: str) -> int:
     return max(t.stride(0), t.shape[1], 1)
 
 
-def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False, stream: Any = None) -> None:
-    """c = cast(relu?(a @ b)) with fp32 accumulation; the cast is chosen by c's dtype
-    (float32: no cast; float16/bfloat16: RNE)."""
+ACT_NONE, ACT_RELU, ACT_LEAKY_RELU = 0, 1, 2
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False, stream: Any = None,
+           bias: Optional[torch.Tensor] = None, leaky_alpha: Optional[float] = None) -> None:
+    """c = cast(act(a @ b + bias)) with fp32 accumulation; the cast is chosen by c's dtype
+    (float32: no cast; float16/bfloat16: RNE).  ``bias``: float32 with N elements (added
+    per column), ``relu``: max(v, 0), ``leaky_alpha``: v >= 0 ? v : v * alpha (excludes relu)."""
     for t, n in ((a, "a"), (b, "b"), (c, "c")):
         _device_tensor(t, n)
     in_code = _code(a, "a", (torch.float32, torch.float16, torch.bfloat16))
@@ -210,8 +215,21 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False
         raise ValueError(f"inner dimensions differ: a is {tuple(a.shape)}, b is {tuple(b.shape)}")
     if tuple(c.shape) != (M, N):
         raise ValueError(f"c must be {(M, N)}, got {tuple(c.shape)}")
-    _native.call("asc_matmul", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, lda, ldb, ldc,
-                 int(bool(relu)), _stream(stream))
+    if bias is None and leaky_alpha is None:
+        _native.call("asc_matmul", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, lda, ldb,
+                     ldc, int(bool(relu)), _stream(stream))
+        return
+    if relu and leaky_alpha is not None:
+        raise ValueError("relu and leaky_alpha are exclusive")
+    bias_ptr = 0
+    if bias is not None:
+        _contiguous(_device_tensor(bias, "bias"), "bias")
+        if bias.dtype != torch.float32 or bias.numel() != N:
+            raise ValueError(f"bias must be float32 with {N} elements, got {bias.dtype} with {bias.numel()}")
+        bias_ptr = bias.data_ptr()
+    act = ACT_LEAKY_RELU if leaky_alpha is not None else (ACT_RELU if relu else ACT_NONE)
+    _native.call("asc_matmul_bias_act", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), bias_ptr, M, N,
+                 K, lda, ldb, ldc, act, float(leaky_alpha or 0.0), _stream(stream))
 
 
 def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional[torch.Tensor] = None,

@@ -193,6 +193,19 @@ def _matmul_chained(call: KernelCall) -> None:
 
 # ------------------------------------------------------------- int8 matmul (build-defined asc2 style)
 
+@register("matmul_leakyrelu_kernel", ("a", "b", "c", "bias", "alpha", "tiling", "workspace"),
+          "python/tutorials/05_matmul_leakyrelu/matmul_leakyrelu.py:27-70")
+def _matmul_leakyrelu(call: KernelCall) -> None:
+    """c = leaky_relu(a @ b + bias, alpha) in fp32 (the tutorial's Matmul + set_bias + asc.leaky_relu).
+    Shapes come from the tensors: a [M, K], b [K, N], c [M, N], bias N elements.  The
+    tiling argument (the CANN tiling library's per-core split) and the workspace are
+    accepted and not used: the MI355X kernel picks its own tiles."""
+    a, b, c, bias = call.args["a"], call.args["b"], call.args["c"], call.args["bias"]
+    if a.dim() != 2 or b.dim() != 2 or c.dim() != 2:
+        raise ValueError("a, b and c must be 2-D")
+    kernels.matmul(a, b, c, bias=bias.reshape(-1), leaky_alpha=_scalar(call.args["alpha"]), stream=call.stream)
+
+
 @register("matmul_int8_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape"),
           "python/test/generalization/adv/test_matmul_iterate_all.py:106-120 (int8 -> int32 case)")
 def _matmul_int8(call: KernelCall) -> None:

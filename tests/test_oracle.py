@@ -337,3 +337,21 @@ def test_gelu_matches_torch_and_identities(approximate):
     np.testing.assert_allclose(ours - O.gelu_values(-x, approximate), x.astype(np.float64), rtol=0, atol=1e-12)
     out = O.gelu_rows(np.tile(x[:64], 3), np.full(192, 5.0), 3, 64, 40, approximate)
     assert (out[:, 40:] == 5.0).all()
+
+
+def test_matmul_bias_leaky_relu_known_answer_and_tutorial_golden():
+    a = np.array([[1.0, 2.0], [3.0, -4.0]], np.float32)
+    b = np.array([[1.0, -1.0], [1.0, 1.0]], np.float32)
+    # a @ b = [[3, 1], [-1, -7]]; + bias [0.5, -2] = [[3.5, -1], [-0.5, -9]]; leaky 0.25
+    got = O.matmul_bias_leaky_relu(a, b, np.array([0.5, -2.0], np.float32), 0.25)
+    np.testing.assert_array_equal(got, np.array([[3.5, -0.25], [-0.125, -2.25]], np.float32))
+    # the tutorial's recipe and golden (matmul_leakyrelu.py:121-128)
+    g = torch.Generator().manual_seed(5)
+    m, k, n = 1024, 256, 640
+    at = torch.randint(-5, 5, (m, k), generator=g).to(torch.float16)
+    bt = torch.randint(-5, 5, (k, n), generator=g).to(torch.float16)
+    bias = torch.randint(-5, 5, (1, n), generator=g).to(torch.float32)
+    mm = (torch.matmul(at.to(torch.float32), bt.to(torch.float32)).to(torch.float32) + bias).to(torch.float32)
+    golden = torch.where(mm >= 0, mm, mm * 0.001)
+    ours = O.matmul_bias_leaky_relu(at.float().numpy(), bt.float().numpy(), bias.numpy(), 0.001)
+    np.testing.assert_array_equal(ours, golden.numpy())
