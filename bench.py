@@ -269,6 +269,79 @@ class Gelu(Workload):
                 "seconds_per_call": secs}
 
 
+class RmsNorm(Workload):
+    """asc2.rms_norm rows (build-defined rms_norm_kernel) at softmax's headline shape."""
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "rms_norm"
+
+    def __init__(self, rows: int, cols: int):
+        self.rows, self.cols = rows, cols
+        self.name = f"rms_norm_{rows}x{cols}_f32"
+
+    def setup(self, dev):
+        import torch
+        g = torch.Generator(device=dev).manual_seed(1)
+        self.gamma = torch.rand(self.cols, device=dev, generator=g) + 0.5
+        self.sets = [(torch.randn(self.rows, self.cols, device=dev, generator=g) * 2.0,
+                      torch.empty(self.rows, self.cols, device=dev))
+                     for _ in range(_sets_for(8 * self.rows * self.cols))]
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        x, out = self.sets[i % len(self.sets)]
+        kernels.rms_norm(x, self.gamma, out, self.rows, self.cols, 1e-6)
+
+    def work(self) -> float:
+        return 8.0 * self.rows * self.cols + 4.0 * self.cols
+
+    def config(self) -> dict:
+        return {"workload": self.name, "rows": self.rows, "cols": self.cols, "epsilon": 1e-6,
+                "input": "randn*2 fp32, gamma rand+0.5", "rotating_sets": len(self.sets)}
+
+    def cpu_baseline(self):
+        import torch
+        x = torch.randn(self.rows, self.cols) * 2.0
+        gamma = torch.rand(self.cols) + 0.5
+        secs = _time_cpu(lambda: torch.nn.functional.rms_norm(x, [self.cols], gamma, eps=1e-6), budget_s=10.0)
+        return {"value": round(self.work() / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port", "sample": f"torch.nn.functional.rms_norm on the full {self.rows}x{self.cols} input",
+                "seconds_per_call": secs}
+
+
+class ReduceRows(Workload):
+    """asc2.reduce_sum along dim 1 (test_reduce_ops.py's kernel) at a bandwidth size."""
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "reduce_rows"
+
+    def __init__(self, rows: int, cols: int):
+        self.rows, self.cols = rows, cols
+        self.name = f"reduce_sum_dim1_{rows}x{cols}_f32"
+
+    def setup(self, dev):
+        import torch
+        g = torch.Generator(device=dev).manual_seed(1)
+        self.sets = [(torch.randn(self.rows, self.cols, device=dev, generator=g) * 2.0,
+                      torch.empty(self.rows, device=dev)) for _ in range(_sets_for(4 * self.rows * self.cols))]
+
+    def launch(self, i: int) -> None:
+        from pyasc_amd import kernels
+        x, out = self.sets[i % len(self.sets)]
+        kernels.reduce_f32(x, out, "sum", 1)
+
+    def work(self) -> float:
+        return 4.0 * self.rows * self.cols + 4.0 * self.rows
+
+    def config(self) -> dict:
+        return {"workload": self.name, "rows": self.rows, "cols": self.cols, "op": "sum", "dim": 1,
+                "input": "randn*2 fp32", "rotating_sets": len(self.sets)}
+
+    def cpu_baseline(self):
+        import torch
+        x = torch.randn(self.rows, self.cols) * 2.0
+        secs = _time_cpu(lambda: torch.sum(x, 1), budget_s=10.0)
+        return {"value": round(self.work() / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port", "sample": f"torch.sum(x, 1) on the full {self.rows}x{self.cols} input",
+                "seconds_per_call": secs}
+
+
 class Matmul(Workload):
     bound, unit, kernel_hint = "mfma", "TFLOP/s", "gemm_mfma"
 
@@ -378,11 +451,14 @@ WORKLOADS = {
     "vmuladd_268435456": lambda: VMulAdd(1 << 28),
     "gelu_tanh_16384x1024": lambda: Gelu(16384, 1024, True),
     "gelu_erf_16384x1024": lambda: Gelu(16384, 1024, False),
+    "rms_norm_4096x4096": lambda: RmsNorm(4096, 4096),
+    "reduce_sum_dim1_16384x4096": lambda: ReduceRows(16384, 4096),
 }
 HEADLINE = "softmax_4096x4096"
 SUITE = ["softmax_16384x1024", "vadd_268435456", "matmul_bf16_8192", "matmul_f16_8192", "matmul_i8_4096x11008x4096",
-         "matmul_f16_8192_bias_leakyrelu", "fa_fwd_noncausal", "fa_fwd_causal", "leaky_relu_268435456", "vmuladd_268435456", "gelu_tanh_16384x1024",
-         "gelu_erf_16384x1024"]
+         "matmul_f16_8192_bias_leakyrelu", "fa_fwd_noncausal", "fa_fwd_causal", "leaky_relu_268435456",
+         "vmuladd_268435456", "gelu_tanh_16384x1024", "gelu_erf_16384x1024", "rms_norm_4096x4096",
+         "reduce_sum_dim1_16384x4096"]
 
 
 def _time_cpu(fn, budget_s: float) -> float:

@@ -142,6 +142,32 @@ int32_t asc_softmax_blocks_f32(const float* x, float* out, int64_t num_rows,
                                int64_t num_cols, int32_t block_size,
                                int32_t grid, asc_stream_t stream);
 
+/* ---- reductions ---------------------------------------------------------------
+ * asc2.reduce_sum / reduce_max / reduce_min / reduce_prod
+ *   (python/asc/language/tile/reduction_ops.py:61-126) as the reference's
+ *   reduction tests launch them (python/test/asc2/operations/test_reduce_ops.py:
+ *   kernel, kernel_all, reduce_tile_kernel).
+ * x: fp32 [rows, cols] row-major.  op: 0 sum, 1 max, 2 min, 3 prod (fp32
+ * accumulation; max/min return the non-NaN operand).  dim 1: out[r] over
+ * columns; dim 0: out[c] over rows; dim -1: over all elements, the result
+ * written to out[0 .. out_count) (asc2.full of the scalar). */
+int32_t asc_reduce_f32(int32_t op, const float* x, float* out, int64_t rows,
+                       int64_t cols, int32_t dim, int64_t out_count,
+                       asc_stream_t stream);
+
+/* ---- RMS norm -------------------------------------------------------------------
+ * asc2.rms_norm(input, gamma, epsilon) (python/asc/language/tile/unary_ops.py:
+ * 225-237; AscendC RmsNorm) in the build's asc2-style kernel
+ *   rms_norm_kernel(x_ptr, gamma_ptr, out_ptr, num_rows: int, num_cols: int,
+ *                   epsilon: float, tile_size: ConstExpr[int])
+ * (the reference has the op but no kernel test).  For every row, the first
+ * tile_size columns get y = (x * r) * gamma[c], r = 1 / sqrt(sum(x^2) /
+ * tile_size + epsilon), computed in fp32; other columns are untouched.
+ * dtype ASC_DT_FLOAT32 or FLOAT16 (x and out; gamma is fp32). */
+int32_t asc_rms_norm(int32_t dtype, const void* x, const float* gamma, void* out,
+                     int64_t num_rows, int64_t num_cols, int32_t tile_size,
+                     float epsilon, asc_stream_t stream);
+
 /* ---- dense matmul (cube path) ------------------------------------------------
  * C[M,N] = epilogue(A[M,K] . B[K,N]) with fp32 accumulation, row-major
  * operands with leading dimensions lda/ldb/ldc (elements).

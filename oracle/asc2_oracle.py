@@ -30,6 +30,10 @@ How each function is pinned (tests/test_oracle.py):
                   different expression), gelu(0) = 0, gelu(x) - gelu(-x) = x.
   matmul + bias   the tutorial's golden (torch fp32 matmul + bias, then where) on
   + leaky_relu    its integer-valued recipe (exact), a hand-computed 2x2 case.
+  reduce          torch sum / amax / amin / prod (the reduction tests' goldens),
+                  integer-valued sums (exact), products of powers of two (exact).
+  rms_norm        torch.nn.functional.rms_norm in float64, constant rows (closed
+                  form c / sqrt(c^2 + eps) * gamma), scale invariance.
 Every function here has at least one such check; none is "parity unpinned".
 """
 from __future__ import annotations
@@ -155,6 +159,40 @@ def gelu_rows(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, tile
     res = np.array(out, dtype=np.float64).reshape(num_rows, num_cols)
     res[:, :tile_size] = gelu_values(x2[:, :tile_size], approximate)
     return res
+
+
+# --------------------------------------------------------------------------------- reductions, rms_norm
+
+def reduce(x: np.ndarray, op: str, dim) -> np.ndarray:
+    """asc2.reduce_{sum,max,min,prod} (python/asc/language/tile/reduction_ops.py:61-126) of a
+    float32 tile along ``dim`` (None: all elements).  Sums and products in float64, rounded
+    once to float32; max / min exact (the non-NaN operand, IEEE maxNum / minNum)."""
+    xd = np.asarray(x, dtype=np.float32).astype(np.float64)
+    axis = None if dim is None else int(dim)
+    if op == "sum":
+        r = xd.sum(axis=axis)
+    elif op == "prod":
+        r = xd.prod(axis=axis)
+    elif op == "max":
+        r = np.fmax.reduce(xd, axis=axis) if axis is not None else np.fmax.reduce(xd.reshape(-1))
+    elif op == "min":
+        r = np.fmin.reduce(xd, axis=axis) if axis is not None else np.fmin.reduce(xd.reshape(-1))
+    else:
+        raise ValueError(op)
+    with np.errstate(over="ignore"):  # products of many elements overflow to +-inf, as in fp32
+        return np.asarray(r).astype(np.float32)
+
+
+def rms_norm_rows(x: np.ndarray, gamma: np.ndarray, eps: float, tile_size: int) -> np.ndarray:
+    """asc2.rms_norm (unary_ops.py:225-237, AscendC RmsNorm) over each row's first
+    ``tile_size`` columns, in float64: y = x / sqrt(mean(x^2) + eps) * gamma; other columns
+    keep x's values (the caller's output buffer is untouched there)."""
+    xd = np.asarray(x, dtype=np.float64)
+    head = xd[:, :tile_size]
+    r = 1.0 / np.sqrt((head * head).mean(axis=1, keepdims=True) + np.float64(np.float32(eps)))
+    out = xd.copy()
+    out[:, :tile_size] = head * r * np.asarray(gamma, dtype=np.float64)[:tile_size]
+    return out
 
 
 # ------------------------------------------------------------------------------------------- softmax

@@ -18,85 +18,31 @@
 #include <math.h>
 
 #include "common.h"
+#include "rows.h"
 
 namespace {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using asc::rows::f32x4;
+using asc::rows::load_row;
+using asc::rows::load_vec;
+using asc::rows::RowView;
+using asc::rows::store_row;
+using asc::rows::store_vec;
 
-struct RowView {
-  const float* x;
-  float* out;
-  int64_t rows;    // covered rows [0, rows)
-  int64_t stride;  // elements between row starts
-  int32_t len;     // columns processed per row
-  bool vec_ok;     // rows start 16-byte aligned
-};
-
-// Loads vector q (elements 4q..4q+3) of a row, padding with -inf past `len`.
-__device__ __forceinline__ float4 load_vec(const float* row, int q, int len, bool vec_ok) {
-  const int e = q * 4;
-  if (vec_ok && e + 3 < len) {
-    // streamed once: non-temporal so the rows do not displace other cached data
-    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + e));
-    return make_float4(v.x, v.y, v.z, v.w);
-  }
-  float4 v;
-  v.x = e + 0 < len ? row[e + 0] : -INFINITY;
-  v.y = e + 1 < len ? row[e + 1] : -INFINITY;
-  v.z = e + 2 < len ? row[e + 2] : -INFINITY;
-  v.w = e + 3 < len ? row[e + 3] : -INFINITY;
-  return v;
-}
-
-__device__ __forceinline__ void store_vec(float* row, int q, int len, bool vec_ok, float4 v) {
-  const int e = q * 4;
-  if (vec_ok && e + 3 < len) {
-    __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(row + e));
-    return;
-  }
-  if (e + 0 < len) row[e + 0] = v.x;
-  if (e + 1 < len) row[e + 1] = v.y;
-  if (e + 2 < len) row[e + 2] = v.z;
-  if (e + 3 < len) row[e + 3] = v.w;
-}
+// softmax rows are padded with -inf (no effect on max, sum or the exp path)
+constexpr float kPad = -INFINITY;
 
 constexpr float kL2E = 1.44269504088896340736f;   // log2(e) rounded to fp32
 constexpr float kL2ELo = 1.925963033500011e-08f;  // log2(e) - kL2E
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kMinNormalLog2 = -126.0f;
 
-// Vectors q0 + kStride*j (j < N) of a row, where q0 < kStride is the thread's
-// index in its group.  The test that a vector lies inside the row for every
-// thread of the group depends on kernel arguments only (uniform branch), so
-// full vectors are plain 16-byte loads issued back to back; only a ragged
-// tail takes the per-lane path.  (A per-lane choice between the two load
-// forms would run both and serialise the loads on their shared registers.)
+// Normalises the row in registers and stores it.
 template <int N, int kStride>
-__device__ __forceinline__ void load_row(float4 (&v)[N], const float* row, int q0, int len, bool vec_ok) {
+__device__ __forceinline__ void store_scaled(float4 (&v)[N], float* row, int q0, int len, bool vec_ok, float rs) {
 #pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const int q = q0 + kStride * j;
-    if (vec_ok && kStride * (j + 1) * 4 <= len) {
-      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row) + q);
-      v[j] = make_float4(t.x, t.y, t.z, t.w);
-    } else {
-      v[j] = load_vec(row, q, len, vec_ok);
-    }
-  }
-}
-
-template <int N, int kStride>
-__device__ __forceinline__ void store_row(const float4 (&v)[N], float* row, int q0, int len, bool vec_ok, float rs) {
-#pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const int q = q0 + kStride * j;
-    const float4 o = make_float4(v[j].x * rs, v[j].y * rs, v[j].z * rs, v[j].w * rs);
-    if (vec_ok && kStride * (j + 1) * 4 <= len) {
-      __builtin_nontemporal_store(f32x4{o.x, o.y, o.z, o.w}, reinterpret_cast<f32x4*>(row) + q);
-    } else {
-      store_vec(row, q, len, vec_ok, o);
-    }
-  }
+  for (int j = 0; j < N; ++j) v[j] = make_float4(v[j].x * rs, v[j].y * rs, v[j].z * rs, v[j].w * rs);
+  store_row<N, kStride>(v, row, q0, len, vec_ok);
 }
 
 // exp(y) for finite y <= 0 with y*log2(e) >= -126 (the caller checks the row's
@@ -186,7 +132,7 @@ __global__ void __launch_bounds__(256) softmax_wave_kernel(RowView p) {
 #pragma unroll
   for (int k = 0; k < kRows; ++k) {
     if (r0 + k >= p.rows) continue;
-    load_row<VPL, 64>(v[k], p.x + (r0 + k) * p.stride, lane, p.len, p.vec_ok);
+    load_row<VPL, 64>(v[k], p.x + (r0 + k) * p.stride, lane, p.len, p.vec_ok, kPad);
   }
 #pragma unroll
   for (int k = 0; k < kRows; ++k) {
@@ -200,7 +146,7 @@ __global__ void __launch_bounds__(256) softmax_wave_kernel(RowView p) {
     m = asc::wave_max(m);
     mn = asc::wave_min(mn);
     const float rs = 1.0f / asc::wave_sum(exp_row(v[k], m, mn));
-    store_row<VPL, 64>(v[k], p.out + (r0 + k) * p.stride, lane, p.len, p.vec_ok, rs);
+    store_scaled<VPL, 64>(v[k], p.out + (r0 + k) * p.stride, lane, p.len, p.vec_ok, rs);
   }
 }
 
@@ -213,7 +159,7 @@ __global__ void __launch_bounds__(kThreads) softmax_block_kernel(RowView p) {
   const int t = threadIdx.x;
   const int64_t r = blockIdx.x;
   float4 v[VPT];
-  load_row<VPT, kThreads>(v, p.x + r * p.stride, t, p.len, p.vec_ok);
+  load_row<VPT, kThreads>(v, p.x + r * p.stride, t, p.len, p.vec_ok, kPad);
   float m = -INFINITY, mn = INFINITY;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -240,7 +186,7 @@ __global__ void __launch_bounds__(kThreads) softmax_block_kernel(RowView p) {
   float sum = red[2][0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) sum += red[2][w];
-  store_row<VPT, kThreads>(v, p.out + r * p.stride, t, p.len, p.vec_ok, 1.0f / sum);
+  store_scaled<VPT, kThreads>(v, p.out + r * p.stride, t, p.len, p.vec_ok, 1.0f / sum);
 }
 
 // Rows longer than the register-resident variants: three passes over the row.
@@ -253,7 +199,7 @@ __global__ void __launch_bounds__(256) softmax_long_kernel(RowView p) {
   const int nvec = (p.len + 3) / 4;
   float m = -INFINITY, mn = INFINITY;
   for (int q = t; q < nvec; q += 256) {
-    const float4 v = load_vec(row, q, p.len, p.vec_ok);
+    const float4 v = load_vec(row, q, p.len, p.vec_ok, kPad);
     m = fmaxf(m, max4(v));
     mn = fminf(mn, min4(v));
   }
@@ -268,7 +214,7 @@ __global__ void __launch_bounds__(256) softmax_long_kernel(RowView p) {
   mn = fminf(fminf(red[1][0], red[1][1]), fminf(red[1][2], red[1][3]));
   float s = 0.f;
   for (int q = t; q < nvec; q += 256) {
-    float4 v[1] = {load_vec(row, q, p.len, p.vec_ok)};
+    float4 v[1] = {load_vec(row, q, p.len, p.vec_ok, kPad)};
     s += exp_row(v, m, mn);
   }
   s = asc::wave_sum(s);
@@ -277,7 +223,7 @@ __global__ void __launch_bounds__(256) softmax_long_kernel(RowView p) {
   const float rs = 1.0f / ((red[2][0] + red[2][1]) + (red[2][2] + red[2][3]));
   float* orow = p.out + r * p.stride;
   for (int q = t; q < nvec; q += 256) {
-    float4 v[1] = {load_vec(row, q, p.len, p.vec_ok)};
+    float4 v[1] = {load_vec(row, q, p.len, p.vec_ok, kPad)};
     exp_row(v, m, mn);
     store_vec(orow, q, p.len, p.vec_ok, make_float4(v[0].x * rs, v[0].y * rs, v[0].z * rs, v[0].w * rs));
   }

@@ -183,6 +183,61 @@ def softmax_blocks(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: 
                  _stream(stream))
 
 
+# ---------------------------------------------------------------------------------- reductions, rms_norm
+
+REDUCE_OPS = {"sum": 0, "max": 1, "min": 2, "prod": 3}
+
+
+def reduce_f32(x: torch.Tensor, out: torch.Tensor, op: str, dim: Optional[int], stream: Any = None) -> None:
+    """asc2.reduce_{sum,max,min,prod} of a 1-D or 2-D float32 tensor along ``dim`` (0 or 1 of
+    a 2-D tensor) or over all elements (``dim=None``: the scalar is written to every element
+    of ``out``, as asc2.full does in test_reduce_ops.py's kernel_all)."""
+    if op not in REDUCE_OPS:
+        raise ValueError(f"unknown reduction {op!r}; expected one of {sorted(REDUCE_OPS)}")
+    for t, n in ((x, "x"), (out, "out")):
+        _contiguous(_device_tensor(t, n), n)
+        if t.dtype != torch.float32:
+            raise TypeError(f"reductions support float32, '{n}' is {t.dtype}")
+    if x.dim() == 1:
+        rows, cols = 1, x.shape[0]
+    elif x.dim() == 2:
+        rows, cols = x.shape
+    else:
+        raise ValueError("x must be 1-D or 2-D")
+    if dim is None:
+        _native.call("asc_reduce_f32", REDUCE_OPS[op], x.data_ptr(), out.data_ptr(), rows, cols, -1, out.numel(),
+                     _stream(stream))
+        return
+    if x.dim() != 2 or dim not in (0, 1):
+        raise ValueError(f"dim must be 0 or 1 of a 2-D tensor, got dim={dim} for shape {tuple(x.shape)}")
+    need = rows if dim == 1 else cols
+    if out.numel() != need:
+        raise ValueError(f"out must hold {need} elements, holds {out.numel()}")
+    _native.call("asc_reduce_f32", REDUCE_OPS[op], x.data_ptr(), out.data_ptr(), rows, cols, dim, need,
+                 _stream(stream))
+
+
+def rms_norm(x: torch.Tensor, gamma: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int,
+             epsilon: float, tile_size: Optional[int] = None, stream: Any = None) -> None:
+    """asc2.rms_norm over the first ``tile_size`` (default: all) columns of each row:
+    y = x / sqrt(mean(x^2) + epsilon) * gamma, fp32 or fp16 rows, fp32 gamma."""
+    tile = num_cols if tile_size is None else int(tile_size)
+    if num_rows < 0 or num_cols < 0 or not 0 < tile <= num_cols:
+        raise ValueError(f"invalid rms_norm launch: rows={num_rows}, cols={num_cols}, tile={tile}")
+    for t, n in ((x, "x"), (out, "out")):
+        _contiguous(_device_tensor(t, n), n)
+        if t.numel() < num_rows * num_cols:
+            raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {num_rows}x{num_cols}")
+    code = _code(x, "x", (torch.float32, torch.float16))
+    if out.dtype != x.dtype:
+        raise TypeError(f"out must be {x.dtype}, got {out.dtype}")
+    _contiguous(_device_tensor(gamma, "gamma"), "gamma")
+    if gamma.dtype != torch.float32 or gamma.numel() < tile:
+        raise ValueError(f"gamma must be float32 with at least {tile} elements")
+    _native.call("asc_rms_norm", code, x.data_ptr(), gamma.data_ptr(), out.data_ptr(), num_rows, num_cols, tile,
+                 float(epsilon), _stream(stream))
+
+
 # -------------------------------------------------------------------------------------------- matmul
 
 def _row_major_2d(t: torch.Tensor, name: str) -> int:

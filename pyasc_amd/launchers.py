@@ -108,6 +108,73 @@ def _softmax_blocks(call: KernelCall) -> None:
                            int(call.get("num_cols")), int(call.get("block_size")), call.grid, call.stream)
 
 
+# ---------------------------------------------------------------------------------- reductions, rms_norm
+
+def _reduce_name(op) -> str:
+    """The asc2 reduction passed as a ConstExpr (asc2.reduce_sum ...) -> its kernel op name."""
+    name = getattr(op, "__name__", str(op))
+    for k in ("sum", "max", "min", "prod"):
+        if name == f"reduce_{k}":
+            return k
+    raise NotImplementedError(f"no native reduction for op {name!r}")
+
+
+def _zero_offsets(offsets, what: str) -> None:
+    if any(int(o) != 0 for o in offsets):
+        raise NotImplementedError(f"{what} must be all zero (the reference tests load the whole tensor)")
+
+
+@register("kernel", ("input_ptr", "output_ptr", "reduce_dim", "input_shape", "input_offsets", "output_shape",
+                     "output_offsets", "op", "keep_dims"),
+          "python/test/asc2/operations/test_reduce_ops.py:33-41")
+def _reduce_dim(call: KernelCall) -> None:
+    x, out = call.args["input_ptr"], call.args["output_ptr"]
+    shape = [int(v) for v in call.consts["input_shape"]]
+    _zero_offsets(call.consts["input_offsets"], "input_offsets")
+    _zero_offsets(call.consts["output_offsets"], "output_offsets")
+    if len(shape) != 2:
+        raise NotImplementedError("reductions along a dim are implemented for 2-D tiles")
+    kernels.reduce_f32(_as2d(x, shape[0], shape[1]), out.reshape(-1), _reduce_name(call.consts["op"]),
+                       int(call.consts["reduce_dim"]), call.stream)
+
+
+@register("kernel_all", ("input_ptr", "output_ptr", "input_shape", "input_offsets", "output_shape", "output_offsets",
+                         "op"),
+          "python/test/asc2/operations/test_reduce_ops.py:44-52")
+def _reduce_all(call: KernelCall) -> None:
+    x, out = call.args["input_ptr"], call.args["output_ptr"]
+    shape = [int(v) for v in call.consts["input_shape"]]
+    _zero_offsets(call.consts["input_offsets"], "input_offsets")
+    _zero_offsets(call.consts["output_offsets"], "output_offsets")
+    n = 1
+    for d in shape:
+        n *= d
+    out_n = 1
+    for d in call.consts["output_shape"]:
+        out_n *= int(d)
+    kernels.reduce_f32(x.reshape(-1)[:n], out.reshape(-1)[:out_n], _reduce_name(call.consts["op"]), None,
+                       call.stream)
+
+
+@register("reduce_tile_kernel", ("x_ptr", "out_ptr", "size", "tile_size"),
+          "python/test/asc2/operations/test_reduce_ops.py:85-92")
+def _reduce_tile(call: KernelCall) -> None:
+    # max over the first tile_size elements, stored as a [1] tile
+    tile = int(call.consts["tile_size"])
+    x = call.args["x_ptr"]
+    if tile > int(call.args["size"]) or tile > x.numel():
+        raise ValueError("tile_size exceeds the tensor")
+    kernels.reduce_f32(x.reshape(-1)[:tile], call.args["out_ptr"].reshape(-1)[:1], "max", None, call.stream)
+
+
+@register("rms_norm_kernel", ("x_ptr", "gamma_ptr", "out_ptr", "num_rows", "num_cols", "epsilon", "tile_size"),
+          "python/asc/language/tile/unary_ops.py:225-237 (asc2.rms_norm; build-defined kernel)")
+def _rms_norm(call: KernelCall) -> None:
+    kernels.rms_norm(call.args["x_ptr"], call.args["gamma_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
+                     int(call.get("num_cols")), _scalar(call.args["epsilon"]), int(call.consts["tile_size"]),
+                     call.stream)
+
+
 # -------------------------------------------------------------------------------------------- matmul
 
 def mnblock_rectangles(M: int, N: int, grid: int, m_tile: int, m_tiles_per_block: int, n_tile: int,

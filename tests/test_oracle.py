@@ -355,3 +355,43 @@ def test_matmul_bias_leaky_relu_known_answer_and_tutorial_golden():
     golden = torch.where(mm >= 0, mm, mm * 0.001)
     ours = O.matmul_bias_leaky_relu(at.float().numpy(), bt.float().numpy(), bias.numpy(), 0.001)
     np.testing.assert_array_equal(ours, golden.numpy())
+
+
+# ---------------------------------------------------------------------------- reductions, rms_norm
+
+@pytest.mark.parametrize("op,torch_op", [("sum", torch.sum), ("max", torch.amax), ("min", torch.amin),
+                                         ("prod", torch.prod)])
+def test_reduce_matches_torch_goldens(op, torch_op):
+    # test_reduce_ops.py:55-82: randn * 2.0 on [64, 32], dims 0 and 1, and all elements
+    x = torch.randn(64, 32, generator=torch.Generator().manual_seed(1)) * 2.0
+    for dim in (0, 1):
+        torch.testing.assert_close(torch.from_numpy(O.reduce(x.numpy(), op, dim)), torch_op(x, dim))
+    torch.testing.assert_close(torch.from_numpy(O.reduce(x.numpy(), op, None)), torch_op(x))
+
+
+def test_reduce_exact_cases():
+    ints = np.arange(-50, 50, dtype=np.float32).reshape(10, 10)
+    np.testing.assert_array_equal(O.reduce(ints, "sum", 1), ints.sum(1))
+    np.testing.assert_array_equal(O.reduce(ints, "max", 0), ints[-1])
+    np.testing.assert_array_equal(O.reduce(ints, "min", None), np.float32(-50))
+    pw = np.array([[2.0, 0.5, 4.0], [-1.0, 8.0, 0.25]], np.float32)
+    np.testing.assert_array_equal(O.reduce(pw, "prod", 1), np.array([4.0, -2.0], np.float32))
+    nan = np.array([[1.0, np.nan, 3.0]], np.float32)
+    assert O.reduce(nan, "max", 1)[0] == 3.0  # maxNum: the non-NaN operand
+
+
+def test_rms_norm_matches_torch_and_closed_forms():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(37, 300, generator=g, dtype=torch.float64) * 3
+    gamma = torch.randn(300, generator=g, dtype=torch.float64)
+    ours = O.rms_norm_rows(x.numpy(), gamma.numpy(), 1e-6, 300)
+    ref = torch.nn.functional.rms_norm(x, [300], gamma, eps=float(np.float32(1e-6)))
+    np.testing.assert_allclose(ours, ref.numpy(), rtol=1e-12, atol=1e-14)
+    c = np.full((1, 8), 3.0)
+    np.testing.assert_allclose(O.rms_norm_rows(c, np.full(8, 2.0), 0.5, 8),
+                               np.full((1, 8), 3.0 / np.sqrt(9.0 + 0.5) * 2.0), rtol=1e-15)
+    # scale invariance with eps = 0, and untouched columns past tile_size
+    y1 = O.rms_norm_rows(x.numpy(), gamma.numpy(), 0.0, 200)
+    y2 = O.rms_norm_rows(7.0 * x.numpy(), gamma.numpy(), 0.0, 200)
+    np.testing.assert_allclose(y1[:, :200], y2[:, :200], rtol=1e-13)
+    np.testing.assert_array_equal(y1[:, 200:], x.numpy()[:, 200:])
