@@ -33,7 +33,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
@@ -86,6 +85,39 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 // Two fp32 -> packed bf16 pair, RNE (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p));
+}
+
+// MFMA operand reads from LDS are inline asm.  The compiler cannot prove that a
+// read of one ring stage does not alias the buffer_load ... lds still streaming
+// into the other stage, so with plain loads it inserts an s_waitcnt vmcnt for
+// that DMA in the middle of the step.  The kernel orders DMA and reads itself
+// (every stage is refilled only after the workgroup barrier that follows its
+// last read, and each step ends with vmcnt(0) + barrier before the stage it
+// filled is read); the asm reads carry explicit lgkmcnt waits, tied to the
+// registers they produce so that the consuming MFMA cannot move above them.
+// LDS reads complete in order, so lgkmcnt(n) after a group of reads makes all
+// but the newest n of them available.
+// (`off` must fold to a constant once the calling loops are unrolled.)
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr, int off) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off));
+  return r;
+}
+__device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t addr, int off) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off));
+  return r;
+}
+__device__ __forceinline__ void lds_wait(u32x4& r, int n) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(n));
+}
+__device__ __forceinline__ void lds_wait(u32x4 (&r)[4], int n) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "i"(n));
 }
 
 // Value of lane l^32 (v_permlane32_swap: lanes 32..63 of the first operand trade
@@ -173,14 +205,20 @@ struct FaState {
 
   // S^T = K Q^T for keys k0 .. k0+63 (two 32-key blocks).  Register r of block
   // kb then holds key k0 + 32*kb + 8*(r/4) + 4*h + r%4 for query my_q.
+  // The kKSteps operand reads of a block go out together; each MFMA waits only
+  // for its own.
   __device__ __forceinline__ void scores(const uint8_t* ks_, f32x16 (&s)[2]) const {
+    const uint32_t base = lds_addr(ks_);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = f32x16{};
+      u32x4 a[kKSteps];
+#pragma unroll
+      for (int kk = 0; kk < kKSteps; ++kk) a[kk] = lds_read_b128(base + kaddr[kk], kb * 32 * (D * 2));
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(ks_ + kb * 32 * (D * 2) + kaddr[kk]);
-        s[kb] = mfma_bf16(a, qreg[kk], s[kb]);
+        lds_wait(a[kk], kKSteps - 1 - kk);
+        s[kb] = mfma_bf16(a[kk], qreg[kk], s[kb]);
       }
     }
   }
@@ -247,24 +285,36 @@ struct FaState {
     l_part += rs;
   }
 
+  // V^T operands of d block db: for (kb, u) the rows kb*32 + u*16 + {0, 8}
+  // of the tile, four MFMA A operands of two transpose reads each.
+  __device__ __forceinline__ void vt_reads(uint32_t base, int db, u32x4 (&a)[4]) const {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x2 lo = lds_read_tr16_b64(base + vaddr[db], (kb * 32 + u * 16) * (D * 2));
+        const u32x2 hi = lds_read_tr16_b64(base + vaddr[db], (kb * 32 + u * 16 + 8) * (D * 2));
+        a[kb * 2 + u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+  }
+
   // O^T += V^T P^T; V^T comes from transpose reads of the row-major V tile.
+  // The reads of d block db+1 are in flight while block db multiplies.
   __device__ __forceinline__ void pv(const uint8_t* vs_, const u32x4 (&pb)[2][2]) {
+    const uint32_t base = lds_addr(vs_);
+    u32x4 a[2][4];
+    vt_reads(base, 0, a[0]);
 #pragma unroll
     for (int db = 0; db < kDBlocks; ++db) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint8_t* base = vs_ + (kb * 32 + u * 16) * (D * 2) + vaddr[db];
-          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(base));
-          const i16x4 hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(base + 8 * (D * 2)));
-          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
-          const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
-          const u32x4 a = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
-          acc_o[db] = mfma_bf16(a, pb[kb][u], acc_o[db]);
-        }
+      u32x4(&cur)[4] = a[db & 1];
+      if (db + 1 < kDBlocks) {
+        vt_reads(base, db + 1, a[(db + 1) & 1]);
+        lds_wait(cur, 8);  // the newest 8 reads belong to block db+1
+      } else {
+        lds_wait(cur, 0);
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc_o[db] = mfma_bf16(cur[i], pb[i >> 1][i & 1], acc_o[db]);
     }
   }
 };
@@ -379,6 +429,9 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   asm volatile("s_barrier" ::: "memory");
   f32x16 sa[2], sb[2];
   st.scores(kst0, sa);  // tile 0 is active for every wave
+  // step 0 refills kst0 with tile 2: every wave must be done reading tile 0
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
   st.mask(sa, 0);
   st.rebase(st.tile_max(sa));
   // Clean tiles need no mask and are active for every wave: all their keys are
