@@ -7,7 +7,7 @@
 // each wave 128x128 = 4x4 MFMA blocks (256 fp32 accumulators per lane):
 //   - tile-aligned shapes (M, N multiples of 256, K of 32, offsets within
 //     32 bits): the direct-to-LDS loop of gemm_direct.h -- operands go from HBM
-//     straight into four 32 KiB LDS stages, B stays row-major and its
+//     straight into five 32 KiB LDS stages, B stays row-major and its
 //     K-contiguous MFMA operand comes from LDS transpose reads;
 //   - other shapes: the register-staged loop of gemm_core.h with bounds-checked
 //     loads (zero fill), B transposed in registers, masked stores;
@@ -142,11 +142,13 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
     L.lds[1] = lds1;
     L.run(acc);
   } else {
-    // four LDS stages as distinct objects (see gemm_direct.h)
+    // the LDS stages as distinct objects (see gemm_direct.h)
     __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
+    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
     asc::gemm::GemmDirectLoop<Tr16<kBf16>> L;
     L.a = p.a;
     L.b = p.b;
@@ -160,6 +162,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
     L.lds[1] = lds1;
     L.lds[2] = lds2;
     L.lds[3] = lds3;
+    L.lds[4] = lds4;
     L.init(p.lda, p.ldb);
     L.run(p.K, acc);
   }

@@ -121,11 +121,13 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
     L.lds[1] = lds1;
     L.run(acc);
   } else {
-    // four LDS stages as distinct objects (see gemm_direct.h)
+    // the LDS stages as distinct objects (see gemm_direct.h)
     __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
+    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
     asc::gemm::GemmDirectLoop<TrI8> L;
     L.a = p.a;
     L.b = p.b;
@@ -139,6 +141,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
     L.lds[1] = lds1;
     L.lds[2] = lds2;
     L.lds[3] = lds3;
+    L.lds[4] = lds4;
     L.init(p.K, p.N);
     L.run(p.K, acc);
   }
