@@ -524,6 +524,51 @@ def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True) -> di
             "timing": "hip-graph replay" if graph else "per-launch events"}
 
 
+def launch_latency(dev, n: int = 2000) -> dict:
+    """Host time per launch of the reference-size vadd (8192 fp32, grid 16, tile 128,
+    tpb 4; test_vadd.py:31-38) on device tensors, through the asc2 surface with the
+    kernel cache, with always_compile=True (re-resolved every call), and through the
+    kernel API.  Wall time over ``n`` back-to-back launches / n: the GPU work (a few
+    microseconds) overlaps the host work, so this is the host-side launch cost."""
+    import torch
+    import pyasc_amd
+    from pyasc_amd import kernels
+    pyasc_amd.install_aliases()
+    import asc
+    import asc2
+
+    def make(**options):
+        @asc2.jit(**options)
+        def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                        tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+            raise AssertionError("kernel bodies are not executed")
+
+        return vadd_kernel
+
+    x, y = torch.rand(8192, device=dev), torch.rand(8192, device=dev)
+    out = torch.empty(8192, device=dev)
+
+    def per_launch(fn) -> float:
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    cached, fresh = make(), make(always_compile=True)
+    res = {
+        "workload": "vadd 8192 fp32, grid 16, tile 128, tpb 4, device tensors",
+        "asc2_cached_us": per_launch(lambda: cached[16](x, y, out, 8192, 128, 4)),
+        "asc2_always_compile_us": per_launch(lambda: fresh[16](x, y, out, 8192, 128, 4)),
+        "kernel_api_us": per_launch(lambda: kernels.vadd(x, y, out, 8192, 128, 4, 16)),
+    }
+    assert torch.equal(out, x + y)
+    return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in res.items()}
+
+
 def traffic_for(name: str):
     path = os.path.join(REPO, "profiles", "traffic.json")
     try:
@@ -573,6 +618,7 @@ def main() -> int:
             suite[name] = r
             del w
             torch.cuda.empty_cache()
+    latency = None if args.no_suite else launch_latency(dev)
     if args.copy_calibration:
         src = torch.empty(COPY_BYTES // 4, device=dev)
         dst = torch.empty_like(src)
@@ -602,6 +648,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "device": _native.device_info(0),
         "suite": suite,
+        "launch_latency": latency,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -11,17 +11,25 @@ Follows python/asc/runtime/jit.py:33-223 in its user-visible behaviour:
   - runtime argument types are classified as in jit.py:69-96 (TypeError for
     unsupported ones).
 Instead of compiling the body, the (name, parameter names) pair selects a
-registered native kernel (pyasc_amd.registry).
+registered native kernel (pyasc_amd.registry).  What a call resolves to is cached
+per JITFunction under the reference's cache factors (jit.py:139-186; see
+cache.py): a hit skips annotation evaluation, ConstExpr validation, argument
+classification and the registry lookup.  ``always_compile=True`` bypasses the
+cache, as it bypasses the reference's.
 """
 from __future__ import annotations
 
+import hashlib
 import inspect
-from typing import Any, Callable, Dict, List, Tuple, Union, get_args, get_origin
+import re
+from dataclasses import dataclass
+from typing import Any, Callable, Dict, FrozenSet, List, Optional, Tuple, Union, get_args, get_origin
 
 import numpy as np
 
 from ... import registry
 from ..core import ConstExpr, DataType, require_constexpr
+from .cache import get_mem_cache_key
 from .launcher import LaunchOptions, Launcher
 
 CODEGEN_OPTIONS = ("capture_exceptions", "ir_multithreading", "custom_builtins")
@@ -50,6 +58,26 @@ def _annotations(fn: Callable) -> Dict[str, Any]:
         return dict(getattr(fn, "__annotations__", {}))
 
 
+# a string annotation that could not be evaluated (e.g. `from __future__ import
+# annotations` with `asc` imported inside a function) is recognised by its text
+_CONSTEXPR_TEXT = re.compile(r"^\s*(?:[A-Za-z_][\w.]*\.)?ConstExpr\b")
+
+
+def _is_constexpr_annotation(ann_type: Any) -> bool:
+    if isinstance(ann_type, str):
+        return _CONSTEXPR_TEXT.match(ann_type) is not None
+    origin = get_origin(ann_type) or ann_type
+    return inspect.isclass(origin) and issubclass(origin, ConstExpr)
+
+
+@dataclass(frozen=True)
+class ResolvedKernel:
+    """One cached specialisation: the native kernel a call resolves to (the
+    counterpart of the reference's CompiledKernel / LaunchedKernel cache entry)."""
+    entry: registry.KernelEntry
+    cache_key: str
+
+
 class JITFunction:
 
     def __init__(self, fn: Callable, **options):
@@ -66,6 +94,13 @@ class JITFunction:
             raise RuntimeError("The following option names are unknown: " + ", ".join(sorted(unknown)))
         self.default_options: Dict[str, Any] = options
         self.launch_options = LaunchOptions()
+        self.kernel_cache: Dict[str, ResolvedKernel] = {}
+        self._const_names: Optional[FrozenSet[str]] = None  # ConstExpr parameters, from the annotations
+        self._hash: Optional[str] = None
+        # plain positional calls can skip inspect.Signature.bind
+        self._positional_only_call = all(
+            p.kind in (inspect.Parameter.POSITIONAL_ONLY, inspect.Parameter.POSITIONAL_OR_KEYWORD)
+            for p in self.signature.parameters.values())
         self.__doc__ = fn.__doc__
         self.__name__ = fn.__name__
 
@@ -125,9 +160,8 @@ class JITFunction:
         constexprs: Dict[str, Any] = {}
         for name, value in args.items():
             ann_type = annotations.get(name, object)
-            origin = get_origin(ann_type) or ann_type
-            if inspect.isclass(origin) and issubclass(origin, ConstExpr):
-                ann_args = get_args(ann_type)
+            if _is_constexpr_annotation(ann_type):
+                ann_args = () if isinstance(ann_type, str) else get_args(ann_type)
                 if len(ann_args) != 0:
                     require_constexpr(value, *ann_args, arg_name=name)
                 constexprs[name] = ConstExpr.unwrap(value)
@@ -136,7 +170,7 @@ class JITFunction:
         return runtime_args, constexprs
 
     def bind(self, *args, **kwargs) -> Tuple[Dict[str, Any], Dict[str, Any], Dict[str, Any]]:
-        """(runtime args, constexprs, options) of one call, without launching."""
+        """(runtime args, constexprs, options) of one call, validated, without launching."""
         kwargs = {**self.default_options, **kwargs}
         options = {k: kwargs.pop(k) for k in list(kwargs) if k in self.get_config_keywords()}
         call_args = self.signature.bind(*args, **kwargs)
@@ -146,10 +180,99 @@ class JITFunction:
             self.get_arg_type(value)
         return runtime_args, constexprs, options
 
-    def _run(self, *args, **kwargs) -> None:
+    # ------------------------------------------------------------------------------------ cache
+
+    @property
+    def cache_key(self) -> str:
+        """Identity of the decorated function (source text and qualified name), as the
+        reference's Function.cache_key (python/asc/codegen/function.py:63-87)."""
+        if self._hash is None:
+            try:
+                src = inspect.getsource(self.fn)
+            except (OSError, TypeError):
+                src = ""
+            self._hash = hashlib.sha256(f"{self.fn.__module__}.{self.fn.__qualname__}\n{src}".encode()).hexdigest()
+        return self._hash
+
+    @staticmethod
+    def arg_kind(value: Any) -> str:
+        """``kind:dtype`` of a runtime argument, the reference's per-argument cache factor
+        (jit.py:151-152); raises TypeError like get_arg_type for unsupported types."""
+        cls = value.__class__
+        if cls is bool:
+            return "plain:int8"
+        if cls is int:
+            return "plain:int32"
+        if cls is float:
+            return "plain:float32"
+        dtype = getattr(value, "dtype", None)
+        dim = getattr(value, "dim", None)
+        if dtype is not None and callable(dim) and cls.__module__.startswith("torch"):
+            name = str(dtype)
+            return ("plain:" if dim() == 0 else "pointer:") + (name[6:] if name.startswith("torch.") else name)
+        t = JITFunction.get_arg_type(value)
+        return f"{t.kind}:{t.dtype}"
+
+    def _gen_cache_factors(self, arg_kinds: Dict[str, str], constexprs: Dict[str, Any],
+                           options: Dict[str, Any]) -> str:
+        """Cache factors in the reference's order (jit.py:139-156): options, ConstExpr
+        values, argument kinds/dtypes, function name."""
+        factors = [
+            ";".join(f"{k}={options[k]!r}" for k in sorted(options) if k not in LAUNCH_OPTIONS),
+            ";".join(f"{name}={val!r}" for name, val in constexprs.items()),
+            ";".join(f"{name}={kind}" for name, kind in arg_kinds.items()),
+            f"fn_name={self.fn_name}",
+        ]
+        return "__".join(factors)
+
+    def _constexpr_names(self) -> FrozenSet[str]:
+        if self._const_names is None:
+            ann = _annotations(self.fn)
+            self._const_names = frozenset(n for n in self.params if _is_constexpr_annotation(ann.get(n, object)))
+        return self._const_names
+
+    def _fast_bind(self, args: tuple, kwargs: Dict[str, Any]) -> Tuple[Dict[str, Any], Dict[str, Any], Dict[str, Any]]:
+        """Binding and ConstExpr split without validation (validation runs on a cache miss)."""
+        if self.default_options:
+            kwargs = {**self.default_options, **kwargs}
+        options = {k: kwargs.pop(k) for k in list(kwargs) if k in self.get_config_keywords()} if kwargs else {}
+        if not kwargs and self._positional_only_call and len(args) == len(self.params):
+            bound = dict(zip(self.params, args))
+        else:
+            call_args = self.signature.bind(*args, **kwargs)
+            call_args.apply_defaults()
+            bound = dict(call_args.arguments)
+        const_names = self._constexpr_names()
+        runtime_args: Dict[str, Any] = {}
+        constexprs: Dict[str, Any] = {}
+        for name, value in bound.items():
+            if name in const_names:
+                constexprs[name] = ConstExpr.unwrap(value)
+            else:
+                runtime_args[name] = value
+        return runtime_args, constexprs, options
+
+    def resolve(self, *args, **kwargs) -> Tuple[ResolvedKernel, Dict[str, Any], Dict[str, Any]]:
+        """(cached specialisation, runtime args, constexprs) of one call, without launching."""
+        if kwargs.get("always_compile", self.default_options.get("always_compile", False)):
+            # no lookup and no store (jit.py:164-186): resolve from scratch
+            runtime_args, constexprs, _ = self.bind(*args, **kwargs)
+            return ResolvedKernel(registry.lookup(self.fn_name, self.params), ""), runtime_args, constexprs
+        runtime_args, constexprs, options = self._fast_bind(args, dict(kwargs))
+        arg_kinds = {name: self.arg_kind(value) for name, value in runtime_args.items()}
+        key = get_mem_cache_key(self._gen_cache_factors(arg_kinds, constexprs, options))
+        hit = self.kernel_cache.get(key)
+        if hit is not None:
+            return hit, runtime_args, constexprs
+        # miss: full validation (ConstExpr types, argument types), then the registry
         runtime_args, constexprs, _ = self.bind(*args, **kwargs)
-        entry = registry.lookup(self.fn_name, self.params)
-        Launcher(self.launch_options).run(entry, self.fn_name, runtime_args, constexprs)
+        resolved = ResolvedKernel(registry.lookup(self.fn_name, self.params), key)
+        self.kernel_cache[key] = resolved
+        return resolved, runtime_args, constexprs
+
+    def _run(self, *args, **kwargs) -> None:
+        resolved, runtime_args, constexprs = self.resolve(*args, **kwargs)
+        Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs)
 
 
 def jit(fn: Callable = None, **options):

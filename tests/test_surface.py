@@ -183,3 +183,110 @@ def test_launcher_mnblock_rectangles_merge():
 def test_ceildiv_and_dtypes():
     assert asc.ceildiv(8192, 128) == 64 and asc.ceildiv(1, 16) == 1
     assert asc.float16.to_torch() == torch.float16 and asc.bfloat16.is_float() and asc.int8.is_int()
+
+
+# ---------------------------------------------------------------------------------- kernel cache
+# The reference caches what a call compiles to under its cache factors and skips the
+# cache with always_compile (python/asc/runtime/jit.py:139-186); here the cached
+# value is the resolved native kernel.
+
+def _cached_vadd(**options):
+    @asc2.jit(**options)
+    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                    tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+        pass
+
+    return vadd_kernel
+
+
+@pytest.fixture
+def lookups(monkeypatch):
+    seen = []
+    real = registry.lookup
+
+    def counting(name, params):
+        seen.append(name)
+        return real(name, params)
+
+    monkeypatch.setattr(registry, "lookup", counting)
+    return seen
+
+
+def test_cache_hit_skips_resolution(recorded, lookups):
+    k = _cached_vadd()
+    x = torch.zeros(64)
+    for _ in range(3):
+        k[2](x, x, x, 64, 8, 4)
+    assert len(lookups) == 1 and len(k.kernel_cache) == 1
+    assert [r[3] for r in recorded] == [{"tile_size": 8, "tile_per_block": 4}] * 3
+    assert all(r[0] is recorded[0][0] for r in recorded)
+    # new specialisations: a ConstExpr value, an argument dtype, a by-value type, an option
+    k[2](x, x, x, 64, 16, 4)
+    k[2](x.double(), x, x, 64, 8, 4)
+    k[2](x, x, x, torch.tensor(64), 8, 4)
+    k[2](x, x, x, 64, 8, 4, debug=True)
+    assert len(k.kernel_cache) == 5 and len(lookups) == 5
+    # the launch options are not part of the key (LaunchOptions are not cache factors)
+    k[7](x, x, x, 64, 8, 4)
+    assert len(k.kernel_cache) == 5 and recorded[-1][4].core_num == 7
+
+
+def test_always_compile_bypasses_cache(recorded, lookups):
+    k = _cached_vadd(always_compile=True)
+    x = torch.zeros(64)
+    k[2](x, x, x, 64, 8, 4)
+    k[2](x, x, x, 64, 8, 4)
+    assert len(lookups) == 2 and k.kernel_cache == {}
+    k2 = _cached_vadd()
+    k2[2](x, x, x, 64, 8, 4)
+    k2[2](x, x, x, 64, 8, 4, always_compile=True)  # per-call option: resolved afresh, nothing stored
+    assert len(lookups) == 4 and len(k2.kernel_cache) == 1
+
+
+def test_cache_miss_still_validates(recorded):
+    k = _cached_vadd()
+    x = torch.zeros(64)
+    k[2](x, x, x, 64, 8, 4)
+    with pytest.raises(RuntimeError, match="ConstExpr"):
+        k[2](x, x, x, 64, 8.0, 4)  # ConstExpr[int] given a float: a new key, validated
+    with pytest.raises(TypeError):
+        k[2](x, x, x, "64", 8, 4)  # unsupported runtime argument type
+    assert len(k.kernel_cache) == 1
+
+
+def test_cache_key_components():
+    from pyasc_amd.asc.runtime import cache
+    k = _cached_vadd()
+    factors = k._gen_cache_factors({"x_ptr": "pointer:float32", "size": "plain:int32"}, {"tile_size": 8},
+                                   {"debug": True, "core_num": 3})
+    assert factors == "debug=True__tile_size=8__x_ptr=pointer:float32;size=plain:int32__fn_name=vadd_kernel"
+    assert cache.get_mem_cache_key(factors) == cache.hexdigest(f"{cache.library_key()}__{factors}".encode())
+    assert k.cache_key == _cached_vadd().cache_key != vadd_kernel.cache_key
+    assert JITFunction.arg_kind(torch.zeros(3, dtype=torch.bfloat16)) == "pointer:bfloat16"
+    assert JITFunction.arg_kind(torch.tensor(1.5)) == "plain:float32"
+    assert JITFunction.arg_kind(np.zeros(3, np.int8)) == "pointer:int8"
+    assert JITFunction.arg_kind(np.float16(1)) == "plain:float16"
+    assert JITFunction.arg_kind(True) == "plain:int8"
+
+
+def test_string_annotations_with_local_import(recorded):
+    # `from __future__ import annotations` with asc imported inside a function: the
+    # annotation strings cannot be evaluated in the module globals, ConstExpr is
+    # still recognised by its text
+    src = (
+        "from __future__ import annotations\n"
+        "def make():\n"
+        "    import asc, asc2\n"
+        "    @asc2.jit\n"
+        "    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress,\n"
+        "                    size: int, tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):\n"
+        "        pass\n"
+        "    return vadd_kernel\n")
+    ns = {"__name__": "local_import_kernels"}
+    exec(compile(src, "local_import_kernels", "exec"), ns)
+    k = ns["make"]()
+    x = torch.zeros(64)
+    k[2](x, x, x, 64, 8, 4)
+    k[2](x, x, x, 64, 8, 4, always_compile=True)
+    assert [r[3] for r in recorded] == [{"tile_size": 8, "tile_per_block": 4}] * 2
+    assert list(recorded[0][2]) == ["x_ptr", "y_ptr", "out_ptr", "size"]
