@@ -4,8 +4,10 @@
 // head_dim 128, scale 1/sqrt(128), causal and non-causal).
 //
 // Design (gfx950, wave64, MFMA 32x32x16 bf16):
-//  - A workgroup owns 128 queries of one (batch, head): 4 waves x 32 queries.
-//    Keys/values stream through LDS in tiles of 64, double-buffered.
+//  - A wave owns 32 queries of one (batch, head); a workgroup has 4 waves
+//    (128 queries; causal and head_dim 64) or 8 waves (256 queries; non-causal
+//    head_dim 128).  Keys/values stream through LDS in tiles of 64,
+//    double-buffered.
 //  - Each wave computes S^T = K Q^T (keys x queries) instead of S = Q K^T:
 //    in the MFMA result layout a lane then holds ONE query column and 16 keys
 //    per 32x32 block, so the online-softmax max/sum of a query live in two
@@ -34,10 +36,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int BQ = 32 * kWaves;  // queries per workgroup
-constexpr int BKV = 64;          // keys per LDS tile
+constexpr int BKV = 64;  // keys per LDS tile
 
 struct FaArgs {
   const uint16_t* q;
@@ -133,8 +132,9 @@ __device__ __forceinline__ float other_half(float v) {
 // the running max is moved; bounds exp2 values by 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-// Per-wave state of the attention kernel (a wave owns 32 queries).
-template <int D>
+// Per-wave state of the attention kernel (a wave owns 32 queries; a workgroup
+// of kWaves waves owns 32*kWaves).
+template <int D, int kWaves>
 struct FaState {
   static constexpr int kChunks = D / 8;           // 16-byte chunks per row
   static constexpr int kTileBytes = BKV * D * 2;  // one K or V tile
@@ -147,7 +147,7 @@ struct FaState {
   int q0, S, my_q, wave_qmax, causal;
   float scale_log2;
   __amdgpu_buffer_rsrc_t rsrc_k, rsrc_v;
-  int voff_k[4], voff_v;
+  int voff_k[4], voff_v;  // voff_k[i]: this wave's i-th K load (kLoadsPerWave <= 4)
   // Per-lane LDS read offsets, loop-invariant: the K swizzle of row kb*32+col
   // equals that of row col, and the V swizzle of row r0+j (r0 % 4 == 0) equals
   // that of row j, so every other term of a read address is an immediate.
@@ -168,9 +168,13 @@ struct FaState {
     rsrc_v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Vh), static_cast<short>(0), bytes, 0x00020000);
     constexpr int kLanesPerRow = 64 / kRowsPerLoad;
     const int rr = lane / kLanesPerRow, pos = lane % kLanesPerRow;
+    static_assert(kLoadsPerWave >= 1 && kLoadsPerWave <= 4, "K load offsets");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // the K swizzle depends on (row mod 16) = kRowsPerLoad*(R mod 4) + rr
-      const int row = kRowsPerLoad * i + rr;
+    for (int i = 0; i < kLoadsPerWave; ++i) {
+      // the K swizzle depends on (row mod 16) = kRowsPerLoad*(R mod 4) + rr; indexing
+      // by the load number keeps the array in registers whatever the wave count
+      const int R = wave * kLoadsPerWave + i;
+      const int row = kRowsPerLoad * (R & 3) + rr;
       voff_k[i] = rr * (D * 2) + ((pos ^ kswz<D>(row)) << 4);
     }
     voff_v = rr * (D * 2) + ((pos ^ vswz<D>(rr)) << 4);
@@ -196,7 +200,7 @@ struct FaState {
       const int roff = (k0 + kRowsPerLoad * R) * (D * 2);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(kIsV ? rsrc_v : rsrc_k,
                                                (__attribute__((address_space(3))) void*)(dst + R * 1024), 16,
-                                               (kIsV ? voff_v : voff_k[R & 3]) + roff, 0, 0, 0);
+                                               (kIsV ? voff_v : voff_k[i]) + roff, 0, 0, 0);
     }
   }
 
@@ -326,8 +330,8 @@ struct FaState {
 // tile j+1, and the P.V MFMAs of tile j with the max of tile j+1.  kGuard
 // false (a clean step): tile j+1 exists, every wave is active for tiles j and
 // j+1, and tile j+1 needs no mask -- the caller guarantees it.
-template <int D, bool kGuard>
-__device__ __forceinline__ void fa_step(FaState<D>& st, int j, int n_tiles, uint8_t* k_load, uint8_t* v_load,
+template <int D, int kWaves, bool kGuard>
+__device__ __forceinline__ void fa_step(FaState<D, kWaves>& st, int j, int n_tiles, uint8_t* k_load, uint8_t* v_load,
                                         const uint8_t* k_next, const uint8_t* v_cur, f32x16 (&sc)[2],
                                         f32x16 (&sn)[2]) {
   const int k1 = (j + 1) * BKV;
@@ -349,12 +353,22 @@ __device__ __forceinline__ void fa_step(FaState<D>& st, int j, int n_tiles, uint
   if (act_next) st.rebase(mt);
 }
 
-template <int D>
-__global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
-  constexpr int kTileBytes = FaState<D>::kTileBytes;
-  constexpr int kChunks = FaState<D>::kChunks;
-  constexpr int kKSteps = FaState<D>::kKSteps;
-  constexpr int kDBlocks = FaState<D>::kDBlocks;
+// kWaves = 4: two workgroups per CU, the two waves of a SIMD come from different
+// workgroups and drift apart.  kWaves = 8: one workgroup of 256 queries per CU,
+// each K/V tile streamed once for twice the queries (half the DMA per query);
+// the two waves of a SIMD belong to one workgroup and would run their exp2 and
+// MFMA phases in lockstep, so waves 0-3 run at raised priority and their SIMD
+// partners fill in behind them (non-causal +3.6% over kWaves = 4; causal is
+// better with the finer 128-query blocks).
+template <int D, int kWaves>
+__global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs p) {
+  using St = FaState<D, kWaves>;
+  constexpr int kTileBytes = St::kTileBytes;
+  constexpr int kChunks = St::kChunks;
+  constexpr int kKSteps = St::kKSteps;
+  constexpr int kDBlocks = St::kDBlocks;
+  constexpr int kThreads = kWaves * 64;
+  constexpr int BQ = 32 * kWaves;  // queries per workgroup
   // K and V rings of two stages each, as distinct objects, so the compiler can
   // tell that loads into one stage do not alias reads of another.  K runs one
   // tile ahead of V.
@@ -363,9 +377,10 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t vst0[kTileBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vst1[kTileBytes];
 
-  FaState<D> st;
+  St st;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  if (kWaves == 8 && (tid >> 6) < 4) __builtin_amdgcn_s_setprio(1);
   st.lane = lane;
   st.wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   st.col = lane & 31;  // query column within the wave's 32
@@ -441,23 +456,25 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   const int n_clean = p.causal ? min(q0 / BKV, S / BKV) : S / BKV;
   int j = 0;
   for (; j + 2 < n_clean; j += 2) {
-    fa_step<D, false>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
-    fa_step<D, false>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
+    fa_step<D, kWaves, false>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
+    fa_step<D, kWaves, false>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
   }
   for (; j < n_tiles; j += 2) {
-    fa_step<D, true>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
-    if (j + 1 < n_tiles) fa_step<D, true>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
+    fa_step<D, kWaves, true>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
+    if (j + 1 < n_tiles) fa_step<D, kWaves, true>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
   }
 
   // ---- epilogue: O = O^T / l, transposed through LDS (the K ring, free after
   //      the last step's barrier) into row-major bf16.  Lane holds query my_q
   //      and, for d block db and register r, d = 32*db + 8*(r/4) + 4*h + r%4.
-  //      Rows 0..63 of the block go to kst0, rows 64..127 to kst1.
+  //      Block rows 0..63 go to kst0, 64..127 to kst1, 128..191 to vst0,
+  //      192..255 to vst1 (all four stages are free after the last barrier).
   const float l_run = st.l_part + other_half(st.l_part);
   const float m_run = st.m_run;
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
   {
-    uint8_t* os_ = wave < 2 ? kst0 : kst1;
+    const int sg = wave >> 1;
+    uint8_t* os_ = sg == 0 ? kst0 : sg == 1 ? kst1 : sg == 2 ? vst0 : vst1;
     const int row = (wave & 1) * 32 + col;
 #pragma unroll
     for (int db = 0; db < kDBlocks; ++db) {
@@ -480,7 +497,8 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   for (int i = 0; i < BQ * kChunks / kThreads; ++i) {
     const int c = tid + kThreads * i;
     const int row = c / kChunks, ch = c % kChunks;
-    const uint8_t* os_ = row < 64 ? kst0 : kst1;
+    const int sg = row >> 6;
+    const uint8_t* os_ = sg == 0 ? kst0 : sg == 1 ? kst1 : sg == 2 ? vst0 : vst1;
     const int q = q0 + row;
     if (q < S) {
       *reinterpret_cast<u32x4*>(Oh + static_cast<int64_t>(q) * D + ch * 8) =
@@ -489,10 +507,13 @@ __global__ void __launch_bounds__(kThreads, 2) fa_fwd_kernel(FaArgs p) {
   }
 }
 
-template <int D>
-int32_t launch(const FaArgs& p, hipStream_t stream) {
+template <int D, int kWaves>
+int32_t launch(FaArgs p, hipStream_t stream) {
+  constexpr int BQ = 32 * kWaves;
+  p.n_qblocks = static_cast<int>((p.seq + BQ - 1) / BQ);
   const int64_t blocks = p.heads_total * p.n_qblocks;
-  hipLaunchKernelGGL(fa_fwd_kernel<D>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((fa_fwd_kernel<D, kWaves>), dim3(static_cast<uint32_t>(blocks)), dim3(kWaves * 64), 0, stream,
+                     p);
   return asc::check_launch("asc_flash_attention_fwd_bf16");
 }
 
@@ -523,9 +544,9 @@ extern "C" int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k, co
   p.lse = lse;
   p.heads_total = batch * heads;
   p.seq = static_cast<int>(seq_len);
-  p.n_qblocks = static_cast<int>((seq_len + BQ - 1) / BQ);
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.causal = causal ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return head_dim == 128 ? launch<128>(p, s) : launch<64>(p, s);
+  if (head_dim == 64) return launch<64, 4>(p, s);
+  return p.causal ? launch<128, 4>(p, s) : launch<128, 8>(p, s);
 }
