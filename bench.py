@@ -378,6 +378,21 @@ class Matmul(Workload):
             cfg.update({"out": "f32", "epilogue": "leaky_relu(acc + bias[n], 0.001)"})
         return cfg
 
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        rows = 1024  # a row band of A against all of B: 1/8 of the FLOPs of the full product
+        td = getattr(torch, self.dt)
+        g = torch.Generator().manual_seed(2)
+        a = (torch.randn(rows, self.n, generator=g) / math.sqrt(self.n)).to(td)
+        b = (torch.randn(self.n, self.n, generator=g) / math.sqrt(self.n)).to(td)
+        secs = _time_cpu(lambda: cpu_golden.matmul(a, b), budget_s=20.0)
+        return {"value": round(2.0 * rows * self.n * self.n / secs / 1e12, 4), "unit": "TFLOP/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"a.to(float32) @ b.to(float32) (python/test/asc2/kernels/test_matmul_tiled.py:49) on "
+                          f"rows 0..{rows - 1} of A ({rows}x{self.n}x{self.n}), median of up to 5 runs after 1 "
+                          "warm-up", "seconds_per_call": secs}
+
 
 class MatmulI8(Workload):
     bound, unit, dtype, kernel_hint = "mfma", "TOPS", "int8", "gemm_i8"
@@ -405,6 +420,22 @@ class MatmulI8(Workload):
     def config(self) -> dict:
         return {"workload": self.name, "M": self.M, "N": self.N, "K": self.K, "accumulate": "int32 (exact)",
                 "epilogue": "fp16(fp32(acc) * scale[n])", "input": "int8 uniform[-127,127], seed 3"}
+
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        rows = 128  # a row band: 1/32 of the full product's operations
+        g = torch.Generator().manual_seed(3)
+        a = torch.randint(-127, 128, (rows, self.K), dtype=torch.int8, generator=g)
+        b = torch.randint(-127, 128, (self.K, self.N), dtype=torch.int8, generator=g)
+        scale = torch.rand(self.N, generator=g) * 0.009 + 0.001
+        secs = _time_cpu(lambda: cpu_golden.dequant(cpu_golden.matmul_i8(a, b), scale), budget_s=20.0)
+        return {"value": round(2.0 * rows * self.N * self.K / secs / 1e12, 4), "unit": "TOPS",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"(a.to(int32) @ b.to(int32)) then (acc.float() * scale).half() "
+                          f"(test_matmul_iterate_all.py:116, test_matmul_quant.py dequant) on rows 0..{rows - 1} "
+                          f"of A ({rows}x{self.N}x{self.K}), median of up to 5 runs after 1 warm-up",
+                "seconds_per_call": secs}
 
 
 class FlashAttention(Workload):
@@ -434,6 +465,26 @@ class FlashAttention(Workload):
         return {"workload": self.name, "batch": self.B, "heads": self.H, "seq_len": self.S, "head_dim": self.D,
                 "causal": self.causal, "sm_scale": 1 / math.sqrt(self.D), "input": "bf16 randn, seed 4",
                 "flop_convention": "4*B*H*S^2*D, halved for causal"}
+
+    def cpu_baseline(self):
+        import torch
+        from oracle import cpu_golden
+        heads = 2  # (batch, head) slices, each the full S x S problem
+        g = torch.Generator().manual_seed(4)
+        q, k, v = [torch.randn(heads, self.S, self.D, generator=g).to(torch.bfloat16) for _ in range(3)]
+        scale = 1 / math.sqrt(self.D)
+
+        def run():
+            for i in range(heads):
+                cpu_golden.attention(q[i], k[i], v[i], scale, self.causal)
+
+        secs = _time_cpu(run, budget_s=20.0)
+        work = heads * 4.0 * self.S * self.S * self.D * (0.5 if self.causal else 1.0)
+        return {"value": round(work / secs / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+                "kind": "port",
+                "sample": f"fp32 softmax((q @ k.T) * scale [+ causal mask]) @ v per (batch, head) slice on {heads} "
+                          f"slices of S={self.S}, D={self.D}, same FLOP convention, median of up to 5 runs after 1 "
+                          "warm-up", "seconds_per_call": secs}
 
 
 WORKLOADS = {
@@ -587,6 +638,8 @@ def main() -> int:
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time with per-launch event pairs, no HIP graph")
+    ap.add_argument("--cpu-all", action="store_true",
+                    help="also time the CPU baseline of every suite workload (adds a few minutes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -615,6 +668,8 @@ def main() -> int:
             r = measure(w, max(5, args.steps // 2), max(2, args.warmup // 2), dev, graph=not args.no_graph)
             r["roofline"] = {"bound": w.bound, "achieved": r["value"], "peak": w.peak, "unit": w.unit,
                              "frac": r["value"] / w.peak, "traffic": traffic_for(w.name)}
+            if args.cpu_all and not args.no_cpu:
+                r["cpu_baseline"] = w.cpu_baseline()
             suite[name] = r
             del w
             torch.cuda.empty_cache()
