@@ -52,6 +52,7 @@ typedef void* asc_stream_t; /* hipStream_t */
 #define ASC_DT_BFLOAT16 2
 #define ASC_DT_INT32 3
 #define ASC_DT_INT8 4
+#define ASC_DT_INT16 5
 
 /* ---- runtime / platform --------------------------------------------------
  * Replaces rt_wrapper.cpp's device queries (GetDeviceInfoWrapper,
@@ -236,6 +237,71 @@ int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k,
                                      int64_t seq_len, int32_t head_dim,
                                      float sm_scale, int32_t causal,
                                      asc_stream_t stream);
+
+/* ---- element-wise tile operations ------------------------------------------------
+ * The generic kernels of the reference's operation tests, one op per launch:
+ *   unary   kernel(x_ptr, z_ptr, block_length, op)
+ *             python/test/asc2/operations/test_unary_ops.py:35-40
+ *   binary  kernel(x_ptr, y_ptr, z_ptr, block_length, fmt, op)
+ *             python/test/asc2/operations/test_binary_ops.py:24-38
+ *   where   where_kernel(x_ptr, y_ptr, z_ptr, op), where_scalar_kernel(x_ptr, scalar, z_ptr, op)
+ *             python/test/asc2/operations/test_where.py:18-27,48-55
+ * Op semantics: python/asc/language/tile/{unary_ops,binary_ops}.py; a scalar
+ * operand takes the tile's dtype (utils.py:73-94).  16-bit floats compute in
+ * fp32 and round once (RNE); integers wrap; integer div truncates (x / 0 = 0);
+ * float max/min propagate NaN and order -0 below +0 (arith.maximumf /
+ * minimumf, IEEE 754-2019).  n elements, contiguous. */
+#define ASC_UNARY_ABS 0
+#define ASC_UNARY_CEIL 1
+#define ASC_UNARY_COS 2
+#define ASC_UNARY_COSH 3
+#define ASC_UNARY_ERF 4
+#define ASC_UNARY_EXP 5
+#define ASC_UNARY_EXP2 6
+#define ASC_UNARY_FLOOR 7
+#define ASC_UNARY_LOG 8
+#define ASC_UNARY_LOG2 9
+#define ASC_UNARY_NEGATIVE 10
+#define ASC_UNARY_RELU 11
+#define ASC_UNARY_RSQRT 12
+#define ASC_UNARY_SIN 13
+#define ASC_UNARY_SINH 14
+#define ASC_UNARY_SQRT 15
+#define ASC_UNARY_TAN 16
+#define ASC_UNARY_TANH 17
+/* out[i] = op(x[i]), fp32 (libm-accurate; rsqrt is 1 / sqrt, relu maps negative to +0). */
+int32_t asc_unary_f32(int32_t op, const float* x, float* out, int64_t n,
+                      asc_stream_t stream);
+
+#define ASC_BIN_ADD 0
+#define ASC_BIN_SUB 1
+#define ASC_BIN_MUL 2
+#define ASC_BIN_DIV 3
+#define ASC_BIN_MAXIMUM 4
+#define ASC_BIN_MINIMUM 5
+#define ASC_BIN_LEFT_SHIFT 6  /* integer dtypes, scalar amount in [0, bits) */
+#define ASC_BIN_RIGHT_SHIFT 7 /* arithmetic */
+/* out[i] = op(a, b) with (a, b) = (x[i], y[i]) for mode 0, (x[i], s) for mode 1,
+ * (s, y[i]) for mode 2; s is scalar_f for float dtypes (rounded to fp32, then to
+ * the element type), scalar_i for integer dtypes (wrapped).  dtype:
+ * ASC_DT_FLOAT32 / FLOAT16 / BFLOAT16 / INT32 / INT16. */
+int32_t asc_binary(int32_t op, int32_t dtype, const void* x, const void* y,
+                   void* out, int64_t n, int32_t mode, double scalar_f,
+                   int64_t scalar_i, asc_stream_t stream);
+
+#define ASC_CMP_EQ 0
+#define ASC_CMP_NE 1
+#define ASC_CMP_GT 2
+#define ASC_CMP_GE 3
+#define ASC_CMP_LT 4
+#define ASC_CMP_LE 5
+/* mode 0: out[i] = cmp(x[i], y[i]) ? x[i] : y[i];
+ * mode 1: out[i] = cmp(x[i], s) ? true_value : false_value (s, true_value and
+ * false_value converted to the element type as for asc_binary).  Same dtypes. */
+int32_t asc_where_cmp(int32_t cmp, int32_t dtype, const void* x, const void* y,
+                      void* out, int64_t n, int32_t mode, double scalar_f,
+                      int64_t scalar_i, double true_value, double false_value,
+                      asc_stream_t stream);
 
 #ifdef __cplusplus
 }

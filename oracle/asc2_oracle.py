@@ -34,6 +34,12 @@ How each function is pinned (tests/test_oracle.py):
                   integer-valued sums (exact), products of powers of two (exact).
   rms_norm        torch.nn.functional.rms_norm in float64, constant rows (closed
                   form c / sqrt(c^2 + eps) * gamma), scale invariance.
+  tile ops        torch's add / sub / mul / div / maximum / minimum / shifts on
+  (binary,        every dtype with signed-zero, NaN, infinity and integer-extreme
+  unary, where)   pairs (bit-exact; NaN compared as NaN); hand known answers for
+                  integer x / 0, min / -1, shifts and IEEE 754-2019 max/min ties;
+                  torch's unary functions in float64 rounded once; torch.where over
+                  torch's comparisons (the where tests' goldens).
 Every function here has at least one such check; none is "parity unpinned".
 """
 from __future__ import annotations
@@ -97,7 +103,8 @@ def _from_f32(v: np.ndarray, dtype: str) -> np.ndarray:
     """RNE from float32 to the element type (bfloat16 as uint16 bit patterns)."""
     if dtype == "bfloat16":
         return f32_to_bf16_bits(v)
-    return np.asarray(v, dtype=np.float32).astype(np.float16 if dtype == "float16" else np.float32)
+    with np.errstate(over="ignore"):  # beyond the float16 range rounds to inf
+        return np.asarray(v, dtype=np.float32).astype(np.float16 if dtype == "float16" else np.float32)
 
 
 def leaky_relu_elements(x: np.ndarray, alpha: float, dtype: str) -> np.ndarray:
@@ -321,6 +328,122 @@ def dequant_reference_golden(acc: np.ndarray, scale: np.ndarray) -> np.ndarray:
     with np.errstate(over="ignore"):
         g = acc.astype(np.float16)
         return (g.astype(np.float32) * trunc19(scale).reshape(1, -1)).astype(np.float16)
+
+
+# ---------------------------------------------------------------------- element-wise tile operations
+
+def _erf64(v: np.ndarray) -> np.ndarray:
+    from scipy.special import erf
+    return erf(v)
+
+
+_UNARY_F64 = {
+    "abs": np.abs, "ceil": np.ceil, "cos": np.cos, "cosh": np.cosh, "erf": _erf64, "exp": np.exp, "exp2": np.exp2,
+    "floor": np.floor, "log": np.log, "log2": np.log2, "negative": np.negative,
+    "relu": lambda v: np.where(v < 0, 0.0, v),  # negative -> +0; -0 and NaN pass through (torch.relu)
+    "rsqrt": lambda v: 1.0 / np.sqrt(v), "sin": np.sin, "sinh": np.sinh, "sqrt": np.sqrt, "tan": np.tan,
+    "tanh": np.tanh,
+}
+
+
+def unary_f32(x: np.ndarray, op: str) -> np.ndarray:
+    """One asc2 unary op on a float32 tile (python/asc/language/tile/unary_ops.py;
+    python/test/asc2/operations/test_unary_ops.py:9-28): the exact value (fp64)
+    rounded once to float32."""
+    with np.errstate(all="ignore"):
+        return _UNARY_F64[op](np.asarray(x, dtype=np.float32).astype(np.float64)).astype(np.float32)
+
+
+_INT_BITS = {"int32": 32, "int16": 16}
+
+
+def _wrap(v: np.ndarray, dtype: str) -> np.ndarray:
+    bits = _INT_BITS[dtype]
+    u = np.asarray(v, dtype=np.int64).astype(np.uint64) & np.uint64((1 << bits) - 1)
+    signed = u.astype(np.int64) - ((u >> np.uint64(bits - 1)) & np.uint64(1)).astype(np.int64) * (1 << bits)
+    return signed.astype(np.int32 if bits == 32 else np.int16)
+
+
+def binary_elements(x: np.ndarray, y: np.ndarray, op: str, dtype: str) -> np.ndarray:
+    """One asc2 binary op on equal-shape operands of one element type
+    (python/asc/language/tile/binary_ops.py:110-175; a scalar operand is broadcast
+    by the caller after conversion to the tile's dtype, utils.py:73-94).
+    Floats: computed in float32, rounded once (RNE) to the element type (bfloat16
+    as uint16 bit patterns); maximum/minimum are IEEE 754-2019 maximum/minimum
+    (arith.maximumf/minimumf): NaN propagates, -0 < +0.  Integers: two's-complement wrap,
+    div truncates toward zero with x / 0 = 0, shifts are shl / arithmetic shr."""
+    if dtype in _INT_BITS:
+        a, b = np.asarray(x).astype(np.int64), np.asarray(y).astype(np.int64)
+        if op == "add":
+            r = a + b
+        elif op == "sub":
+            r = a - b
+        elif op == "mul":
+            r = a * b  # |a*b| < 2^62: exact before the wrap
+        elif op == "div":
+            safe = np.where(b == 0, 1, b)
+            q = np.abs(a) // np.abs(safe)
+            r = np.where(b == 0, 0, np.where((a < 0) ^ (safe < 0), -q, q))
+        elif op == "maximum":
+            r = np.maximum(a, b)
+        elif op == "minimum":
+            r = np.minimum(a, b)
+        elif op == "left_shift":
+            r = a << b
+        elif op == "right_shift":
+            r = a >> b  # arithmetic on signed values
+        else:
+            raise ValueError(op)
+        return _wrap(r, dtype)
+    fa, fb = _to_f32(x, dtype), _to_f32(y, dtype)
+    with np.errstate(all="ignore"):
+        if op == "add":
+            r = fa + fb
+        elif op == "sub":
+            r = fa - fb
+        elif op == "mul":
+            r = fa * fb
+        elif op == "div":
+            r = fa / fb
+        elif op == "maximum":
+            tie = np.where(np.signbit(fa), fb, fa)  # equal operands: +0 over -0
+            r = np.where(np.isnan(fa), fa, np.where(np.isnan(fb), fb, np.where(fa == fb, tie, np.maximum(fa, fb))))
+        elif op == "minimum":
+            tie = np.where(np.signbit(fa), fa, fb)  # equal operands: -0 over +0
+            r = np.where(np.isnan(fa), fa, np.where(np.isnan(fb), fb, np.where(fa == fb, tie, np.minimum(fa, fb))))
+        else:
+            raise ValueError(op)
+    return _from_f32(np.asarray(r, dtype=np.float32), dtype)
+
+
+def _compare(a: np.ndarray, b: np.ndarray, cmp: str) -> np.ndarray:
+    return {"equal": np.equal, "not_equal": np.not_equal, "greater": np.greater, "greater_equal": np.greater_equal,
+            "less": np.less, "less_equal": np.less_equal}[cmp](a, b)
+
+
+def where_compare(x: np.ndarray, y: np.ndarray, cmp: str, dtype: str) -> np.ndarray:
+    """python/test/asc2/operations/test_where.py:24-26: where(cmp(x, y), x, y); 16-bit
+    floats compare exactly in float32 (bfloat16 as uint16 bit patterns)."""
+    if dtype in _INT_BITS:
+        return np.where(_compare(x, y, cmp), x, y)
+    return np.where(_compare(_to_f32(x, dtype), _to_f32(y, dtype), cmp), x, y)
+
+
+def where_scalar(x: np.ndarray, s, cmp: str, dtype: str, true_value, false_value) -> np.ndarray:
+    """python/test/asc2/operations/test_where.py:53-54: where(cmp(x, s), t, f) with s, t,
+    f converted to x's dtype (bfloat16 as uint16 bit patterns)."""
+    shape = np.asarray(x).shape
+
+    def full(v):
+        if dtype in _INT_BITS:
+            return _wrap(np.full(shape, int(v), dtype=np.int64), dtype)
+        return _from_f32(np.full(shape, v, dtype=np.float32), dtype)
+
+    if dtype in _INT_BITS:
+        c = _compare(np.asarray(x), full(s), cmp)
+    else:
+        c = _compare(_to_f32(x, dtype), _to_f32(full(s), dtype), cmp)
+    return np.where(c, full(true_value), full(false_value))
 
 
 # --------------------------------------------------------------------------------- flash attention

@@ -25,12 +25,13 @@ DT_FLOAT16 = 1
 DT_BFLOAT16 = 2
 DT_INT32 = 3
 DT_INT8 = 4
+DT_INT16 = 5
 
 ERR_INVALID_ARG = -1
 ERR_UNSUPPORTED = -2
 ERR_ALIGNMENT = -3
 
-_c_i32, _c_i64, _c_p, _c_f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
+_c_i32, _c_i64, _c_p, _c_f32, _c_f64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_double
 
 # name -> argtypes; every entry point returns int32_t.
 SIGNATURES = {
@@ -52,6 +53,9 @@ SIGNATURES = {
     "asc_matmul_i8_dequant_f16": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
     "asc_flash_attention_fwd_bf16": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_f32, _c_i32,
                                      _c_p],
+    "asc_unary_f32": [_c_i32, _c_p, _c_p, _c_i64, _c_p],
+    "asc_binary": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f64, _c_i64, _c_p],
+    "asc_where_cmp": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f64, _c_i64, _c_f64, _c_f64, _c_p],
 }
 # entry points returning a C string
 STRING_FUNCS = ("asc_last_error", "asc_version")

@@ -1,0 +1,299 @@
+// Element-wise asc2 tile operations, as the reference's operation tests use them:
+//   unary   python/test/asc2/operations/test_unary_ops.py:35-40   z = op(x)       (fp32)
+//   binary  python/test/asc2/operations/test_binary_ops.py:24-38  z = op(x, y), either operand may be a scalar
+//   where   python/test/asc2/operations/test_where.py:18-27, 48-55
+//           z = where(cmp(x, y), x, y)  or  z = where(cmp(x, s), 0, 1)
+//
+// Semantics follow the op definitions (python/asc/language/tile/binary_ops.py,
+// unary_ops.py; dtype inference utils.py:73-94): a scalar operand takes the
+// tile's dtype; integer add/sub/mul wrap (arith.addi/subi/muli), integer div
+// truncates (arith.divsi), max/min are signed for integers and NaN-propagating
+// for floats (arith.maximumf/minimumf: -0 < +0), shifts are shli / shrsi
+// (arithmetic) by a non-negative amount below the bit width.  16-bit float
+// elements are computed in fp32 and rounded once (RNE) to the element type.
+// Integer division by zero yields 0 (arith.divsi leaves it undefined).  A
+// scalar operand of a 16-bit float tile is rounded to fp32 on the host, then to
+// the element type (exact for values that come from such a tile).
+//
+// One grid-stride kernel per (element type, operation family); the op code is a
+// kernel argument (uniform branch).  These are HBM-bound streams; the reference
+// tests run them on 32 elements.
+#include <math.h>
+
+#include "common.h"
+#include "numeric.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct F32 {
+  using T = float;
+  static constexpr bool kFloat = true;
+  __device__ static float in(float v) { return v; }
+  __device__ static float out(float v) { return v; }
+};
+struct F16 {
+  using T = uint16_t;
+  static constexpr bool kFloat = true;
+  __device__ static float in(uint16_t v) { return asc::f16_to_f32(v); }
+  __device__ static uint16_t out(float v) { return asc::f32_to_f16_rne(v); }
+};
+struct BF16 {
+  using T = uint16_t;
+  static constexpr bool kFloat = true;
+  __device__ static float in(uint16_t v) { return asc::bf16_to_f32(v); }
+  __device__ static uint16_t out(float v) { return asc::f32_to_bf16_rne(v); }
+};
+struct I32 {
+  using T = int32_t;
+  using U = uint32_t;
+  static constexpr bool kFloat = false;
+  static constexpr int kBits = 32;
+};
+struct I16 {
+  using T = int16_t;
+  using U = uint16_t;
+  static constexpr bool kFloat = false;
+  static constexpr int kBits = 16;
+};
+
+// ---- unary (fp32): op codes of ASC_UNARY_* in asc_hip.h
+__device__ __forceinline__ float unary_f32(int op, float x) {
+  switch (op) {
+    case 0: return fabsf(x);
+    case 1: return ceilf(x);
+    case 2: return cosf(x);
+    case 3: return coshf(x);
+    case 4: return erff(x);
+    case 5: return expf(x);
+    case 6: return exp2f(x);
+    case 7: return floorf(x);
+    case 8: return logf(x);
+    case 9: return log2f(x);
+    case 10: return -x;
+    case 11: return x < 0.f ? 0.f : x;  // relu: negative -> +0; -0 and NaN pass through
+    case 12: return 1.0f / sqrtf(x);
+    case 13: return sinf(x);
+    case 14: return sinhf(x);
+    case 15: return sqrtf(x);
+    case 16: return tanf(x);
+    default: return tanhf(x);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) unary_f32_kernel(int op, const float* __restrict__ x,
+                                                             float* __restrict__ out, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    out[i] = unary_f32(op, x[i]);
+}
+
+// ---- binary: op codes of ASC_BIN_* in asc_hip.h
+// IEEE 754-2019 maximum / minimum (arith.maximumf / minimumf): NaN propagates,
+// -0 orders below +0.
+__device__ __forceinline__ float max_f(float x, float y) {
+  if (x != x) return x;
+  if (y != y) return y;
+  if (x == y) return __builtin_signbit(x) ? y : x;
+  return x > y ? x : y;
+}
+__device__ __forceinline__ float min_f(float x, float y) {
+  if (x != x) return x;
+  if (y != y) return y;
+  if (x == y) return __builtin_signbit(x) ? x : y;
+  return x < y ? x : y;
+}
+
+template <class E>
+__device__ __forceinline__ typename E::T binary_op(int op, typename E::T a, typename E::T b) {
+  if constexpr (E::kFloat) {
+    const float x = E::in(a), y = E::in(b);
+    float r;
+    switch (op) {
+      case 0: r = x + y; break;
+      case 1: r = x - y; break;
+      case 2: r = x * y; break;
+      case 3: r = x / y; break;
+      case 4: r = max_f(x, y); break;
+      default: r = min_f(x, y); break;
+    }
+    return E::out(r);
+  } else {
+    using T = typename E::T;
+    using U = typename E::U;
+    const U ua = static_cast<U>(a), ub = static_cast<U>(b);
+    switch (op) {
+      case 0: return static_cast<T>(static_cast<U>(ua + ub));
+      case 1: return static_cast<T>(static_cast<U>(ua - ub));
+      case 2: return static_cast<T>(static_cast<U>(ua * ub));
+      case 3:
+        if (b == 0) return T(0);
+        if (b == T(-1)) return static_cast<T>(static_cast<U>(U(0) - ua));  // wraps for the minimum value
+        return static_cast<T>(a / b);
+      case 4: return a > b ? a : b;
+      case 5: return a < b ? a : b;
+      case 6: return static_cast<T>(static_cast<U>(ua << static_cast<int>(b)));
+      default: return static_cast<T>(a >> static_cast<int>(b));
+    }
+  }
+}
+
+// A scalar operand travels as fp32 (float elements) or int64 (integer
+// elements) and is rounded (RNE) or wrapped to the element type here.
+template <class E>
+__device__ __forceinline__ typename E::T element_of(float v_f, int64_t v_i) {
+  if constexpr (E::kFloat) {
+    return E::out(v_f);
+  } else {
+    return static_cast<typename E::T>(static_cast<typename E::U>(static_cast<uint64_t>(v_i)));
+  }
+}
+
+// mode 0: x, y vectors; 1: y is the scalar s; 2: x is the scalar s
+template <class E>
+__global__ void __launch_bounds__(kThreads) binary_kernel(int op, int mode, const typename E::T* __restrict__ x,
+                                                          const typename E::T* __restrict__ y,
+                                                          typename E::T* __restrict__ out, float s_f, int64_t s_i,
+                                                          int64_t n) {
+  const typename E::T s = element_of<E>(s_f, s_i);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const typename E::T a = mode == 2 ? s : x[i];
+    const typename E::T b = mode == 1 ? s : y[i];
+    out[i] = binary_op<E>(op, a, b);
+  }
+}
+
+// ---- compare + where: cmp codes of ASC_CMP_* in asc_hip.h
+template <class E>
+__device__ __forceinline__ bool compare(int cmp, typename E::T a, typename E::T b) {
+  if constexpr (E::kFloat) {
+    const float x = E::in(a), y = E::in(b);
+    switch (cmp) {
+      case 0: return x == y;
+      case 1: return x != y;
+      case 2: return x > y;
+      case 3: return x >= y;
+      case 4: return x < y;
+      default: return x <= y;
+    }
+  } else {
+    switch (cmp) {
+      case 0: return a == b;
+      case 1: return a != b;
+      case 2: return a > b;
+      case 3: return a >= b;
+      case 4: return a < b;
+      default: return a <= b;
+    }
+  }
+}
+
+// mode 0: out = cmp(x, y) ? x : y; mode 1: out = cmp(x, s) ? t : f
+template <class E>
+__global__ void __launch_bounds__(kThreads) where_kernel(int cmp, int mode, const typename E::T* __restrict__ x,
+                                                         const typename E::T* __restrict__ y,
+                                                         typename E::T* __restrict__ out, float s_f, int64_t s_i,
+                                                         float t_f, float f_f, int64_t n) {
+  const typename E::T s = element_of<E>(s_f, s_i);
+  const typename E::T t = element_of<E>(t_f, static_cast<int64_t>(t_f));
+  const typename E::T f = element_of<E>(f_f, static_cast<int64_t>(f_f));
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const typename E::T a = x[i];
+    if (mode == 0) {
+      const typename E::T b = y[i];
+      out[i] = compare<E>(cmp, a, b) ? a : b;
+    } else {
+      out[i] = compare<E>(cmp, a, s) ? t : f;
+    }
+  }
+}
+
+uint32_t grid_for(int64_t n) {
+  const int64_t blocks = asc::ceil_div(n, kThreads);
+  return static_cast<uint32_t>(blocks < 8192 ? blocks : 8192);
+}
+
+template <class E>
+int32_t launch_binary(int op, int mode, const void* x, const void* y, void* out, int64_t n, double s_f, int64_t s_i,
+                      hipStream_t stream) {
+  using T = typename E::T;
+  hipLaunchKernelGGL(binary_kernel<E>, dim3(grid_for(n)), dim3(kThreads), 0, stream, op, mode,
+                     static_cast<const T*>(x), static_cast<const T*>(y), static_cast<T*>(out),
+                     static_cast<float>(s_f), s_i, n);
+  return asc::check_launch("asc_binary");
+}
+
+template <class E>
+int32_t launch_where(int cmp, int mode, const void* x, const void* y, void* out, int64_t n, double s_f, int64_t s_i,
+                     double t, double f, hipStream_t stream) {
+  using T = typename E::T;
+  hipLaunchKernelGGL(where_kernel<E>, dim3(grid_for(n)), dim3(kThreads), 0, stream, cmp, mode,
+                     static_cast<const T*>(x), static_cast<const T*>(y), static_cast<T*>(out),
+                     static_cast<float>(s_f), s_i, static_cast<float>(t), static_cast<float>(f), n);
+  return asc::check_launch("asc_where_cmp");
+}
+
+}  // namespace
+
+extern "C" int32_t asc_unary_f32(int32_t op, const float* x, float* out, int64_t n, asc_stream_t stream) {
+  ASC_REQUIRE(op >= 0 && op <= 17, ASC_ERR_INVALID_ARG, "asc_unary_f32: unknown op code %d", op);
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_unary_f32: negative length");
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_unary_f32: null buffer");
+  hipLaunchKernelGGL(unary_f32_kernel, dim3(grid_for(n)), dim3(kThreads), 0, static_cast<hipStream_t>(stream), op,
+                     x, out, n);
+  return asc::check_launch("asc_unary_f32");
+}
+
+extern "C" int32_t asc_binary(int32_t op, int32_t dtype, const void* x, const void* y, void* out, int64_t n,
+                              int32_t mode, double scalar_f, int64_t scalar_i, asc_stream_t stream) {
+  ASC_REQUIRE(op >= 0 && op <= 7, ASC_ERR_INVALID_ARG, "asc_binary: unknown op code %d", op);
+  ASC_REQUIRE(mode >= 0 && mode <= 2, ASC_ERR_INVALID_ARG, "asc_binary: unknown operand mode %d", mode);
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_binary: negative length");
+  const bool is_int = dtype == ASC_DT_INT32 || dtype == ASC_DT_INT16;
+  ASC_REQUIRE(op < 6 || is_int, ASC_ERR_UNSUPPORTED, "asc_binary: shifts need an integer dtype");
+  if (op >= 6) {
+    const int bits = dtype == ASC_DT_INT32 ? 32 : 16;
+    ASC_REQUIRE(mode == 1 && scalar_i >= 0 && scalar_i < bits, ASC_ERR_INVALID_ARG,
+                "asc_binary: a shift takes a scalar amount in [0, %d), got mode %d amount %lld", bits, mode,
+                (long long)scalar_i);
+  }
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(out && (mode == 2 || x) && (mode == 1 || y), ASC_ERR_INVALID_ARG, "asc_binary: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ASC_DT_FLOAT32: return launch_binary<F32>(op, mode, x, y, out, n, scalar_f, scalar_i, s);
+    case ASC_DT_FLOAT16: return launch_binary<F16>(op, mode, x, y, out, n, scalar_f, scalar_i, s);
+    case ASC_DT_BFLOAT16: return launch_binary<BF16>(op, mode, x, y, out, n, scalar_f, scalar_i, s);
+    case ASC_DT_INT32: return launch_binary<I32>(op, mode, x, y, out, n, scalar_f, scalar_i, s);
+    case ASC_DT_INT16: return launch_binary<I16>(op, mode, x, y, out, n, scalar_f, scalar_i, s);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_binary: unsupported dtype code %d", dtype);
+  }
+}
+
+extern "C" int32_t asc_where_cmp(int32_t cmp, int32_t dtype, const void* x, const void* y, void* out, int64_t n,
+                                 int32_t mode, double scalar_f, int64_t scalar_i, double true_value,
+                                 double false_value, asc_stream_t stream) {
+  ASC_REQUIRE(cmp >= 0 && cmp <= 5, ASC_ERR_INVALID_ARG, "asc_where_cmp: unknown comparison code %d", cmp);
+  ASC_REQUIRE(mode == 0 || mode == 1, ASC_ERR_INVALID_ARG, "asc_where_cmp: unknown operand mode %d", mode);
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_where_cmp: negative length");
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(x && out && (mode == 1 || y), ASC_ERR_INVALID_ARG, "asc_where_cmp: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ASC_DT_FLOAT32:
+      return launch_where<F32>(cmp, mode, x, y, out, n, scalar_f, scalar_i, true_value, false_value, s);
+    case ASC_DT_FLOAT16:
+      return launch_where<F16>(cmp, mode, x, y, out, n, scalar_f, scalar_i, true_value, false_value, s);
+    case ASC_DT_BFLOAT16:
+      return launch_where<BF16>(cmp, mode, x, y, out, n, scalar_f, scalar_i, true_value, false_value, s);
+    case ASC_DT_INT32:
+      return launch_where<I32>(cmp, mode, x, y, out, n, scalar_f, scalar_i, true_value, false_value, s);
+    case ASC_DT_INT16:
+      return launch_where<I16>(cmp, mode, x, y, out, n, scalar_f, scalar_i, true_value, false_value, s);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_where_cmp: unsupported dtype code %d", dtype);
+  }
+}

@@ -19,6 +19,7 @@ _DTYPE_CODES = {
     torch.bfloat16: _native.DT_BFLOAT16,
     torch.int32: _native.DT_INT32,
     torch.int8: _native.DT_INT8,
+    torch.int16: _native.DT_INT16,
 }
 
 
@@ -343,3 +344,104 @@ def flash_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: to
         lse_ptr = lse.data_ptr()
     _native.call("asc_flash_attention_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse_ptr,
                  batch, heads, seq_len, head_dim, float(sm_scale), int(bool(causal)), _stream(stream))
+
+
+# ------------------------------------------------------------------ element-wise tile operations
+
+UNARY_OPS = ("abs", "ceil", "cos", "cosh", "erf", "exp", "exp2", "floor", "log", "log2", "negative", "relu",
+             "rsqrt", "sin", "sinh", "sqrt", "tan", "tanh")
+BINARY_OPS = ("add", "sub", "mul", "div", "maximum", "minimum", "left_shift", "right_shift")
+COMPARE_OPS = ("equal", "not_equal", "greater", "greater_equal", "less", "less_equal")
+_TILE_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.int32, torch.int16)
+
+
+def _flat(t: torch.Tensor, name: str, n: int) -> torch.Tensor:
+    _contiguous(_device_tensor(t, name), name)
+    if t.numel() < n:
+        raise ValueError(f"'{name}' holds {t.numel()} elements, {n} needed")
+    return t
+
+
+def _scalar_parts(value: Any, dtype: torch.dtype):
+    """(scalar_f, scalar_i) transport of a scalar operand for an element type."""
+    if isinstance(value, torch.Tensor):
+        if value.dim() != 0:
+            raise ValueError("a scalar operand must be a 0-dim tensor or a python number")
+        value = value.item()
+    if dtype.is_floating_point:
+        return float(value), 0
+    if isinstance(value, float) and not value.is_integer():
+        raise TypeError(f"an integer tile takes an integer scalar, got {value}")
+    return 0.0, int(value)
+
+
+def unary_f32(x: torch.Tensor, out: torch.Tensor, op: str, n: Optional[int] = None, stream=None) -> None:
+    """out[:n] = op(x[:n]), fp32 (asc2 unary ops, python/asc/language/tile/unary_ops.py)."""
+    if op not in UNARY_OPS:
+        raise ValueError(f"unknown unary op {op!r}; expected one of {UNARY_OPS}")
+    n = x.numel() if n is None else int(n)
+    for t, name in ((x, "x"), (out, "out")):
+        _flat(t, name, n)
+        if t.dtype != torch.float32:
+            raise TypeError(f"'{name}' must be float32, got {t.dtype}")
+    _native.call("asc_unary_f32", UNARY_OPS.index(op), x.data_ptr(), out.data_ptr(), n, _stream(stream))
+
+
+def binary(x: Any, y: Any, out: torch.Tensor, op: str, n: Optional[int] = None, stream=None) -> None:
+    """out[:n] = op(x, y) with either operand a tensor or a scalar (asc2 binary ops,
+    python/asc/language/tile/binary_ops.py); the result dtype is the tensor operand's."""
+    if op not in BINARY_OPS:
+        raise ValueError(f"unknown binary op {op!r}; expected one of {BINARY_OPS}")
+    x_t, y_t = isinstance(x, torch.Tensor) and x.dim() > 0, isinstance(y, torch.Tensor) and y.dim() > 0
+    if not (x_t or y_t):
+        raise TypeError("at least one operand must be a tensor")
+    ref = x if x_t else y
+    n = ref.numel() if n is None else int(n)
+    code = _code(ref, "x" if x_t else "y", _TILE_DTYPES)
+    if out.dtype != ref.dtype:
+        raise TypeError(f"'out' must be {ref.dtype}, got {out.dtype}")
+    _flat(out, "out", n)
+    mode, scalar = 0, None
+    if x_t and y_t:
+        if y.dtype != x.dtype:
+            raise TypeError(f"operand dtypes differ: {x.dtype} and {y.dtype}")
+        _flat(x, "x", n)
+        _flat(y, "y", n)
+    elif x_t:
+        mode, scalar = 1, y
+        _flat(x, "x", n)
+    else:
+        mode, scalar = 2, x
+        _flat(y, "y", n)
+    if op in ("left_shift", "right_shift") and (mode != 1 or ref.dtype.is_floating_point):
+        raise TypeError(f"{op} takes an integer tensor and a scalar shift amount")
+    s_f, s_i = _scalar_parts(scalar, ref.dtype) if scalar is not None else (0.0, 0)
+    # an unused operand slot gets the output buffer (valid for n elements), never NULL
+    _native.call("asc_binary", BINARY_OPS.index(op), code, x.data_ptr() if x_t else out.data_ptr(),
+                 y.data_ptr() if y_t else out.data_ptr(), out.data_ptr(), n, mode, s_f, s_i, _stream(stream))
+
+
+def where_compare(x: torch.Tensor, y: Any, out: torch.Tensor, cmp: str, true_value=None, false_value=None,
+                  n: Optional[int] = None, stream=None) -> None:
+    """out = where(cmp(x, y), x, y) for a tensor y, or where(cmp(x, s), true_value,
+    false_value) for a scalar s (asc2.where over a comparison, test_where.py)."""
+    if cmp not in COMPARE_OPS:
+        raise ValueError(f"unknown comparison {cmp!r}; expected one of {COMPARE_OPS}")
+    n = x.numel() if n is None else int(n)
+    code = _code(x, "x", _TILE_DTYPES)
+    _flat(x, "x", n)
+    _flat(out, "out", n)
+    if out.dtype != x.dtype:
+        raise TypeError(f"'out' must be {x.dtype}, got {out.dtype}")
+    if isinstance(y, torch.Tensor) and y.dim() > 0:
+        if y.dtype != x.dtype:
+            raise TypeError(f"operand dtypes differ: {x.dtype} and {y.dtype}")
+        _flat(y, "y", n)
+        _native.call("asc_where_cmp", COMPARE_OPS.index(cmp), code, x.data_ptr(), y.data_ptr(), out.data_ptr(), n,
+                     0, 0.0, 0, 0.0, 0.0, _stream(stream))
+        return
+    if true_value is None or false_value is None:
+        raise ValueError("a scalar comparison needs true_value and false_value")
+    s_f, s_i = _scalar_parts(y, x.dtype)
+    _native.call("asc_where_cmp", COMPARE_OPS.index(cmp), code, x.data_ptr(), x.data_ptr(), out.data_ptr(), n, 1, s_f,
+                 s_i, float(true_value), float(false_value), _stream(stream))

@@ -322,3 +322,54 @@ def _flash_attention(call: KernelCall) -> None:
     q, k, v, o = views
     kernels.flash_attention_fwd(q, k, v, o, float(call.get("sm_scale")), bool(call.get("causal")),
                                 stream=call.stream)
+
+
+# --------------------------------------------------------- element-wise tile operations (operation tests)
+
+def _op_name(op, allowed, what: str) -> str:
+    """The asc2 function passed as a ConstExpr (asc2.add ...) -> its name, checked."""
+    name = getattr(op, "__name__", str(op))
+    if name not in allowed:
+        raise NotImplementedError(f"no native {what} for op {name!r}")
+    return name
+
+
+@register("kernel", ("x_ptr", "z_ptr", "block_length", "op"), "python/test/asc2/operations/test_unary_ops.py:35-40")
+def _unary(call: KernelCall) -> None:
+    n = int(call.consts["block_length"])
+    kernels.unary_f32(call.args["x_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1),
+                      _op_name(call.consts["op"], kernels.UNARY_OPS, "unary op"), n, call.stream)
+
+
+@register("kernel", ("x_ptr", "y_ptr", "z_ptr", "block_length", "fmt", "op"),
+          "python/test/asc2/operations/test_binary_ops.py:24-38")
+def _binary(call: KernelCall) -> None:
+    # fmt "VV" / "VS" / "SV": which operand is a tile (test_binary_ops.py:8-9, 25-35);
+    # by-value operands arrive as python scalars
+    fmt = str(call.consts["fmt"])
+    x, y = call.args["x_ptr"], call.args["y_ptr"]
+    x_vec, y_vec = isinstance(x, torch.Tensor), isinstance(y, torch.Tensor)
+    if (x_vec, y_vec) != {"VV": (True, True), "VS": (True, False), "SV": (False, True)}.get(fmt, (None, None)):
+        raise ValueError(f"operands do not match fmt {fmt!r}")
+    n = int(call.consts["block_length"])
+    kernels.binary(x.reshape(-1) if x_vec else x, y.reshape(-1) if y_vec else y, call.args["z_ptr"].reshape(-1),
+                   _op_name(call.consts["op"], kernels.BINARY_OPS, "binary op"), n, call.stream)
+
+
+@register("where_kernel", ("x_ptr", "y_ptr", "z_ptr", "op"), "python/test/asc2/operations/test_where.py:18-27")
+def _where(call: KernelCall) -> None:
+    # the body's tiles span the tensors (SIZE elements in the reference test)
+    x = call.args["x_ptr"].reshape(-1)
+    kernels.where_compare(x, call.args["y_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1),
+                          _op_name(call.consts["op"], kernels.COMPARE_OPS, "comparison"), n=x.numel(),
+                          stream=call.stream)
+
+
+@register("where_scalar_kernel", ("x_ptr", "scalar", "z_ptr", "op"),
+          "python/test/asc2/operations/test_where.py:48-55")
+def _where_scalar(call: KernelCall) -> None:
+    # where(op(x, scalar), 0, 1) in x's dtype
+    x = call.args["x_ptr"].reshape(-1)
+    kernels.where_compare(x, call.args["scalar"], call.args["z_ptr"].reshape(-1),
+                          _op_name(call.consts["op"], kernels.COMPARE_OPS, "comparison"), true_value=0,
+                          false_value=1, n=x.numel(), stream=call.stream)

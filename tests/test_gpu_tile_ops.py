@@ -1,0 +1,253 @@
+"""Element-wise asc2 tile operations on the GPU: the generic kernels of the
+reference's operation tests (python/test/asc2/operations/test_unary_ops.py,
+test_binary_ops.py, test_where.py).
+
+First the reference tests themselves: the same kernel signatures, parametrisation,
+input recipes (size 32) and assertions (allclose atol 1e-3 for float32,
+torch.equal otherwise; assert_close for where).  Then the kernel API at a
+million elements against the oracle, with edge values (signed zeros, NaN,
+infinities, integer extremes): bit-exact for binary and where (NaN compared as
+NaN), within a few float32 ulps (rtol 1e-6, atol 1e-7) for the libm unary ops."""
+import numpy as np
+import pytest
+import torch
+
+import asc
+import asc2
+from oracle import asc2_oracle as O
+from pyasc_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+VV, VS, SV = "VV", "VS", "SV"
+
+
+@asc2.jit(always_compile=True)
+def kernel(x_ptr, y_ptr, z_ptr, block_length: asc.ConstExpr, fmt: asc.ConstExpr, op: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+# test_binary_ops.py:11-20
+BINARY_OPS = [
+    (asc2.add, torch.add, [VV, VS, SV], [torch.bfloat16, torch.float32, torch.int32]),
+    (asc2.div, torch.div, [VV, VS, SV], [torch.float32]),
+    (asc2.mul, torch.mul, [VV, VS, SV], [torch.bfloat16, torch.float32, torch.int32]),
+    (asc2.sub, torch.sub, [VV, VS, SV], [torch.bfloat16, torch.float32, torch.int32]),
+    (asc2.left_shift, torch.bitwise_left_shift, [VS], [torch.int32]),
+    (asc2.right_shift, torch.bitwise_right_shift, [VS], [torch.int32]),
+    (asc2.maximum, torch.maximum, [VV, VS, SV], [torch.bfloat16, torch.float32, torch.int32]),
+    (asc2.minimum, torch.minimum, [VV, VS, SV], [torch.bfloat16, torch.float32, torch.int32]),
+]
+
+
+@pytest.mark.parametrize("asc_op, torch_op, fmt, dtype", [(a, t, f, d) for a, t, fmts, dtypes in BINARY_OPS
+                                                          for f in fmts for d in dtypes],
+                         ids=lambda v: getattr(v, "__name__", str(v)))
+def test_binary_reference_cases(device, asc_op, torch_op, fmt, dtype):
+    # test_binary_ops.py:46-87
+    size = 32
+
+    def create_input(is_vector):
+        if is_vector:
+            if dtype.is_floating_point:
+                return torch.randn((size,), dtype=dtype).clamp(1, 100)
+            return torch.randint(1, 100, (size,), dtype=dtype)
+        return torch.tensor(2, dtype=dtype)
+
+    x = create_input(fmt in (VV, VS))
+    y = create_input(fmt in (VV, SV))
+    z = torch.zeros(size, dtype=dtype)
+    kernel[1](x, y, z, size, fmt, asc_op)
+    if dtype == torch.float32:
+        assert torch.allclose(z, torch_op(x, y), atol=1e-3)
+    else:
+        assert torch.equal(z, torch_op(x, y))
+
+
+@asc2.jit(always_compile=True)
+def unary_kernel(x_ptr: asc.GlobalAddress, z_ptr: asc.GlobalAddress, block_length: asc.ConstExpr,
+                 op: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+# the reference names this kernel `kernel` too (test_unary_ops.py:35); dispatch is by
+# name and parameter names, so the same registered entry serves it under either name
+unary_kernel.fn_name = "kernel"
+
+UNARY_OPS = [(asc2.abs, torch.abs), (asc2.ceil, torch.ceil), (asc2.cos, torch.cos), (asc2.cosh, torch.cosh),
+             (asc2.erf, torch.erf), (asc2.exp, torch.exp), (asc2.exp2, torch.exp2), (asc2.floor, torch.floor),
+             (asc2.log, torch.log), (asc2.negative, torch.neg), (asc2.relu, torch.relu), (asc2.rsqrt, torch.rsqrt),
+             (asc2.sin, torch.sin), (asc2.sinh, torch.sinh), (asc2.sqrt, torch.sqrt), (asc2.tan, torch.tan),
+             (asc2.tanh, torch.tanh)]  # test_unary_ops.py:10-28
+
+
+@pytest.mark.parametrize("asc_op, torch_op", UNARY_OPS, ids=lambda v: getattr(v, "__name__", str(v)))
+def test_unary_reference_cases(device, asc_op, torch_op):
+    # test_unary_ops.py:43-69
+    x = torch.randn((32,), dtype=torch.float32).clamp(1, 100)
+    z = torch.zeros(32, dtype=torch.float32)
+    unary_kernel[1](x, z, 32, asc_op)
+    assert torch.allclose(z, torch_op(x), atol=1e-3)
+
+
+@asc2.jit(always_compile=True)
+def where_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, z_ptr: asc.GlobalAddress, op: asc.ConstExpr):
+    raise AssertionError("kernel bodies are not executed")
+
+
+@asc2.jit(always_compile=True)
+def where_scalar_kernel(x_ptr: asc.GlobalAddress, scalar, z_ptr: asc.GlobalAddress, op: asc.ConstExpr):
+    raise AssertionError("kernel bodies are not executed")
+
+
+WHERE_DTYPES = [torch.float16, torch.bfloat16, torch.float32, torch.int16, torch.int32]
+COMPARES = [(asc2.equal, torch.eq), (asc2.not_equal, torch.ne), (asc2.greater, torch.gt),
+            (asc2.greater_equal, torch.ge), (asc2.less, torch.lt), (asc2.less_equal, torch.le)]
+
+
+def _where_input(dtype):
+    # test_where.py:11-15
+    if dtype.is_floating_point:
+        return torch.rand(32, dtype=dtype)
+    return torch.randint(-100, 100, (32,), dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", WHERE_DTYPES, ids=str)
+@pytest.mark.parametrize("asc_op, torch_op", COMPARES, ids=lambda v: getattr(v, "__name__", str(v)))
+def test_where_reference_cases(device, asc_op, torch_op, dtype):
+    # test_where.py:39-46 and 70-77
+    x, y = _where_input(dtype), _where_input(dtype)
+    result = torch.zeros_like(x)
+    where_kernel[1](x, y, result, asc_op)
+    torch.testing.assert_close(result, torch.where(torch_op(x, y), x, y))
+    s = torch.tensor(0 if dtype.is_signed else 0.5, dtype=dtype)
+    result = torch.zeros_like(x)
+    where_scalar_kernel[1](x, s, result, asc_op)
+    torch.testing.assert_close(result, torch.where(torch_op(x, s), torch.tensor(0, dtype=dtype),
+                                                   torch.tensor(1, dtype=dtype)))
+
+
+# ------------------------------------------------------------- kernel API at size, against the oracle
+
+N = (1 << 20) + 37
+_EDGE_F = [0.0, -0.0, 1.0, -1.0, float("nan"), float("inf"), float("-inf"), 3.5, -2.25, 65504.0, 1e-8, 1e30]
+
+
+def _float_data(dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randn(N, generator=g) * 8
+    v[:len(_EDGE_F) ** 2] = torch.tensor(_EDGE_F * len(_EDGE_F)) if seed % 2 else \
+        torch.tensor([e for e in _EDGE_F for _ in _EDGE_F])
+    return v.to(dtype)
+
+
+def _int_data(dtype, seed):
+    info = torch.iinfo(dtype)
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randint(info.min, info.max, (N,), generator=g, dtype=torch.int64)
+    edge = [0, 1, -1, info.max, info.min, 7, -7]
+    v[:len(edge) ** 2] = torch.tensor(edge * len(edge)) if seed % 2 else torch.tensor([e for e in edge for _ in edge])
+    return v.to(dtype)
+
+
+def _np(t: torch.Tensor, dtype: str) -> np.ndarray:
+    return t.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else t.numpy()
+
+
+def _assert_same(got: torch.Tensor, expected: np.ndarray, dtype: str):
+    g = _np(got, dtype)
+    if dtype in ("int32", "int16"):
+        np.testing.assert_array_equal(g, expected)
+        return
+    as_f = (lambda a: O.bf16_bits_to_f32(a)) if dtype == "bfloat16" else (lambda a: a.astype(np.float32))
+    nan = np.isnan(as_f(expected))
+    assert np.array_equal(np.isnan(as_f(g)), nan)
+    view = np.uint32 if dtype == "float32" else np.uint16
+    np.testing.assert_array_equal(g.view(view)[~nan], expected.view(view)[~nan])
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int32", "int16"])
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "maximum", "minimum"])
+def test_binary_vs_oracle(device, op, dtype):
+    td = getattr(torch, dtype)
+    make = _float_data if td.is_floating_point else _int_data
+    x, y = make(td, 1), make(td, 2)
+    out = torch.empty(N, dtype=td, device=device)
+    kernels.binary(x.to(device), y.to(device), out, op)
+    torch.cuda.synchronize()
+    _assert_same(out.cpu(), O.binary_elements(_np(x, dtype), _np(y, dtype), op, dtype), dtype)
+    # scalar operands on either side (VS and SV), converted to the tile's dtype
+    s = torch.tensor(-2.5 if td.is_floating_point else -3, dtype=td)
+    s_np = _np(s.reshape(1), dtype)
+    for mode, (a, b) in (("VS", (x, s)), ("SV", (s, x))):
+        kernels.binary(a.to(device) if a.dim() else a, b.to(device) if b.dim() else b, out, op)
+        torch.cuda.synchronize()
+        full = np.repeat(s_np, N)
+        expected = O.binary_elements(_np(x, dtype), full, op, dtype) if mode == "VS" else \
+            O.binary_elements(full, _np(x, dtype), op, dtype)
+        _assert_same(out.cpu(), expected, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["int32", "int16"])
+def test_shifts_vs_oracle(device, dtype):
+    td = getattr(torch, dtype)
+    x = _int_data(td, 3)
+    out = torch.empty(N, dtype=td, device=device)
+    for op in ("left_shift", "right_shift"):
+        for amount in (0, 1, 7, torch.iinfo(td).bits - 1):
+            kernels.binary(x.to(device), amount, out, op)
+            torch.cuda.synchronize()
+            expected = O.binary_elements(x.numpy(), np.full(N, amount, dtype=x.numpy().dtype), op, dtype)
+            np.testing.assert_array_equal(out.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("op", kernels.UNARY_OPS)
+def test_unary_vs_oracle(device, op):
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(N, generator=g) * 6
+    if op in ("log", "log2", "rsqrt", "sqrt"):
+        x = x.abs() + 1e-6
+    if op in ("cosh", "sinh", "exp", "exp2"):
+        x = x.clamp(-60, 60)
+    x[:6] = torch.tensor([-0.0, 0.0, float("nan"), 1.0, 0.5, -0.5])
+    out = torch.empty(N, device=device)
+    kernels.unary_f32(x.to(device), out, op)
+    torch.cuda.synchronize()
+    expected = O.unary_f32(x.numpy(), op)
+    np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=1e-6, atol=1e-7, equal_nan=True)
+    if op in ("abs", "ceil", "floor", "negative", "relu", "sqrt"):  # exactly rounded: bit-exact
+        got = out.cpu().numpy()
+        keep = ~np.isnan(expected)
+        np.testing.assert_array_equal(got.view(np.uint32)[keep], expected.view(np.uint32)[keep])
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int32", "int16"])
+@pytest.mark.parametrize("cmp", kernels.COMPARE_OPS)
+def test_where_vs_oracle(device, cmp, dtype):
+    td = getattr(torch, dtype)
+    make = _float_data if td.is_floating_point else _int_data
+    x, y = make(td, 1), make(td, 2)
+    y[-1000:] = x[-1000:]  # ties
+    out = torch.empty(N, dtype=td, device=device)
+    kernels.where_compare(x.to(device), y.to(device), out, cmp)
+    torch.cuda.synchronize()
+    _assert_same(out.cpu(), O.where_compare(_np(x, dtype), _np(y, dtype), cmp, dtype), dtype)
+    s = torch.tensor(1 if not td.is_floating_point else 0.75, dtype=td)
+    kernels.where_compare(x.to(device), s, out, cmp, true_value=0, false_value=1)
+    torch.cuda.synchronize()
+    _assert_same(out.cpu(), O.where_scalar(_np(x, dtype), s.item(), cmp, dtype, 0, 1), dtype)
+
+
+def test_tile_op_argument_errors(device):
+    x = torch.zeros(64, dtype=torch.int32, device=device)
+    f = torch.zeros(64, device=device)
+    with pytest.raises(TypeError):
+        kernels.binary(x, x, x, "left_shift")  # shifts take a scalar amount
+    with pytest.raises(RuntimeError, match="asc_binary"):
+        kernels.binary(x, 32, x, "left_shift")  # amount outside [0, 32)
+    with pytest.raises(TypeError):
+        kernels.binary(f, x, f, "add")  # mixed tensor dtypes
+    with pytest.raises(ValueError):
+        kernels.unary_f32(f, f, "not_an_op")
+    with pytest.raises(ValueError):
+        kernels.binary(f, f, torch.zeros(8, device=device), "add")  # output too short

@@ -395,3 +395,140 @@ def test_rms_norm_matches_torch_and_closed_forms():
     y2 = O.rms_norm_rows(7.0 * x.numpy(), gamma.numpy(), 0.0, 200)
     np.testing.assert_allclose(y1[:, :200], y2[:, :200], rtol=1e-13)
     np.testing.assert_array_equal(y1[:, 200:], x.numpy()[:, 200:])
+
+
+# ------------------------------------------------------------------ element-wise tile operations
+# Pinned against torch's CPU ops (the operation tests' goldens,
+# python/test/asc2/operations/test_{unary_ops,binary_ops,where}.py) and hand-derived
+# known answers for what torch does not define the same way (integer x / 0).
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float32:
+        return t.numpy().view(np.uint32)
+    return t.numpy()
+
+
+def _as_oracle(t: torch.Tensor, dtype: str) -> np.ndarray:
+    return t.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else t.numpy()
+
+
+_EDGE_F = [0.0, -0.0, 1.0, -1.0, float("nan"), float("inf"), float("-inf"), 3.5, -2.25, 65504.0, 1e-8]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "maximum", "minimum"])
+def test_binary_float_matches_torch(op, dtype):
+    g = torch.Generator().manual_seed(21)
+    td = getattr(torch, dtype)
+    x = torch.cat([torch.randn(400, generator=g) * 5, torch.tensor(_EDGE_F * len(_EDGE_F))]).to(td)
+    y = torch.cat([torch.randn(400, generator=g) * 5,
+                   torch.tensor([v for v in _EDGE_F for _ in _EDGE_F])]).to(td)  # every pair of edge values
+    expected = getattr(torch, op)(x, y)
+    got = O.binary_elements(_as_oracle(x, dtype), _as_oracle(y, dtype), op, dtype)
+    # bit-exact except the NaN payload, which torch's vector paths choose freely
+    got_f = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).float() if dtype == "bfloat16" else \
+        torch.from_numpy(got).float()
+    nan = torch.isnan(expected.float())
+    assert torch.equal(torch.isnan(got_f), nan)
+    keep = ~nan
+    if op in ("maximum", "minimum"):
+        # torch returns either operand of a -0 / +0 tie depending on its code path;
+        # those ties are pinned below by the IEEE 754-2019 definition
+        keep &= ~((x.float() == 0) & (y.float() == 0))
+    np.testing.assert_array_equal(got.view(np.uint16 if dtype != "float32" else np.uint32)[keep.numpy()],
+                                  _bits(expected)[keep.numpy()])
+
+
+def test_binary_signed_zero_and_nan_ties():
+    # IEEE 754-2019 maximum / minimum (arith.maximumf / minimumf): -0 < +0, NaN propagates
+    z = np.array([-0.0, 0.0, -0.0, 0.0], np.float32)
+    w = np.array([0.0, -0.0, -0.0, 0.0], np.float32)
+    assert O.binary_elements(z, w, "maximum", "float32").view(np.uint32).tolist() == [0, 0, 0x80000000, 0]
+    assert O.binary_elements(z, w, "minimum", "float32").view(np.uint32).tolist() == \
+        [0x80000000, 0x80000000, 0x80000000, 0]
+    assert np.isnan(O.binary_elements(np.array([np.nan, 1], np.float32), np.array([1, np.nan], np.float32),
+                                      "maximum", "float32")).all()
+
+
+@pytest.mark.parametrize("dtype", ["int32", "int16"])
+def test_binary_int_matches_torch(dtype):
+    td = getattr(torch, dtype)
+    info = torch.iinfo(td)
+    g = torch.Generator().manual_seed(22)
+    edge = [0, 1, -1, info.max, info.min, info.max - 1, info.min + 1, 7, -7]
+    x = torch.cat([torch.randint(info.min, info.max, (500,), generator=g, dtype=torch.int64),
+                   torch.tensor(edge * len(edge))]).to(td)
+    y = torch.cat([torch.randint(info.min, info.max, (500,), generator=g, dtype=torch.int64),
+                   torch.tensor([v for v in edge for _ in edge])]).to(td)
+    for op in ("add", "sub", "mul", "maximum", "minimum"):
+        np.testing.assert_array_equal(O.binary_elements(x.numpy(), y.numpy(), op, dtype),
+                                      getattr(torch, op)(x, y).numpy(), err_msg=op)
+    # torch traps on x / 0 and on min / -1 (x86 idiv); both are pinned by known answers below
+    nz = (y != 0) & ~((x == info.min) & (y == -1))
+    np.testing.assert_array_equal(O.binary_elements(x.numpy(), y.numpy(), "div", dtype)[nz.numpy()],
+                                  torch.div(x[nz], y[nz], rounding_mode="trunc").numpy())
+    for amount in (0, 1, 5, info.bits - 1):
+        s = torch.full_like(x, amount)
+        np.testing.assert_array_equal(O.binary_elements(x.numpy(), s.numpy(), "left_shift", dtype),
+                                      torch.bitwise_left_shift(x, s).numpy())
+        np.testing.assert_array_equal(O.binary_elements(x.numpy(), s.numpy(), "right_shift", dtype),
+                                      torch.bitwise_right_shift(x, s).numpy())
+
+
+def test_binary_int_known_answers():
+    i32 = np.int32
+    f = O.binary_elements
+    assert f(np.array([7, -7, 0, -(2**31)], i32), np.array([0, 0, 0, -1], i32), "div", "int32").tolist() == \
+        [0, 0, 0, -(2**31)]  # x / 0 = 0 (build-defined), INT_MIN / -1 wraps
+    assert f(np.array([-7, 7], i32), np.array([2, -2], i32), "div", "int32").tolist() == [-3, -3]  # truncation
+    assert f(np.array([2**31 - 1], i32), np.array([1], i32), "add", "int32").tolist() == [-(2**31)]
+    assert f(np.array([-8, 1], i32), np.array([1, 31], i32), "right_shift", "int32").tolist() == [-4, 0]
+    assert f(np.array([1], i32), np.array([31], i32), "left_shift", "int32").tolist() == [-(2**31)]
+
+
+@pytest.mark.parametrize("op", ["abs", "ceil", "cos", "cosh", "erf", "exp", "exp2", "floor", "log", "log2", "negative",
+                                "relu", "rsqrt", "sin", "sinh", "sqrt", "tan", "tanh"])
+def test_unary_matches_torch(op):
+    g = torch.Generator().manual_seed(23)
+    x = torch.cat([torch.randn(2000, generator=g).clamp(1, 100), torch.randn(2000, generator=g) * 4])
+    if op in ("log", "log2", "rsqrt", "sqrt"):
+        x = x.abs() + 1e-3
+    if op in ("cosh", "sinh", "exp", "exp2"):
+        x = x.clamp(-20, 20)
+    torch_op = {"negative": torch.neg}.get(op) or getattr(torch, op)
+    expected = torch_op(x.double()).float()  # the exact value, rounded once
+    got = O.unary_f32(x.numpy(), op)
+    np.testing.assert_allclose(got, expected.numpy(), rtol=2e-7, atol=0)
+    # and the float32 torch op the reference test compares with, at its own tolerance
+    np.testing.assert_allclose(got, torch_op(x).numpy(), rtol=1e-5, atol=1e-3)
+
+
+def test_unary_special_values():
+    x = np.array([-3.0, -0.0, 0.0, np.nan, 2.0, -0.5], np.float32)
+    assert O.unary_f32(x, "relu").view(np.uint32).tolist() == \
+        torch.relu(torch.from_numpy(x)).numpy().view(np.uint32).tolist()  # +0, -0, +0, NaN, 2, +0
+    assert O.unary_f32(np.array([-0.5, 0.5], np.float32), "ceil").view(np.uint32).tolist() == [0x80000000, 0x3F800000]
+    assert O.unary_f32(np.array([-0.0], np.float32), "negative").view(np.uint32).tolist() == [0]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32", "int16", "int32"])
+@pytest.mark.parametrize("cmp, torch_op", [("equal", torch.eq), ("not_equal", torch.ne), ("greater", torch.gt),
+                                           ("greater_equal", torch.ge), ("less", torch.lt), ("less_equal", torch.le)])
+def test_where_matches_reference_golden(cmp, torch_op, dtype):
+    # test_where.py:46 / :77 goldens, on the tests' input recipes plus ties
+    td = getattr(torch, dtype)
+    g = torch.Generator().manual_seed(24)
+    if td.is_floating_point:
+        x, y = torch.rand(300, generator=g).to(td), torch.rand(300, generator=g).to(td)
+    else:
+        x, y = torch.randint(-100, 100, (300,), generator=g).to(td), torch.randint(-100, 100, (300,), generator=g).to(td)
+    y[:50] = x[:50]
+    expected = torch.where(torch_op(x, y), x, y)
+    got = O.where_compare(_as_oracle(x, dtype), _as_oracle(y, dtype), cmp, dtype)
+    np.testing.assert_array_equal(got, _as_oracle(expected, dtype))
+    s = torch.tensor(0 if td.is_signed else 0.5, dtype=td)
+    expected = torch.where(torch_op(x, s), torch.tensor(0, dtype=td), torch.tensor(1, dtype=td))
+    got = O.where_scalar(_as_oracle(x, dtype), s.item(), cmp, dtype, 0, 1)
+    np.testing.assert_array_equal(got, _as_oracle(expected, dtype))
