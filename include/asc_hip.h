@@ -143,6 +143,18 @@ int32_t asc_softmax_blocks_f32(const float* x, float* out, int64_t num_rows,
                                int64_t num_cols, int32_t block_size,
                                int32_t grid, asc_stream_t stream);
 
+/* The same two kernels on float16 x / out (asc2.softmax on an f16 tile: SURVEY-
+ * listed "f16 also allowed", python/asc/language/tile/unary_ops.py:213-222;
+ * python/test/asc2/operations/test_softmax.py).  fp32 statistics (x - max in
+ * fp32, libm exp, one reciprocal of the sum), each output rounded once (RNE)
+ * to float16.  Same coverage rules as the float32 entries. */
+int32_t asc_softmax_rows_f16(const void* x, void* out, int64_t num_rows,
+                             int64_t num_cols, int32_t tile_size, int32_t grid,
+                             asc_stream_t stream);
+int32_t asc_softmax_blocks_f16(const void* x, void* out, int64_t num_rows,
+                               int64_t num_cols, int32_t block_size,
+                               int32_t grid, asc_stream_t stream);
+
 /* ---- reductions ---------------------------------------------------------------
  * asc2.reduce_sum / reduce_max / reduce_min / reduce_prod
  *   (python/asc/language/tile/reduction_ops.py:61-126) as the reference's

@@ -32,6 +32,8 @@ How each function is pinned (tests/test_oracle.py):
   + leaky_relu    its integer-valued recipe (exact), a hand-computed 2x2 case.
   reduce          torch sum / amax / amin / prod (the reduction tests' goldens),
                   integer-valued sums (exact), products of powers of two (exact).
+  softmax f16     torch.softmax on float16 (within one float16 ulp), constant row
+                  -> 1/n rounded, two-point rows.
   rms_norm        torch.nn.functional.rms_norm in float64, constant rows (closed
                   form c / sqrt(c^2 + eps) * gamma), scale invariance.
   tile ops        torch's add / sub / mul / div / maximum / minimum / shifts on
@@ -212,11 +214,22 @@ def softmax_row(row: np.ndarray) -> np.ndarray:
     reference's Ascend ExpL2/ReduceSumL2 rounding is not observable (no NPU); this
     is the fp32-exact statement both the GPU kernel and torch.softmax approximate.
     """
+    if np.asarray(row).dtype == np.float16:
+        return softmax_row_f16(row)
     row = np.asarray(row, dtype=np.float32)
     r = (row - row.max()).astype(np.float32)
     e = np.exp(r.astype(np.float64)).astype(np.float32)
     s = np.float32(e.astype(np.float64).sum())
     return (e / s).astype(np.float32)
+
+
+def softmax_row_f16(row: np.ndarray) -> np.ndarray:
+    """asc2.softmax of a float16 row (python/asc/language/tile/unary_ops.py:213-222;
+    python/test/asc2/operations/test_softmax.py): the exact softmax of the float16
+    values (fp64 exp, sum and division; x - max is exact) rounded once to float16."""
+    row = np.asarray(row, dtype=np.float16).astype(np.float64)
+    e = np.exp(row - row.max())
+    return (e / e.sum()).astype(np.float16)
 
 
 def softmax_rows(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, tile_size: int,

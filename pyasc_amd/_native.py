@@ -46,6 +46,8 @@ SIGNATURES = {
     "asc_reduce_f32": [_c_i32, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i64, _c_p],
     "asc_rms_norm": [_c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_f32, _c_p],
     "asc_softmax_blocks_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
+    "asc_softmax_rows_f16": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
+    "asc_softmax_blocks_f16": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
     "asc_matmul": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
     "asc_matmul_bias_act": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                             _c_i32, _c_f32, _c_p],

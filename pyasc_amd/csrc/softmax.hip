@@ -259,6 +259,92 @@ bool rows_aligned(const float* x, const float* out, int64_t stride) {
   return asc::aligned16(x) && asc::aligned16(out) && (stride % 4) == 0;
 }
 
+// ---- float16 rows (asc2.softmax on an f16 tile, python/asc/language/tile/unary_ops.py:213-222;
+// python/test/asc2/operations/test_softmax.py).  fp32 statistics: x - max rounded
+// to fp32, libm expf, one reciprocal of the sum, then one RNE rounding of each
+// output to fp16.  One 256-thread workgroup per row, three passes over the row
+// (max, sum, normalise + store); 16-byte vectors of 8 halves when aligned.
+struct RowView16 {
+  const uint16_t* x;
+  uint16_t* out;
+  int64_t rows, stride;
+  int32_t len;
+  bool vec_ok;  // 16-byte aligned rows and len % 8 == 0
+};
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float half_at(const uint16_t* p, int i) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, p[i]));
+}
+__device__ __forceinline__ void halves8(u32x4_t v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v[i] & 0xffffu)));
+    f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v[i] >> 16)));
+  }
+}
+__device__ __forceinline__ uint16_t to_half(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+__global__ void __launch_bounds__(256) softmax_f16_kernel(RowView16 p) {
+  __shared__ float red[2][4];
+  const int t = threadIdx.x;
+  const int nvec = p.vec_ok ? p.len / 8 : 0;
+  for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
+    const uint16_t* row = p.x + r * p.stride;
+    uint16_t* orow = p.out + r * p.stride;
+    float m = -INFINITY;
+    for (int q = t; q < nvec; q += 256) {
+      float f[8];
+      halves8(reinterpret_cast<const u32x4_t*>(row)[q], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m = fmaxf(m, f[i]);
+    }
+    for (int c = nvec * 8 + t; c < p.len; c += 256) m = fmaxf(m, half_at(row, c));
+    m = asc::wave_max(m);
+    __syncthreads();
+    if ((t & 63) == 0) red[0][t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float s = 0.f;
+    for (int q = t; q < nvec; q += 256) {
+      float f[8];
+      halves8(reinterpret_cast<const u32x4_t*>(row)[q], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += expf(f[i] - m);
+    }
+    for (int c = nvec * 8 + t; c < p.len; c += 256) s += expf(half_at(row, c) - m);
+    s = asc::wave_sum(s);
+    if ((t & 63) == 0) red[1][t >> 6] = s;
+    __syncthreads();
+    const float rs = 1.0f / ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3]));
+    for (int q = t; q < nvec; q += 256) {
+      float f[8];
+      halves8(reinterpret_cast<const u32x4_t*>(row)[q], f);
+      u32x4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = static_cast<uint32_t>(to_half(expf(f[2 * i] - m) * rs)) |
+               (static_cast<uint32_t>(to_half(expf(f[2 * i + 1] - m) * rs)) << 16);
+      reinterpret_cast<u32x4_t*>(orow)[q] = o;
+    }
+    for (int c = nvec * 8 + t; c < p.len; c += 256) orow[c] = to_half(expf(half_at(row, c) - m) * rs);
+  }
+}
+
+int32_t launch_rows_f16(const RowView16& p, hipStream_t stream, const char* who) {
+  if (p.rows == 0 || p.len == 0) return ASC_OK;
+  const int64_t blocks = p.rows < 65536 ? p.rows : 65536;
+  hipLaunchKernelGGL(softmax_f16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, p);
+  return asc::check_launch(who);
+}
+
+bool rows_aligned16(const void* x, const void* out, int64_t stride, int64_t len) {
+  return asc::aligned16(x) && asc::aligned16(out) && (stride % 8) == 0 && (len % 8) == 0;
+}
+
 }  // namespace
 
 extern "C" int32_t asc_softmax_rows_f32(const float* x, float* out, int64_t num_rows, int64_t num_cols,
@@ -291,4 +377,37 @@ extern "C" int32_t asc_softmax_blocks_f32(const float* x, float* out, int64_t nu
   ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_softmax_blocks_f32: null buffer");
   RowView p{x, out, rows, num_cols, static_cast<int32_t>(num_cols), rows_aligned(x, out, num_cols)};
   return launch_rows(p, static_cast<hipStream_t>(stream), "asc_softmax_blocks_f32");
+}
+
+extern "C" int32_t asc_softmax_rows_f16(const void* x, void* out, int64_t num_rows, int64_t num_cols,
+                                        int32_t tile_size, int32_t grid, asc_stream_t stream) {
+  ASC_REQUIRE(num_rows >= 0 && num_cols >= 0, ASC_ERR_INVALID_ARG,
+              "asc_softmax_rows_f16: negative shape (%lld, %lld)", (long long)num_rows, (long long)num_cols);
+  ASC_REQUIRE(tile_size > 0 && grid > 0, ASC_ERR_INVALID_ARG,
+              "asc_softmax_rows_f16: need tile_size > 0 and grid > 0 (got %d, %d)", tile_size, grid);
+  ASC_REQUIRE(tile_size <= num_cols, ASC_ERR_UNSUPPORTED,
+              "asc_softmax_rows_f16: tile_size %d > num_cols %lld (the reference's padded reduction and "
+              "row-spilling store are not reproduced)",
+              tile_size, (long long)num_cols);
+  if (num_rows == 0) return ASC_OK;
+  ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_softmax_rows_f16: null buffer");
+  RowView16 p{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), num_rows, num_cols, tile_size,
+              rows_aligned16(x, out, num_cols, tile_size)};
+  return launch_rows_f16(p, static_cast<hipStream_t>(stream), "asc_softmax_rows_f16");
+}
+
+extern "C" int32_t asc_softmax_blocks_f16(const void* x, void* out, int64_t num_rows, int64_t num_cols,
+                                          int32_t block_size, int32_t grid, asc_stream_t stream) {
+  ASC_REQUIRE(num_rows >= 0 && num_cols >= 0, ASC_ERR_INVALID_ARG,
+              "asc_softmax_blocks_f16: negative shape (%lld, %lld)", (long long)num_rows, (long long)num_cols);
+  ASC_REQUIRE(block_size > 0 && grid > 0, ASC_ERR_INVALID_ARG,
+              "asc_softmax_blocks_f16: need block_size > 0 and grid > 0 (got %d, %d)", block_size, grid);
+  ASC_REQUIRE(num_cols <= INT32_MAX, ASC_ERR_UNSUPPORTED, "asc_softmax_blocks_f16: num_cols too large");
+  const int64_t reach = static_cast<int64_t>(grid) * block_size;
+  const int64_t rows = reach < num_rows ? reach : num_rows;
+  if (rows == 0 || num_cols == 0) return ASC_OK;
+  ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_softmax_blocks_f16: null buffer");
+  RowView16 p{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), rows, num_cols,
+              static_cast<int32_t>(num_cols), rows_aligned16(x, out, num_cols, num_cols)};
+  return launch_rows_f16(p, static_cast<hipStream_t>(stream), "asc_softmax_blocks_f16");
 }

@@ -144,13 +144,17 @@ def gelu_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, 
 
 # ------------------------------------------------------------------------------------------- softmax
 
-def _check_softmax(x: torch.Tensor, out: torch.Tensor, rows: int, num_cols: int) -> None:
+def _check_softmax(x: torch.Tensor, out: torch.Tensor, rows: int, num_cols: int) -> str:
+    """Checks the buffers; returns the entry-point suffix of their dtype ("f32" / "f16")."""
     for t, n in ((x, "x"), (out, "out")):
         _contiguous(_device_tensor(t, n), n)
-        if t.dtype != torch.float32:
-            raise TypeError(f"softmax supports float32 only, '{n}' is {t.dtype}")
+        if t.dtype not in (torch.float32, torch.float16):
+            raise TypeError(f"softmax supports float32 and float16, '{n}' is {t.dtype}")
         if t.numel() < rows * num_cols:
             raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {rows}x{num_cols}")
+    if out.dtype != x.dtype:
+        raise TypeError(f"'out' must be {x.dtype}, got {out.dtype}")
+    return "f32" if x.dtype == torch.float32 else "f16"
 
 
 def softmax_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, grid: int,
@@ -162,8 +166,8 @@ def softmax_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: in
     if tile_size > num_cols:
         raise ValueError(f"tile_size {tile_size} > num_cols {num_cols}: the reference kernel's reduction would "
                          "include the zero padding and its store would spill into the next row")
-    _check_softmax(x, out, num_rows, num_cols)
-    _native.call("asc_softmax_rows_f32", x.data_ptr(), out.data_ptr(), num_rows, num_cols, tile_size, grid,
+    suffix = _check_softmax(x, out, num_rows, num_cols)
+    _native.call(f"asc_softmax_rows_{suffix}", x.data_ptr(), out.data_ptr(), num_rows, num_cols, tile_size, grid,
                  _stream(stream))
 
 
@@ -179,9 +183,9 @@ def softmax_blocks(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: 
     if block_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
         raise ValueError(f"invalid softmax launch: rows={num_rows}, cols={num_cols}, block={block_size}, "
                          f"grid={grid}")
-    _check_softmax(x, out, softmax_blocks_covered(num_rows, block_size, grid), num_cols)
-    _native.call("asc_softmax_blocks_f32", x.data_ptr(), out.data_ptr(), num_rows, num_cols, block_size, grid,
-                 _stream(stream))
+    suffix = _check_softmax(x, out, softmax_blocks_covered(num_rows, block_size, grid), num_cols)
+    _native.call(f"asc_softmax_blocks_{suffix}", x.data_ptr(), out.data_ptr(), num_rows, num_cols, block_size,
+                 grid, _stream(stream))
 
 
 # ---------------------------------------------------------------------------------- reductions, rms_norm

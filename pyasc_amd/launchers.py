@@ -373,3 +373,22 @@ def _where_scalar(call: KernelCall) -> None:
     kernels.where_compare(x, call.args["scalar"], call.args["z_ptr"].reshape(-1),
                           _op_name(call.consts["op"], kernels.COMPARE_OPS, "comparison"), true_value=0,
                           false_value=1, n=x.numel(), stream=call.stream)
+
+
+
+# ------------------------------------------------------ asc2.softmax on a whole tile (operation tests)
+
+@register("softmax_1d_kernel", ("dst_ptr", "src_ptr", "length"), "python/test/asc2/operations/test_softmax.py:15-22")
+def _softmax_1d(call: KernelCall) -> None:
+    # one row of `length`; the body also stores src back unchanged
+    n = int(call.consts["length"])
+    src, dst = call.args["src_ptr"], call.args["dst_ptr"]
+    kernels.softmax_blocks(src.reshape(-1), dst.reshape(-1), 1, n, 1, 1, call.stream)
+
+
+@register("softmax_2d_kernel", ("dst_ptr", "src_ptr", "shape"), "python/test/asc2/operations/test_softmax.py:25-32")
+def _softmax_2d(call: KernelCall) -> None:
+    # softmax along the last dim of the [rows, cols] tile; the body also stores src back unchanged
+    rows, cols = _shape2(call.consts["shape"], "shape")
+    src, dst = call.args["src_ptr"], call.args["dst_ptr"]
+    kernels.softmax_blocks(src.reshape(-1), dst.reshape(-1), rows, cols, rows, 1, call.stream)

@@ -81,3 +81,75 @@ def test_extreme_rows(device):
     kernels.softmax_rows(x.to(device), out, 4, 8, 8, 2)
     torch.cuda.synchronize()
     torch.testing.assert_close(out.cpu(), torch.softmax(x, 1), rtol=RTOL, atol=0)
+
+
+# ---------------------------------------------------------------------------------------- float16
+# asc2.softmax on float16 tiles: the reference's operation test
+# (python/test/asc2/operations/test_softmax.py) unchanged in form, then the two kernel
+# signatures on float16 tensors against the oracle (within one float16 ulp: the kernel
+# rounds its fp32 result, the oracle the exact value).
+
+import asc  # noqa: E402
+import asc2  # noqa: E402
+
+
+@asc2.jit(always_compile=True)
+def softmax_1d_kernel(dst_ptr, src_ptr, length: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+@asc2.jit(always_compile=True)
+def softmax_2d_kernel(dst_ptr, src_ptr, shape: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+@pytest.mark.parametrize("dtype, shape", [(torch.float16, [1, 16]), (torch.float16, [4, 1024]),
+                                          (torch.float32, [1, 8]), (torch.float32, [4, 256])])
+def test_operations_softmax_2d(device, dtype, shape):
+    # test_softmax.py:35-45
+    src = torch.rand(shape, dtype=dtype)
+    dst = torch.zeros_like(src)
+    softmax_2d_kernel[1](dst, src, shape)
+    torch.testing.assert_close(dst, torch.softmax(src, dim=1))
+
+
+@pytest.mark.parametrize("dtype, length", [(torch.float16, 16), (torch.float16, 1024), (torch.float32, 8),
+                                           (torch.float32, 1024)])
+def test_operations_softmax_1d(device, dtype, length):
+    # test_softmax.py:48-58
+    src = torch.rand(length, dtype=dtype)
+    dst = torch.zeros_like(src)
+    softmax_1d_kernel[1](dst, src, length)
+    torch.testing.assert_close(dst, torch.softmax(src, dim=0))
+
+
+def _within_one_f16_ulp(got: np.ndarray, expected: np.ndarray):
+    diff = np.abs(got.astype(np.float64) - expected.astype(np.float64))
+    ulp = np.spacing(np.maximum(np.abs(got), np.abs(expected)).astype(np.float16)).astype(np.float64)
+    assert (diff <= ulp).all(), float((diff / ulp).max())
+
+
+@pytest.mark.parametrize("rows,cols,tile", [(4096, 4096, 4096), (37, 1000, 1000), (64, 1000, 993), (3, 100003, 100003),
+                                            (200, 8, 8), (5, 1, 1)])
+def test_f16_rows_vs_oracle(device, rows, cols, tile):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 4).half()
+    out = torch.full((rows, cols), 7.0, dtype=torch.float16, device=device)
+    kernels.softmax_rows(x.to(device), out, rows, cols, tile, 16)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    expected = np.stack([O.softmax_row(r) for r in x.numpy()[:, :tile]])
+    _within_one_f16_ulp(got[:, :tile], expected)
+    assert (got[:, tile:] == np.float16(7.0)).all()
+
+
+def test_f16_blocks_coverage(device):
+    rows, cols, block, grid = 100, 333, 7, 10  # covers rows [0, 70)
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(rows, cols, generator=g) * 2).half()
+    out = torch.full((rows, cols), 3.0, dtype=torch.float16, device=device)
+    kernels.softmax_blocks(x.to(device), out, rows, cols, block, grid)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    _within_one_f16_ulp(got[:70], np.stack([O.softmax_row(r) for r in x.numpy()[:70]]))
+    assert (got[70:] == np.float16(3.0)).all()

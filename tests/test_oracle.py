@@ -532,3 +532,25 @@ def test_where_matches_reference_golden(cmp, torch_op, dtype):
     expected = torch.where(torch_op(x, s), torch.tensor(0, dtype=td), torch.tensor(1, dtype=td))
     got = O.where_scalar(_as_oracle(x, dtype), s.item(), cmp, dtype, 0, 1)
     np.testing.assert_array_equal(got, _as_oracle(expected, dtype))
+
+
+# ---------------------------------------------------------------------------------- softmax float16
+
+def test_softmax_f16_matches_torch():
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(64, 1000, generator=g) * 3).half()
+    expected = torch.softmax(x, dim=1)  # float16 in, float16 out (fp32 math inside)
+    got = np.stack([O.softmax_row(r) for r in x.numpy()])
+    assert got.dtype == np.float16
+    # one float16 ulp apart at most: torch rounds its fp32 result, the oracle the exact value
+    diff = np.abs(got.astype(np.float64) - expected.numpy().astype(np.float64))
+    ulp = np.spacing(np.maximum(np.abs(got), np.abs(expected.numpy())).astype(np.float16)).astype(np.float64)
+    assert (diff <= ulp).all()
+
+
+def test_softmax_f16_closed_forms():
+    assert (O.softmax_row(np.full(7, 2.5, np.float16)) == np.float16(1 / 7)).all()
+    got = O.softmax_row(np.array([0.0, np.log(3)], np.float16))
+    # ln 3 in float16 is 1.0986328125; the exact softmax of the rounded input, rounded
+    e = np.exp(np.float64(np.float16(np.log(3))))
+    assert got.tolist() == [np.float16(1 / (1 + e)), np.float16(e / (1 + e))]
