@@ -315,6 +315,23 @@ int32_t asc_where_cmp(int32_t cmp, int32_t dtype, const void* x, const void* y,
                       int64_t scalar_i, double true_value, double false_value,
                       asc_stream_t stream);
 
+/* Tile load / op / store on a rectangle: z[r0+i, c0+j] = op(x[.], y[.]) for i < h,
+ * j < w in row-major [rows, cols] tensors (1-D: rows = 1), clipped at the tensor
+ * bounds as the tile store clips; op is ASC_BIN_ADD .. ASC_BIN_MINIMUM.  The
+ * offsets are the tile's (asc2.load/store with offsets, or tile_id * tile shape:
+ * python/asc/language/tile/memory_ops.py:24-31, 65-114); the kernels of
+ * python/test/asc2/operations/test_memory_ops.py:58-92. */
+int32_t asc_rect_binary(int32_t op, int32_t dtype, const void* x, const void* y,
+                        void* z, int64_t rows, int64_t cols, int64_t r0,
+                        int64_t c0, int64_t h, int64_t w, asc_stream_t stream);
+
+/* z[r, c] = x[c] for r < rows, c < cols, elements of elem_bytes (1, 2, 4, 8):
+ * asc2.broadcast_to from [1, cols], and with rows = 1 the data movement of
+ * reshape / ravel / squeeze / expand_dims (python/asc/language/tile/shape_ops.py;
+ * python/test/asc2/operations/test_shape_ops.py:47-55). */
+int32_t asc_broadcast_rows(int32_t elem_bytes, const void* x, void* z,
+                           int64_t rows, int64_t cols, asc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

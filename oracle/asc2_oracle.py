@@ -32,6 +32,9 @@ How each function is pinned (tests/test_oracle.py):
   + leaky_relu    its integer-valued recipe (exact), a hand-computed 2x2 case.
   reduce          torch sum / amax / amin / prod (the reduction tests' goldens),
                   integer-valued sums (exact), products of powers of two (exact).
+  tile add        the memory test's own golden (z[slices] = x[slices] + y[slices],
+  (memory ops)    test_memory_ops.py:104-114) on all its cases; clipping by hand.
+  broadcast_rows  torch.broadcast_to / reshape (test_shape_ops.py's goldens).
   softmax f16     torch.softmax on float16 (within one float16 ulp), constant row
                   -> 1/n rounded, two-point rows.
   rms_norm        torch.nn.functional.rms_norm in float64, constant rows (closed
@@ -457,6 +460,27 @@ def where_scalar(x: np.ndarray, s, cmp: str, dtype: str, true_value, false_value
     else:
         c = _compare(_to_f32(x, dtype), _to_f32(full(s), dtype), cmp)
     return np.where(c, full(true_value), full(false_value))
+
+
+# ------------------------------------------------------------------ tile load / store, shape ops
+
+def tile_binary(x: np.ndarray, y: np.ndarray, z: np.ndarray, op: str, tile_shape, offsets,
+                dtype: str) -> np.ndarray:
+    """asc2.load of the same tile of x and y, op, asc2.store to z (python/asc/language/
+    tile/memory_ops.py:65-114; python/test/asc2/operations/test_memory_ops.py:58-92):
+    returns a copy of z with the tile at ``offsets`` (shape ``tile_shape``, None for
+    one element) replaced, clipped at the tensor bounds as the store clips."""
+    res = z.copy()
+    shape = tile_shape if tile_shape is not None else [1] * len(offsets)
+    sl = tuple(slice(o, min(o + s, d)) for o, s, d in zip(offsets, shape, z.shape))
+    res[sl] = binary_elements(x[sl], y[sl], op, dtype)
+    return res
+
+
+def broadcast_rows(x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """asc2.broadcast_to from [1, cols] to [rows, cols] (rows = 1: the unchanged data of
+    reshape / ravel / squeeze / expand_dims; python/asc/language/tile/shape_ops.py)."""
+    return np.tile(np.asarray(x).reshape(-1)[:cols], rows).reshape(rows, cols)
 
 
 # --------------------------------------------------------------------------------- flash attention

@@ -3,6 +3,8 @@
 //   binary  python/test/asc2/operations/test_binary_ops.py:24-38  z = op(x, y), either operand may be a scalar
 //   where   python/test/asc2/operations/test_where.py:18-27, 48-55
 //           z = where(cmp(x, y), x, y)  or  z = where(cmp(x, s), 0, 1)
+//   rect    python/test/asc2/operations/test_memory_ops.py:58-92   z[tile] = x[tile] + y[tile]
+//   rows    python/test/asc2/operations/test_shape_ops.py:47-55    broadcast_to / reshape data movement
 //
 // Semantics follow the op definitions (python/asc/language/tile/binary_ops.py,
 // unary_ops.py; dtype inference utils.py:73-94): a scalar operand takes the
@@ -211,6 +213,34 @@ __global__ void __launch_bounds__(kThreads) where_kernel(int cmp, int mode, cons
   }
 }
 
+// ---- a binary op over a rectangle of a row-major [rows, cols] tensor:
+// z[r0+i, c0+j] = op(x[..], y[..]) for i < h, j < w (the tile load / add / store of
+// python/test/asc2/operations/test_memory_ops.py's kernels).
+template <class E>
+__global__ void __launch_bounds__(kThreads) rect_binary_kernel(int op, const typename E::T* __restrict__ x,
+                                                               const typename E::T* __restrict__ y,
+                                                               typename E::T* __restrict__ z, int64_t cols,
+                                                               int64_t r0, int64_t c0, int64_t h, int64_t w) {
+  const int64_t n = h * w;
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < n;
+       k += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t i = k / w, j = k - (k / w) * w;
+    const int64_t off = (r0 + i) * cols + c0 + j;
+    z[off] = binary_op<E>(op, x[off], y[off]);
+  }
+}
+
+// ---- row broadcast: z[r, c] = x[c] for r < rows (broadcast_to from [1, cols]; with
+// rows = 1 a plain copy, the data movement of reshape / ravel / squeeze / expand_dims).
+template <class T>
+__global__ void __launch_bounds__(kThreads) broadcast_rows_kernel(const T* __restrict__ x, T* __restrict__ z,
+                                                                  int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < n;
+       k += static_cast<int64_t>(gridDim.x) * kThreads)
+    z[k] = x[k % cols];
+}
+
 uint32_t grid_for(int64_t n) {
   const int64_t blocks = asc::ceil_div(n, kThreads);
   return static_cast<uint32_t>(blocks < 8192 ? blocks : 8192);
@@ -296,4 +326,62 @@ extern "C" int32_t asc_where_cmp(int32_t cmp, int32_t dtype, const void* x, cons
       return launch_where<I16>(cmp, mode, x, y, out, n, scalar_f, scalar_i, true_value, false_value, s);
     default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_where_cmp: unsupported dtype code %d", dtype);
   }
+}
+
+extern "C" int32_t asc_rect_binary(int32_t op, int32_t dtype, const void* x, const void* y, void* z, int64_t rows,
+                                   int64_t cols, int64_t r0, int64_t c0, int64_t h, int64_t w,
+                                   asc_stream_t stream) {
+  ASC_REQUIRE(op >= 0 && op <= 5, ASC_ERR_INVALID_ARG, "asc_rect_binary: op code %d is not element-wise", op);
+  ASC_REQUIRE(rows >= 0 && cols >= 0 && h >= 0 && w >= 0, ASC_ERR_INVALID_ARG, "asc_rect_binary: negative shape");
+  ASC_REQUIRE(r0 >= 0 && c0 >= 0, ASC_ERR_INVALID_ARG, "asc_rect_binary: negative offset");
+  // the store clips at the tensor bounds
+  if (r0 + h > rows) h = rows > r0 ? rows - r0 : 0;
+  if (c0 + w > cols) w = cols > c0 ? cols - c0 : 0;
+  if (h == 0 || w == 0) return ASC_OK;
+  ASC_REQUIRE(x && y && z, ASC_ERR_INVALID_ARG, "asc_rect_binary: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(h * w));
+#define ASC_RECT(E)                                                                                              \
+  hipLaunchKernelGGL(rect_binary_kernel<E>, grid, dim3(kThreads), 0, s, op, static_cast<const E::T*>(x),         \
+                     static_cast<const E::T*>(y), static_cast<E::T*>(z), cols, r0, c0, h, w);                    \
+  return asc::check_launch("asc_rect_binary")
+  switch (dtype) {
+    case ASC_DT_FLOAT32: ASC_RECT(F32);
+    case ASC_DT_FLOAT16: ASC_RECT(F16);
+    case ASC_DT_BFLOAT16: ASC_RECT(BF16);
+    case ASC_DT_INT32: ASC_RECT(I32);
+    case ASC_DT_INT16: ASC_RECT(I16);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_rect_binary: unsupported dtype code %d", dtype);
+  }
+#undef ASC_RECT
+}
+
+extern "C" int32_t asc_broadcast_rows(int32_t elem_bytes, const void* x, void* z, int64_t rows, int64_t cols,
+                                      asc_stream_t stream) {
+  ASC_REQUIRE(rows >= 0 && cols >= 0, ASC_ERR_INVALID_ARG, "asc_broadcast_rows: negative shape");
+  if (rows == 0 || cols == 0) return ASC_OK;
+  ASC_REQUIRE(x && z, ASC_ERR_INVALID_ARG, "asc_broadcast_rows: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(rows * cols));
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL(broadcast_rows_kernel<uint8_t>, grid, dim3(kThreads), 0, s, static_cast<const uint8_t*>(x),
+                         static_cast<uint8_t*>(z), rows, cols);
+      break;
+    case 2:
+      hipLaunchKernelGGL(broadcast_rows_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
+                         static_cast<const uint16_t*>(x), static_cast<uint16_t*>(z), rows, cols);
+      break;
+    case 4:
+      hipLaunchKernelGGL(broadcast_rows_kernel<uint32_t>, grid, dim3(kThreads), 0, s,
+                         static_cast<const uint32_t*>(x), static_cast<uint32_t*>(z), rows, cols);
+      break;
+    case 8:
+      hipLaunchKernelGGL(broadcast_rows_kernel<uint64_t>, grid, dim3(kThreads), 0, s,
+                         static_cast<const uint64_t*>(x), static_cast<uint64_t*>(z), rows, cols);
+      break;
+    default:
+      return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_broadcast_rows: element size %d not supported", elem_bytes);
+  }
+  return asc::check_launch("asc_broadcast_rows");
 }

@@ -449,3 +449,55 @@ def where_compare(x: torch.Tensor, y: Any, out: torch.Tensor, cmp: str, true_val
     s_f, s_i = _scalar_parts(y, x.dtype)
     _native.call("asc_where_cmp", COMPARE_OPS.index(cmp), code, x.data_ptr(), x.data_ptr(), out.data_ptr(), n, 1, s_f,
                  s_i, float(true_value), float(false_value), _stream(stream))
+
+
+# ------------------------------------------------------------------- tile load / store, shape ops
+
+def tile_offsets(tensor_shape, tile_shape, tile_id=None, offsets=None):
+    """Offsets of a tile: exactly one of ``tile_id`` (-> tile_id * tile_shape) or
+    ``offsets`` (python/asc/language/tile/memory_ops.py:24-31, 65-80)."""
+    if (tile_id is None) == (offsets is None):
+        raise ValueError("Exactly one of 'tile_id' or 'offsets' must be provided")
+    if tile_shape is not None and len(tile_shape) != len(tensor_shape):
+        raise RuntimeError("rank of 'tensor_shape' must match rank of 'shape'")
+    if tile_id is not None:
+        return [int(i) * int(s) for i, s in zip(tile_id, tile_shape)]
+    if len(offsets) != len(tensor_shape):
+        raise ValueError(f"{len(offsets)} offsets for a rank-{len(tensor_shape)} tensor")
+    return [int(o) for o in offsets]
+
+
+def tile_binary(x: torch.Tensor, y: torch.Tensor, z: torch.Tensor, op: str, tensor_shape, tile_shape, offsets,
+                stream=None) -> None:
+    """z[tile] = op(x[tile], y[tile]) for the tile at ``offsets`` of shape ``tile_shape``
+    (None: one element) in 1-D / 2-D row-major tensors of ``tensor_shape``; the store
+    clips at the tensor bounds (asc2.load, op, asc2.store)."""
+    if op not in BINARY_OPS[:6]:
+        raise ValueError(f"op {op!r} is not an element-wise binary op")
+    shape = [int(v) for v in tensor_shape]
+    if len(shape) not in (1, 2):
+        raise NotImplementedError("tiles of 1-D and 2-D tensors")
+    tile = [1] * len(shape) if tile_shape is None else [int(v) for v in tile_shape]
+    if len(tile) != len(shape) or len(offsets) != len(shape):
+        raise RuntimeError("rank of 'tensor_shape' must match rank of the tile and of 'offsets'")
+    rows, cols = (1, shape[0]) if len(shape) == 1 else shape
+    r0, c0 = (0, int(offsets[0])) if len(shape) == 1 else (int(offsets[0]), int(offsets[1]))
+    h, w = (1, tile[0]) if len(shape) == 1 else tile
+    if r0 < 0 or c0 < 0:
+        raise ValueError(f"negative tile offsets {list(offsets)}")
+    code = _code(x, "x", _TILE_DTYPES)
+    for t, name in ((x, "x"), (y, "y"), (z, "z")):
+        _flat(t, name, rows * cols)
+        if t.dtype != x.dtype:
+            raise TypeError(f"'{name}' must be {x.dtype}, got {t.dtype}")
+    _native.call("asc_rect_binary", BINARY_OPS.index(op), code, x.data_ptr(), y.data_ptr(), z.data_ptr(), rows, cols,
+                 r0, c0, h, w, _stream(stream))
+
+
+def broadcast_rows(x: torch.Tensor, z: torch.Tensor, rows: int, cols: int, stream=None) -> None:
+    """z[r, c] = x[c] for r < rows (asc2.broadcast_to from [1, cols]; rows = 1 copies)."""
+    _flat(x, "x", cols)
+    _flat(z, "z", rows * cols)
+    if z.dtype != x.dtype:
+        raise TypeError(f"'z' must be {x.dtype}, got {z.dtype}")
+    _native.call("asc_broadcast_rows", x.element_size(), x.data_ptr(), z.data_ptr(), rows, cols, _stream(stream))

@@ -392,3 +392,83 @@ def _softmax_2d(call: KernelCall) -> None:
     rows, cols = _shape2(call.consts["shape"], "shape")
     src, dst = call.args["src_ptr"], call.args["dst_ptr"]
     kernels.softmax_blocks(src.reshape(-1), dst.reshape(-1), rows, cols, rows, 1, call.stream)
+
+
+# ------------------------------------------------ tile load / add / store (test_memory_ops.py)
+# Each kernel body loads the same tile of x and y (offsets, or tile_id * tile_shape),
+# adds them and stores the sum to the same tile of z (test_memory_ops.py:58-92).
+
+def _memory_tile(call: KernelCall, tensor_shape) -> None:
+    tile_shape = call.consts.get("tile_shape")
+    offsets = kernels.tile_offsets(tensor_shape, tile_shape, call.consts.get("tile_id"), call.consts.get("offsets"))
+    kernels.tile_binary(call.args["x_ptr"].reshape(-1), call.args["y_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1),
+                        "add", tensor_shape, tile_shape, offsets, call.stream)
+
+
+@register("kernel_static", ("x_ptr", "y_ptr", "z_ptr", "tensor_shape", "tile_shape", "tile_id", "offsets"),
+          "python/test/asc2/operations/test_memory_ops.py:58-64")
+def _memory_static(call: KernelCall) -> None:
+    _memory_tile(call, [int(v) for v in call.consts["tensor_shape"]])
+
+
+@register("kernel_dynamic_1D", ("x_ptr", "y_ptr", "z_ptr", "ts0", "tile_shape", "tile_id", "offsets"),
+          "python/test/asc2/operations/test_memory_ops.py:67-73")
+def _memory_dynamic_1d(call: KernelCall) -> None:
+    _memory_tile(call, [int(call.args["ts0"])])
+
+
+@register("kernel_dynamic_2D", ("x_ptr", "y_ptr", "z_ptr", "ts0", "ts1", "tile_shape", "tile_id", "offsets"),
+          "python/test/asc2/operations/test_memory_ops.py:76-82")
+def _memory_dynamic_2d(call: KernelCall) -> None:
+    _memory_tile(call, [int(call.args["ts0"]), int(call.args["ts1"])])
+
+
+@register("kernel_scalar_load_store", ("x_ptr", "y_ptr", "z_ptr", "tensor_shape", "offsets"),
+          "python/test/asc2/operations/test_memory_ops.py:85-90")
+def _memory_scalar(call: KernelCall) -> None:
+    # shape-less loads read one element at `offsets` (memory_ops.py:70-74)
+    shape = [int(v) for v in call.consts["tensor_shape"]]
+    offsets = kernels.tile_offsets(shape, None, None, call.consts["offsets"])
+    kernels.tile_binary(call.args["x_ptr"].reshape(-1), call.args["y_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1),
+                        "add", shape, None, offsets, call.stream)
+
+
+@register("kernel", ("x_ptr", "y_ptr", "tensor_shape", "offsets"),
+          "python/test/asc2/operations/test_memory_ops.py:131-137")
+def _store_one_element(call: KernelCall) -> None:
+    # y[offsets] = x[offsets]: a scalar load stored through a 1-element tile
+    shape = [int(v) for v in call.consts["tensor_shape"]]
+    offsets = kernels.tile_offsets(shape, None, None, call.consts["offsets"])
+    if len(shape) not in (1, 2) or any(o < 0 or o >= d for o, d in zip(offsets, shape)):
+        raise ValueError(f"offsets {offsets} outside the tensor {shape}")
+    flat = offsets[0] if len(shape) == 1 else offsets[0] * shape[1] + offsets[1]
+    x, y = call.args["x_ptr"].reshape(-1), call.args["y_ptr"].reshape(-1)
+    kernels.broadcast_rows(x[flat:flat + 1], y[flat:flat + 1], 1, 1, call.stream)
+
+
+# --------------------------------------------------------------- shape operations (test_shape_ops.py)
+
+@register("kernel", ("x_ptr", "z_ptr", "input_shape", "output_shape", "in_offsets", "out_offsets", "op", "op_param"),
+          "python/test/asc2/operations/test_shape_ops.py:47-55")
+def _shape_op(call: KernelCall) -> None:
+    name = _op_name(call.consts["op"], ("broadcast_to", "reshape", "ravel", "expand_dims", "squeeze"), "shape op")
+    in_shape = [int(v) for v in call.consts["input_shape"]]
+    out_shape = [int(v) for v in call.consts["output_shape"]]
+    _zero_offsets(call.consts["in_offsets"], "in_offsets")
+    _zero_offsets(call.consts["out_offsets"], "out_offsets")
+    x, z = call.args["x_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1)
+    n_in = 1
+    for d in in_shape:
+        n_in *= d
+    n_out = 1
+    for d in out_shape:
+        n_out *= d
+    if name == "broadcast_to":
+        # [.., 1, C] -> [.., R, C]: every leading dim of the input is 1 (shape_ops broadcast rules)
+        if any(d != 1 for d in in_shape[:-1]) or in_shape[-1] != out_shape[-1]:
+            raise NotImplementedError(f"broadcast_to from {in_shape} to {out_shape}: rows of one row only")
+        kernels.broadcast_rows(x, z, n_out // out_shape[-1], out_shape[-1], call.stream)
+        return
+    if n_in != n_out:
+        raise ValueError(f"{name}: {in_shape} and {out_shape} hold different element counts")
+    kernels.broadcast_rows(x, z, 1, n_out, call.stream)  # a view change: the data are copied as they are

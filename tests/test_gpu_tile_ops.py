@@ -251,3 +251,158 @@ def test_tile_op_argument_errors(device):
         kernels.unary_f32(f, f, "not_an_op")
     with pytest.raises(ValueError):
         kernels.binary(f, f, torch.zeros(8, device=device), "add")  # output too short
+
+
+# --------------------------------------------- tile load / add / store (test_memory_ops.py)
+
+@asc2.jit(always_compile=True)
+def kernel_static(x_ptr, y_ptr, z_ptr, tensor_shape: asc.ConstExpr, tile_shape: asc.ConstExpr, tile_id: asc.ConstExpr,
+                  offsets: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+@asc2.jit(always_compile=True)
+def kernel_dynamic_1D(x_ptr, y_ptr, z_ptr, ts0, tile_shape: asc.ConstExpr, tile_id: asc.ConstExpr,
+                      offsets: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+@asc2.jit(always_compile=True)
+def kernel_dynamic_2D(x_ptr, y_ptr, z_ptr, ts0, ts1, tile_shape: asc.ConstExpr, tile_id: asc.ConstExpr,
+                      offsets: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+@asc2.jit(always_compile=True)
+def kernel_scalar_load_store(x_ptr, y_ptr, z_ptr, tensor_shape: asc.ConstExpr, offsets: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+MEMORY_TESTS = [  # test_memory_ops.py:8-48: dim, tensor_shape, tile_shape, tile_id, offsets, is_static
+    (1, [64], [16], [0], None, True), (1, [64], [16], [3], None, True), (2, [128, 128], [32, 32], [0, 0], None, True),
+    (2, [128, 128], [32, 32], [3, 3], None, True), (2, [1024, 512], [128, 64], [1, 2], None, True),
+    (1, [37], [8], [3], None, True), (2, [123, 456], [13, 16], [2, 5], None, True),
+    (1, [64], [16], None, [0], True), (1, [64], [16], None, [48], True), (2, [128, 128], [32, 32], None, [0, 0], True),
+    (2, [128, 128], [32, 32], None, [96, 64], True), (2, [1024, 512], [128, 64], None, [256, 128], True),
+    (1, [53], [16], None, [22], True), (2, [257, 511], [19, 24], None, [40, 64], True),
+    (1, [32], [8], [1], None, False), (1, [32], [8], [3], None, False), (2, [16, 2048], [4, 512], [0, 3], None, False),
+    (2, [16, 2048], [8, 256], [1, 7], None, False), (2, [512, 512], [64, 64], [4, 4], None, False),
+    (1, [99], [16], [5], None, False), (2, [1000, 1000], [33, 40], [1, 1], None, False),
+    (1, [32], [8], None, [16], False), (1, [32], [8], None, [24], False),
+    (2, [16, 2048], [4, 512], None, [8, 1024], False), (2, [16, 2048], [12, 1024], None, [4, 0], False),
+    (2, [512, 512], [64, 64], None, [128, 256], False), (1, [77], [24], None, [48], False),
+    (2, [150, 300], [21, 40], None, [10, 20], False),
+    (1, [32], None, None, [0], True), (2, [32, 32], None, None, [0, 0], True), (1, [1024], None, None, [0], True),
+    (2, [512, 512], None, None, [0, 0], True),
+]
+
+
+@pytest.mark.parametrize("dim, tensor_shape, tile_shape, tile_id, offsets, is_static", MEMORY_TESTS, ids=str)
+def test_memory_reference_cases(device, dim, tensor_shape, tile_shape, tile_id, offsets, is_static):
+    # test_memory_ops.py:95-114
+    x, y = [torch.randn(tensor_shape) for _ in range(2)]
+    z = torch.zeros(tensor_shape, dtype=torch.float32)
+    if is_static:
+        if tile_shape is None:
+            kernel_scalar_load_store[1](x, y, z, tensor_shape, offsets)
+        else:
+            kernel_static[1](x, y, z, tensor_shape, tile_shape, tile_id, offsets)
+    elif dim == 1:
+        kernel_dynamic_1D[1](x, y, z, tensor_shape[0], tile_shape, tile_id, offsets)
+    else:
+        kernel_dynamic_2D[1](x, y, z, tensor_shape[0], tensor_shape[1], tile_shape, tile_id, offsets)
+    actual = [i * s for i, s in zip(tile_id, tile_shape)] if tile_id is not None else offsets
+    slices = tuple(slice(o, o + s) for o, s in zip(actual, tile_shape)) if tile_shape is not None else tuple(actual)
+    z_expected = torch.zeros_like(z)
+    z_expected[slices] = x[slices] + y[slices]
+    torch.testing.assert_close(z, z_expected, atol=1e-3, rtol=1e-3)
+
+
+@asc2.jit(always_compile=True)
+def store_1elem_kernel(x_ptr, y_ptr, tensor_shape: asc.ConstExpr, offsets: asc.ConstExpr):
+    raise AssertionError("kernel bodies are not executed")
+
+
+store_1elem_kernel.fn_name = "kernel"  # defined as `kernel` inside the reference test (test_memory_ops.py:131)
+
+
+@pytest.mark.parametrize("tensor_shape, offsets", [((16,), (0,)), ((16,), (7,)), ((16, 16), (0, 0)),
+                                                   ((16, 16), (7, 7))], ids=str)
+def test_store_1elem_reference_cases(device, tensor_shape, offsets):
+    # test_memory_ops.py:117-143
+    x = torch.randn(tensor_shape, dtype=torch.float32)
+    y = torch.zeros_like(x)
+    store_1elem_kernel[1](x, y, tensor_shape, offsets)
+    y_ref = torch.zeros_like(x)
+    y_ref[offsets] = x[offsets]
+    torch.testing.assert_close(y, y_ref)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "int32", "float16"])
+@pytest.mark.parametrize("shape, tile, offsets", [([4096, 4096], [1000, 3000], [3500, 2000]),
+                                                  ([1, 3_000_001], [1, 2_000_000], [0, 1_500_000]),
+                                                  ([777, 333], [64, 64], [0, 300])])
+def test_tile_add_vs_oracle(device, dtype, shape, tile, offsets):
+    # large tiles that run past the tensor edge: the store clips
+    td = getattr(torch, dtype)
+    make = _float_data if td.is_floating_point else _int_data
+    n = shape[0] * shape[1]
+    x, y = make(td, 1)[:n].repeat(1 + n // N)[:n], make(td, 2)[:n].repeat(1 + n // N)[:n]
+    z = torch.zeros(n, dtype=td)
+    zd = z.to(device)
+    kernels.tile_binary(x.to(device), y.to(device), zd, "add", shape, tile, offsets)
+    torch.cuda.synchronize()
+    expected = O.tile_binary(_np(x, dtype).reshape(shape), _np(y, dtype).reshape(shape), _np(z, dtype).reshape(shape),
+                             "add", tile, offsets, dtype)
+    _assert_same(zd.cpu(), expected.reshape(-1), dtype)
+
+
+# ---------------------------------------------------------------------- shape ops (test_shape_ops.py)
+
+@asc2.jit(always_compile=True)
+def shape_kernel(x_ptr, z_ptr, input_shape: asc.ConstExpr, output_shape: asc.ConstExpr, in_offsets: asc.ConstExpr,
+                 out_offsets: asc.ConstExpr, op: asc.ConstExpr, op_param: asc.ConstExpr) -> None:
+    raise AssertionError("kernel bodies are not executed")
+
+
+shape_kernel.fn_name = "kernel"  # defined as `kernel` inside the reference test (test_shape_ops.py:47)
+
+SHAPE_OPS = [  # test_shape_ops.py:8-16
+    (asc2.broadcast_to, torch.broadcast_to, [4, 32], [1, 32]), (asc2.broadcast_to, torch.broadcast_to, [50, 32], [1, 32]),
+    (asc2.reshape, torch.reshape, [64], [2, 32]), (asc2.reshape, torch.reshape, [4, 16], [64]),
+    (asc2.ravel, torch.ravel, [], [2, 32]), (asc2.expand_dims, torch.unsqueeze, [0], [32]),
+    (asc2.squeeze, torch.squeeze, [0], [1, 32]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.int32], ids=str)
+@pytest.mark.parametrize("asc_op, torch_op, args, shape", SHAPE_OPS, ids=lambda v: getattr(v, "__name__", str(v)))
+def test_shape_reference_cases(device, asc_op, torch_op, args, shape, dtype):
+    # test_shape_ops.py:25-55
+    def create_input(tensor_shape):
+        if dtype.is_floating_point:
+            return torch.randn(tensor_shape, dtype=dtype).clamp(1, 100)
+        return torch.randint(1, 100, tensor_shape, dtype=dtype)
+
+    x = create_input(shape)
+    if asc_op in (asc2.expand_dims, asc2.squeeze):
+        ref_z = torch_op(x, dim=args[0])
+    elif not args:
+        ref_z = torch_op(x)
+    else:
+        ref_z = torch_op(x, args)
+    z = create_input(ref_z.shape)
+    in_offsets = (0,) * len(x.shape)
+    out_offsets = (0,) * len(ref_z.shape)
+    shape_kernel[1](x, z, x.shape, ref_z.shape, in_offsets, out_offsets, asc_op, args)
+    torch.testing.assert_close(z, ref_z, atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("elem", [torch.int8, torch.float16, torch.float32, torch.float64])
+def test_broadcast_rows_vs_oracle(device, elem):
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(1, 4099, generator=g) * 50).to(elem)
+    z = torch.zeros(2000, 4099, dtype=elem, device=device)
+    kernels.broadcast_rows(x.reshape(-1).to(device), z.reshape(-1), 2000, 4099)
+    torch.cuda.synchronize()
+    assert torch.equal(z.cpu(), torch.from_numpy(O.broadcast_rows(x.numpy(), 2000, 4099)))

@@ -554,3 +554,48 @@ def test_softmax_f16_closed_forms():
     # ln 3 in float16 is 1.0986328125; the exact softmax of the rounded input, rounded
     e = np.exp(np.float64(np.float16(np.log(3))))
     assert got.tolist() == [np.float16(1 / (1 + e)), np.float16(e / (1 + e))]
+
+
+# --------------------------------------------------------------------- tile load / store, shape ops
+
+MEMORY_CASES = [  # test_memory_ops.py:8-48 (dim, tensor_shape, tile_shape, tile_id, offsets)
+    (1, [64], [16], [3], None), (2, [128, 128], [32, 32], [3, 3], None), (2, [1024, 512], [128, 64], [1, 2], None),
+    (1, [37], [8], [3], None), (2, [123, 456], [13, 16], [2, 5], None), (1, [53], [16], None, [22]),
+    (2, [257, 511], [19, 24], None, [40, 64]), (2, [1000, 1000], [33, 40], [1, 1], None),
+    (2, [150, 300], [21, 40], None, [10, 20]), (2, [512, 512], None, None, [0, 0]), (1, [1024], None, None, [0]),
+]
+
+
+@pytest.mark.parametrize("dim, tensor_shape, tile_shape, tile_id, offsets", MEMORY_CASES, ids=str)
+def test_tile_binary_matches_memory_test_golden(dim, tensor_shape, tile_shape, tile_id, offsets):
+    from pyasc_amd.kernels import tile_offsets
+    g = torch.Generator().manual_seed(41)
+    x, y = [torch.randn(tensor_shape, generator=g) for _ in range(2)]
+    z = torch.zeros(tensor_shape)
+    offs = tile_offsets(tensor_shape, tile_shape, tile_id, offsets)
+    got = O.tile_binary(x.numpy(), y.numpy(), z.numpy(), "add", tile_shape, offs, "float32")
+    # test_memory_ops.py:104-114
+    actual = [i * s for i, s in zip(tile_id, tile_shape)] if tile_id is not None else offsets
+    slices = tuple(slice(o, o + s) for o, s in zip(actual, tile_shape)) if tile_shape is not None else tuple(actual)
+    expected = torch.zeros_like(z)
+    expected[slices] = x[slices] + y[slices]
+    np.testing.assert_array_equal(got, expected.numpy())
+
+
+def test_tile_binary_clips_and_offsets_rules():
+    from pyasc_amd.kernels import tile_offsets
+    x = np.arange(10, dtype=np.float32)
+    got = O.tile_binary(x, x, np.zeros(10, np.float32), "add", [4], [8], "float32")
+    assert got.tolist() == [0] * 8 + [16, 18]  # a tile past the end is clipped by the store
+    with pytest.raises(ValueError):
+        tile_offsets([10], [4], [1], [4])  # exactly one of tile_id / offsets
+    with pytest.raises(ValueError):
+        tile_offsets([10], [4], None, None)
+    assert tile_offsets([64, 64], [8, 16], [2, 3], None) == [16, 48]
+
+
+@pytest.mark.parametrize("rows, cols", [(4, 32), (50, 32), (1, 64)])
+def test_broadcast_rows_matches_torch(rows, cols):
+    x = torch.randn(1, cols)
+    np.testing.assert_array_equal(O.broadcast_rows(x.numpy(), rows, cols), torch.broadcast_to(x, (rows, cols)).numpy())
+    np.testing.assert_array_equal(O.broadcast_rows(x.numpy(), 1, cols).reshape(-1), torch.ravel(x).numpy())
