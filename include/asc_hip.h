@@ -332,6 +332,24 @@ int32_t asc_rect_binary(int32_t op, int32_t dtype, const void* x, const void* y,
 int32_t asc_broadcast_rows(int32_t elem_bytes, const void* x, void* z,
                            int64_t rows, int64_t cols, asc_stream_t stream);
 
+/* Atomic combine of tiles: z[j] = op(z[j], x[b * tile_len + j] + c) for b < n_tiles,
+ * j < tile_len, each combine atomic (op: ASC_BIN_ADD, ASC_BIN_MAXIMUM or
+ * ASC_BIN_MINIMUM; dtype float32 / float16 / bfloat16 / int32 / int16; c converted to
+ * the element type as asc_binary's scalar).  Replaces the atomic store of
+ * asc2.atomic_add / atomic_max / atomic_min (python/asc/language/tile/atomic_ops.py:19-33)
+ * in the kernel of python/test/asc2/operations/test_atomic_ops.py:33-40, whose
+ * workgroup b combines tile b.  Float add order is unspecified; the others are
+ * order-independent. */
+int32_t asc_atomic_tiles(int32_t op, int32_t dtype, const void* x, void* z,
+                         int64_t n_tiles, int64_t tile_len, double c_f,
+                         int64_t c_i, asc_stream_t stream);
+
+/* z[i] = c for i < n, c converted to the element type as asc_binary's scalar:
+ * asc2.full(...) (python/asc/language/tile/creation_ops.py:20-31) broadcast to the
+ * tensor's shape and stored whole (python/test/asc2/operations/test_shape_ops.py:64-78). */
+int32_t asc_fill(int32_t dtype, void* z, int64_t n, double c_f, int64_t c_i,
+                 asc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

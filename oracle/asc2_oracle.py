@@ -35,6 +35,10 @@ How each function is pinned (tests/test_oracle.py):
   tile add        the memory test's own golden (z[slices] = x[slices] + y[slices],
   (memory ops)    test_memory_ops.py:104-114) on all its cases; clipping by hand.
   broadcast_rows  torch.broadcast_to / reshape (test_shape_ops.py's goldens).
+  atomic tiles    the atomic test's golden (torch add / maximum / minimum folded over
+                  the blocks, test_atomic_ops.py:62-67); closed forms: the column sum
+                  plus n_tiles * addend (integers), the column max / min plus addend.
+  fill            torch.full (test_shape_ops.py:75-78).
   softmax f16     torch.softmax on float16 (within one float16 ulp), constant row
                   -> 1/n rounded, two-point rows.
   rms_norm        torch.nn.functional.rms_norm in float64, constant rows (closed
@@ -481,6 +485,32 @@ def broadcast_rows(x: np.ndarray, rows: int, cols: int) -> np.ndarray:
     """asc2.broadcast_to from [1, cols] to [rows, cols] (rows = 1: the unchanged data of
     reshape / ravel / squeeze / expand_dims; python/asc/language/tile/shape_ops.py)."""
     return np.tile(np.asarray(x).reshape(-1)[:cols], rows).reshape(rows, cols)
+
+
+def atomic_tiles(x: np.ndarray, z: np.ndarray, op: str, n_tiles: int, tile_len: int, addend,
+                 dtype: str) -> np.ndarray:
+    """asc2.atomic_add / atomic_max / atomic_min of tile b of x plus ``addend`` into
+    z[0:tile_len] for b < n_tiles (python/asc/language/tile/atomic_ops.py:19-33, a store in
+    atomic mode, lib/Conversion/LowerToAsc/LowerAtomic.cpp:44-70; the kernel and golden of
+    python/test/asc2/operations/test_atomic_ops.py:33-68): the tiles combine in block
+    order, each combine being the element type's binary op."""
+    x = np.asarray(x).reshape(-1)
+    res = np.asarray(z).reshape(-1)[:tile_len].copy()
+    c = np.full(tile_len, addend).astype(res.dtype) if dtype != "bfloat16" else \
+        f32_to_bf16_bits(np.full(tile_len, addend, dtype=np.float32))
+    for b in range(n_tiles):
+        tile = binary_elements(x[b * tile_len:(b + 1) * tile_len], c, "add", dtype)
+        res = binary_elements(res, tile, op, dtype)
+    return res
+
+
+def fill(n: int, value, dtype: str) -> np.ndarray:
+    """asc2.full([1], value, dtype) broadcast to n elements and stored
+    (python/asc/language/tile/creation_ops.py:20-31; test_shape_ops.py:64-78)."""
+    if dtype == "bfloat16":
+        return f32_to_bf16_bits(np.full(n, value, dtype=np.float32))
+    with np.errstate(over="ignore"):  # float16 overflow rounds to inf, as the device conversion does
+        return np.full(n, value).astype(np.dtype(dtype))
 
 
 # --------------------------------------------------------------------------------- flash attention

@@ -5,6 +5,8 @@
 //           z = where(cmp(x, y), x, y)  or  z = where(cmp(x, s), 0, 1)
 //   rect    python/test/asc2/operations/test_memory_ops.py:58-92   z[tile] = x[tile] + y[tile]
 //   rows    python/test/asc2/operations/test_shape_ops.py:47-55    broadcast_to / reshape data movement
+//   atomic  python/test/asc2/operations/test_atomic_ops.py:33-40   z[j] = op(z[j], x[b, j] + c), atomically
+//   fill    python/test/asc2/operations/test_shape_ops.py:64-78    z = full([1], c).broadcast_to(shape)
 //
 // Semantics follow the op definitions (python/asc/language/tile/binary_ops.py,
 // unary_ops.py; dtype inference utils.py:73-94): a scalar operand takes the
@@ -241,6 +243,78 @@ __global__ void __launch_bounds__(kThreads) broadcast_rows_kernel(const T* __res
     z[k] = x[k % cols];
 }
 
+// ---- atomic combine.  An asc2 atomic op is a store in atomic mode
+// (python/asc/language/tile/atomic_ops.py:19-33, lowered to a store bracketed by
+// SetAtomicAdd/Max/Min ... SetAtomicNone in lib/Conversion/LowerToAsc/LowerAtomic.cpp:44-70):
+// every element of the tile is combined into the destination.  Here tile b of x (tile_len
+// elements), plus the scalar c in the element type, is combined into z[0, tile_len) for
+// b < n_tiles, the body of the reference test with one workgroup range per tile.
+// 32-bit integers use the hardware atomics (relaxed, device scope), fp32 add the hardware
+// float add; fp32 max/min and every 16-bit element type run a compare-and-swap loop on the
+// enclosing aligned 32-bit word (the other half is written back unchanged, and a concurrent
+// change to it makes the swap fail and retry).  The combine of each element is the binary
+// op of the element type (rounded once for 16-bit floats; IEEE maximum/minimum).
+template <class E>
+__device__ __forceinline__ void atomic_combine(int op, typename E::T* p, typename E::T v) {
+  using T = typename E::T;
+  if constexpr (sizeof(T) == 4 && !E::kFloat) {
+    if (op == 0)
+      __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else if (op == 4)
+      __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      __hip_atomic_fetch_min(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (sizeof(T) == 4) {
+    if (op == 0) {
+      __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    uint32_t* w = reinterpret_cast<uint32_t*>(p);
+    uint32_t old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+      const uint32_t nw = __float_as_uint(binary_op<E>(op, __uint_as_float(old), v));
+      if (nw == old) return;
+      if (__hip_atomic_compare_exchange_strong(w, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
+        return;
+    }
+  } else {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    uint32_t* w = reinterpret_cast<uint32_t*>(a & ~uintptr_t(3));
+    const int shift = (a & 2) ? 16 : 0;
+    uint32_t old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+      const T cur = static_cast<T>(static_cast<uint16_t>(old >> shift));
+      const uint16_t r = static_cast<uint16_t>(binary_op<E>(op, cur, v));
+      const uint32_t nw = (old & ~(0xffffu << shift)) | (static_cast<uint32_t>(r) << shift);
+      if (nw == old) return;
+      if (__hip_atomic_compare_exchange_strong(w, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
+        return;
+    }
+  }
+}
+
+template <class E>
+__global__ void __launch_bounds__(kThreads) atomic_tiles_kernel(int op, const typename E::T* __restrict__ x,
+                                                                typename E::T* z, int64_t tile_len, int64_t n,
+                                                                float c_f, int64_t c_i) {
+  const typename E::T c = element_of<E>(c_f, c_i);
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < n;
+       k += static_cast<int64_t>(gridDim.x) * kThreads)
+    atomic_combine<E>(op, z + (k - (k / tile_len) * tile_len), binary_op<E>(0, x[k], c));
+}
+
+// ---- fill: every element of z takes the scalar c converted to the element type
+template <class E>
+__global__ void __launch_bounds__(kThreads) fill_kernel(typename E::T* __restrict__ z, int64_t n, float c_f,
+                                                        int64_t c_i) {
+  const typename E::T c = element_of<E>(c_f, c_i);
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < n;
+       k += static_cast<int64_t>(gridDim.x) * kThreads)
+    z[k] = c;
+}
+
 uint32_t grid_for(int64_t n) {
   const int64_t blocks = asc::ceil_div(n, kThreads);
   return static_cast<uint32_t>(blocks < 8192 ? blocks : 8192);
@@ -384,4 +458,51 @@ extern "C" int32_t asc_broadcast_rows(int32_t elem_bytes, const void* x, void* z
       return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_broadcast_rows: element size %d not supported", elem_bytes);
   }
   return asc::check_launch("asc_broadcast_rows");
+}
+
+extern "C" int32_t asc_atomic_tiles(int32_t op, int32_t dtype, const void* x, void* z, int64_t n_tiles,
+                                    int64_t tile_len, double c_f, int64_t c_i, asc_stream_t stream) {
+  ASC_REQUIRE(op == ASC_BIN_ADD || op == ASC_BIN_MAXIMUM || op == ASC_BIN_MINIMUM, ASC_ERR_INVALID_ARG,
+              "asc_atomic_tiles: op code %d is not add / maximum / minimum", op);
+  ASC_REQUIRE(n_tiles >= 0 && tile_len >= 0, ASC_ERR_INVALID_ARG, "asc_atomic_tiles: negative shape");
+  if (n_tiles == 0 || tile_len == 0) return ASC_OK;
+  ASC_REQUIRE(n_tiles <= INT64_MAX / tile_len, ASC_ERR_INVALID_ARG, "asc_atomic_tiles: size overflows");
+  ASC_REQUIRE(x && z, ASC_ERR_INVALID_ARG, "asc_atomic_tiles: null buffer");
+  const int64_t n = n_tiles * tile_len;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n));
+#define ASC_ATOMIC(E)                                                                                            \
+  hipLaunchKernelGGL(atomic_tiles_kernel<E>, grid, dim3(kThreads), 0, s, op, static_cast<const E::T*>(x),        \
+                     static_cast<E::T*>(z), tile_len, n, static_cast<float>(c_f), c_i);                          \
+  return asc::check_launch("asc_atomic_tiles")
+  switch (dtype) {
+    case ASC_DT_FLOAT32: ASC_ATOMIC(F32);
+    case ASC_DT_FLOAT16: ASC_ATOMIC(F16);
+    case ASC_DT_BFLOAT16: ASC_ATOMIC(BF16);
+    case ASC_DT_INT32: ASC_ATOMIC(I32);
+    case ASC_DT_INT16: ASC_ATOMIC(I16);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_atomic_tiles: unsupported dtype code %d", dtype);
+  }
+#undef ASC_ATOMIC
+}
+
+extern "C" int32_t asc_fill(int32_t dtype, void* z, int64_t n, double c_f, int64_t c_i, asc_stream_t stream) {
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_fill: negative length");
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(z, ASC_ERR_INVALID_ARG, "asc_fill: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n));
+#define ASC_FILL(E)                                                                                              \
+  hipLaunchKernelGGL(fill_kernel<E>, grid, dim3(kThreads), 0, s, static_cast<E::T*>(z), n,                       \
+                     static_cast<float>(c_f), c_i);                                                              \
+  return asc::check_launch("asc_fill")
+  switch (dtype) {
+    case ASC_DT_FLOAT32: ASC_FILL(F32);
+    case ASC_DT_FLOAT16: ASC_FILL(F16);
+    case ASC_DT_BFLOAT16: ASC_FILL(BF16);
+    case ASC_DT_INT32: ASC_FILL(I32);
+    case ASC_DT_INT16: ASC_FILL(I16);
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_fill: unsupported dtype code %d", dtype);
+  }
+#undef ASC_FILL
 }

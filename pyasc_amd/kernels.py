@@ -501,3 +501,36 @@ def broadcast_rows(x: torch.Tensor, z: torch.Tensor, rows: int, cols: int, strea
     if z.dtype != x.dtype:
         raise TypeError(f"'z' must be {x.dtype}, got {z.dtype}")
     _native.call("asc_broadcast_rows", x.element_size(), x.data_ptr(), z.data_ptr(), rows, cols, _stream(stream))
+
+
+ATOMIC_OPS = ("add", "maximum", "minimum")
+
+
+def atomic_tiles(x: torch.Tensor, z: torch.Tensor, op: str, n_tiles: int, tile_len: int, addend=0,
+                 stream=None) -> None:
+    """z[j] = op(z[j], x[b * tile_len + j] + addend) for b < n_tiles, each combine atomic
+    (asc2.atomic_add / atomic_max / atomic_min, python/asc/language/tile/atomic_ops.py:19-33;
+    the kernel of python/test/asc2/operations/test_atomic_ops.py:33-40).  The order in which
+    the tiles' float sums land is unspecified."""
+    if op not in ATOMIC_OPS:
+        raise ValueError(f"unknown atomic op {op!r}; expected one of {ATOMIC_OPS}")
+    n_tiles, tile_len = int(n_tiles), int(tile_len)
+    if n_tiles < 0 or tile_len < 0:
+        raise ValueError("n_tiles and tile_len must be non-negative")
+    code = _code(x, "x", _TILE_DTYPES)
+    _flat(x, "x", n_tiles * tile_len)
+    _flat(z, "z", tile_len)
+    if z.dtype != x.dtype:
+        raise TypeError(f"'z' must be {x.dtype}, got {z.dtype}")
+    c_f, c_i = _scalar_parts(addend, x.dtype)
+    _native.call("asc_atomic_tiles", BINARY_OPS.index(op), code, x.data_ptr(), z.data_ptr(), n_tiles, tile_len, c_f,
+                 c_i, _stream(stream))
+
+
+def fill(z: torch.Tensor, value, n: Optional[int] = None, stream=None) -> None:
+    """z[:n] = value in z's element type (asc2.full broadcast to the tensor and stored)."""
+    n = z.numel() if n is None else int(n)
+    code = _code(z, "z", _TILE_DTYPES)
+    _flat(z, "z", n)
+    c_f, c_i = _scalar_parts(value, z.dtype)
+    _native.call("asc_fill", code, z.data_ptr(), n, c_f, c_i, _stream(stream))

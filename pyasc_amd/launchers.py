@@ -472,3 +472,32 @@ def _shape_op(call: KernelCall) -> None:
     if n_in != n_out:
         raise ValueError(f"{name}: {in_shape} and {out_shape} hold different element counts")
     kernels.broadcast_rows(x, z, 1, n_out, call.stream)  # a view change: the data are copied as they are
+
+
+# ------------------------------------------------------------------ atomic ops (test_atomic_ops.py)
+
+@register("kernel", ("x_ptr", "z_ptr", "tensor_shape", "tile_length", "op"),
+          "python/test/asc2/operations/test_atomic_ops.py:33-40")
+def _atomic_op(call: KernelCall) -> None:
+    # block b loads x[b*tile_length : (b+1)*tile_length], adds full_like(.., 10) and combines
+    # the tile into z[0:tile_length] with the atomic op
+    name = _op_name(call.consts["op"], ("atomic_add", "atomic_max", "atomic_min"), "atomic op")
+    size = 1
+    for d in call.consts["tensor_shape"]:
+        size *= int(d)
+    tile_length = int(call.consts["tile_length"])
+    if call.grid * tile_length > size:
+        raise ValueError(f"{call.grid} blocks of {tile_length} elements read past the {size}-element tensor")
+    op = {"atomic_add": "add", "atomic_max": "maximum", "atomic_min": "minimum"}[name]
+    kernels.atomic_tiles(call.args["x_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1), op, call.grid, tile_length,
+                         10, call.stream)
+
+
+@register("kernel", ("out_ptr", "shape", "offsets"), "python/test/asc2/operations/test_shape_ops.py:68-72")
+def _broadcast_dup(call: KernelCall) -> None:
+    # asc2.full([1], 777, dtype).broadcast_to(*shape), stored over the whole tensor
+    _zero_offsets(call.consts["offsets"], "offsets")
+    n = 1
+    for d in call.consts["shape"]:
+        n *= int(d)
+    kernels.fill(call.args["out_ptr"].reshape(-1), 777, n, call.stream)

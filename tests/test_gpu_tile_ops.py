@@ -406,3 +406,101 @@ def test_broadcast_rows_vs_oracle(device, elem):
     kernels.broadcast_rows(x.reshape(-1).to(device), z.reshape(-1), 2000, 4099)
     torch.cuda.synchronize()
     assert torch.equal(z.cpu(), torch.from_numpy(O.broadcast_rows(x.numpy(), 2000, 4099)))
+
+
+# ---------------------------------------------------------------------- atomic ops (test_atomic_ops.py)
+
+@asc2.jit(always_compile=True)
+def atomic_kernel(x_ptr: asc.GlobalAddress, z_ptr: asc.GlobalAddress, tensor_shape: asc.ConstExpr,
+                  tile_length: asc.ConstExpr, op: asc.ConstExpr):
+    raise AssertionError("kernel bodies are not executed")
+
+
+atomic_kernel.fn_name = "kernel"  # defined as `kernel` in the reference test (test_atomic_ops.py:33)
+
+ATOMIC_OPS = [(asc2.atomic_add, torch.add), (asc2.atomic_max, torch.maximum), (asc2.atomic_min, torch.minimum)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.int32], ids=str)
+@pytest.mark.parametrize("asc_op, torch_op", ATOMIC_OPS, ids=lambda v: getattr(v, "__name__", str(v)))
+def test_atomic_reference_cases(device, asc_op, torch_op, dtype):
+    # test_atomic_ops.py:45-68 (USE_CORE_NUM = 4 blocks over a 128-element tensor)
+    def create_input(shape):
+        if dtype == torch.float32:
+            return torch.clamp(torch.randn(tuple(shape), dtype=dtype), 1, 100)
+        return torch.randint(1, 100, tuple(shape), dtype=dtype)
+
+    tile_length = 128 // 4
+    x = create_input([128])
+    z = create_input([tile_length])
+    expected_z = z.clone()
+    atomic_kernel[4](x, z, [128], tile_length, asc_op)
+    for i in range(4):
+        expected_z = torch_op(expected_z, x[i * tile_length:(i + 1) * tile_length] + 10)
+    torch.testing.assert_close(z, expected_z, atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int32", "int16"])
+@pytest.mark.parametrize("op", ["add", "maximum", "minimum"])
+@pytest.mark.parametrize("n_tiles, tile_len", [(64, (1 << 16) + 37), (1000, 257), (3, 1)])
+def test_atomic_tiles_vs_oracle(device, op, dtype, n_tiles, tile_len):
+    # max / min are order-independent (IEEE maximum / minimum, signed integers): random data
+    # with edge values, bit-exact.  Integer add wraps, so any order gives the same bits.
+    # Float add: tile values x + 3 in {0, 1}, so every partial sum, in any order, lies
+    # between z and the column total, which stays below 256 (exact in bfloat16 too).
+    td = getattr(torch, dtype)
+    n = n_tiles * tile_len
+    if td.is_floating_point and op == "add":
+        g = torch.Generator().manual_seed(n_tiles)
+        p = min(0.5, 100 / n_tiles)
+        x = (torch.rand(n, generator=g) < p).to(torch.int32).sub(3).to(td)
+        z0 = torch.randint(0, 9, (tile_len,), generator=g).to(td)
+        totals = z0.to(torch.int64) + (x.to(torch.int64) + 3).reshape(n_tiles, tile_len).sum(0)
+        assert int(totals.max()) < 256
+    else:
+        make = _float_data if td.is_floating_point else _int_data
+        x = make(td, 1).repeat(1 + n // N)[:n]
+        z0 = make(td, 2)[:tile_len]
+    addend = 3 if td.is_floating_point and op == "add" else (-2 if op == "minimum" else 1)
+    # z at an odd element offset: the 16-bit combines run on both halves of each word
+    buf = torch.zeros(tile_len + 1, dtype=td, device=device)
+    z = buf[1:]
+    z.copy_(z0.to(device))
+    kernels.atomic_tiles(x.to(device), z, op, n_tiles, tile_len, addend)
+    torch.cuda.synchronize()
+    expected = O.atomic_tiles(_np(x, dtype), _np(z0, dtype), op, n_tiles, tile_len, addend, dtype)
+    _assert_same(z.cpu(), expected, dtype)
+    assert _np(buf[:1].cpu(), dtype).view(np.uint8).sum() == 0  # the element before z is untouched
+
+
+@asc2.jit(always_compile=True)
+def broadcast_dup_kernel(out_ptr, shape: asc.ConstExpr, offsets: asc.ConstExpr):
+    raise AssertionError("kernel bodies are not executed")
+
+
+broadcast_dup_kernel.fn_name = "kernel"  # defined as `kernel` inside the reference test (test_shape_ops.py:68)
+
+
+@pytest.mark.parametrize("shape", ([32], [3, 32]), ids=str)
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32, torch.int16, torch.int32), ids=str)
+def test_broadcast_dup_reference_cases(device, shape, dtype):
+    # test_shape_ops.py:62-78
+    out = torch.zeros(shape, dtype=dtype)
+    out_ref = torch.full_like(out, 777)
+    size = tuple(out.size())
+    broadcast_dup_kernel[1](out, size, [0] * len(size))
+    torch.testing.assert_close(out, out_ref, atol=1e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int32", "int16"])
+@pytest.mark.parametrize("value", [777, -3.75, 1e30])
+def test_fill_vs_oracle(device, dtype, value):
+    td = getattr(torch, dtype)
+    if not td.is_floating_point and value != 777:
+        value = -123456 if dtype == "int32" else -1234
+    z = torch.zeros((1 << 22) + 3, dtype=td, device=device)
+    kernels.fill(z, value, z.numel() - 1)
+    torch.cuda.synchronize()
+    got = z.cpu()
+    _assert_same(got[:-1], O.fill(z.numel() - 1, value, dtype), dtype)
+    assert _np(got[-1:], dtype).view(np.uint8).sum() == 0

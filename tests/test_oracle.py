@@ -599,3 +599,59 @@ def test_broadcast_rows_matches_torch(rows, cols):
     x = torch.randn(1, cols)
     np.testing.assert_array_equal(O.broadcast_rows(x.numpy(), rows, cols), torch.broadcast_to(x, (rows, cols)).numpy())
     np.testing.assert_array_equal(O.broadcast_rows(x.numpy(), 1, cols).reshape(-1), torch.ravel(x).numpy())
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "int32"])
+@pytest.mark.parametrize("op, torch_op", [("add", torch.add), ("maximum", torch.maximum), ("minimum", torch.minimum)])
+def test_atomic_tiles_matches_atomic_test_golden(op, torch_op, dtype):
+    # test_atomic_ops.py:45-68: 4 blocks of 32 over a 128-element x, +10 in the body
+    td = getattr(torch, dtype)
+    g = torch.Generator().manual_seed(11)
+    if td.is_floating_point:
+        x = torch.randn(128, generator=g).clamp(1, 100).to(td)
+        z = torch.randn(32, generator=g).clamp(1, 100).to(td)
+    else:
+        x = torch.randint(1, 100, (128,), generator=g, dtype=td)
+        z = torch.randint(1, 100, (32,), generator=g, dtype=td)
+    expected = z.clone()
+    for i in range(4):
+        expected = torch_op(expected, x[i * 32:(i + 1) * 32] + 10)
+    got = O.atomic_tiles(x.numpy(), z.numpy(), op, 4, 32, 10, dtype)
+    np.testing.assert_allclose(got, expected.numpy(), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", ["int32", "int16", "float16", "bfloat16", "float32"])
+def test_atomic_tiles_closed_forms(dtype):
+    # integer-valued data with every partial sum below 256 in magnitude: each combine is
+    # exact (bfloat16 too), so the result is a column reduction
+    rng = np.random.default_rng(5)
+    xv = rng.integers(-2, 3, size=(37, 53))
+    zv = rng.integers(-30, 31, size=53)
+
+    def enc(v):
+        return O.f32_to_bf16_bits(v.astype(np.float32)) if dtype == "bfloat16" else v.astype(np.dtype(dtype))
+
+    def dec(v):
+        return O.bf16_bits_to_f32(v) if dtype == "bfloat16" else v
+    x, z = enc(xv).reshape(-1), enc(zv)
+    np.testing.assert_array_equal(dec(O.atomic_tiles(x, z, "add", 37, 53, 3, dtype)), zv + xv.sum(0) + 37 * 3)
+    np.testing.assert_array_equal(dec(O.atomic_tiles(x, z, "maximum", 37, 53, 3, dtype)),
+                                  np.maximum(zv, xv.max(0) + 3))
+    np.testing.assert_array_equal(dec(O.atomic_tiles(x, z, "minimum", 37, 53, -4, dtype)),
+                                  np.minimum(zv, xv.min(0) - 4))
+    # no tiles: z unchanged
+    np.testing.assert_array_equal(O.atomic_tiles(x, z, "add", 0, 53, 3, dtype), z)
+
+
+def test_atomic_tiles_int_wraps():
+    x = np.array([2**31 - 1, 5], dtype=np.int32)
+    z = np.array([1, 0], dtype=np.int32)
+    np.testing.assert_array_equal(O.atomic_tiles(x, z, "add", 1, 2, 0, "int32"), np.array([-2**31, 5], np.int32))
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32", "int16", "int32", "bfloat16"])
+def test_fill_matches_torch_full(dtype):
+    td = getattr(torch, dtype)
+    ref = torch.full((3, 32), 777, dtype=td).reshape(-1)
+    ref_np = ref.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else ref.numpy()
+    np.testing.assert_array_equal(O.fill(96, 777, dtype), ref_np)
