@@ -143,8 +143,8 @@ int32_t asc_softmax_blocks_f32(const float* x, float* out, int64_t num_rows,
                                int64_t num_cols, int32_t block_size,
                                int32_t grid, asc_stream_t stream);
 
-/* The same two kernels on float16 x / out (asc2.softmax on an f16 tile: SURVEY-
- * listed "f16 also allowed", python/asc/language/tile/unary_ops.py:213-222;
+/* The same two kernels on float16 x / out (asc2.softmax on an f16 tile,
+ * which the op allows: python/asc/language/tile/unary_ops.py:213-222;
  * python/test/asc2/operations/test_softmax.py).  fp32 statistics (x - max in
  * fp32, libm exp, one reciprocal of the sum), each output rounded once (RNE)
  * to float16.  Same coverage rules as the float32 entries. */

@@ -1,4 +1,4 @@
-"""Matmul with a bias + activation epilogue on the GPU (SURVEY next-row: the
+"""Matmul with a bias + activation epilogue on the GPU (the
 05_matmul_leakyrelu tutorial, python/tutorials/05_matmul_leakyrelu/matmul_leakyrelu.py).
 
 The tutorial's kernel is declared with its own signature and launched through the

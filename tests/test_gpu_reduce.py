@@ -1,4 +1,4 @@
-"""Reductions and RMS norm on the GPU (SURVEY next-row: row reductions and rms_norm).
+"""Reductions and RMS norm on the GPU (row reductions and rms_norm).
 
 First the reference's own reduction tests (python/test/asc2/operations/
 test_reduce_ops.py): the same kernels, parametrisation and goldens (torch sum /
