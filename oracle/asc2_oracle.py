@@ -35,6 +35,8 @@ How each function is pinned (tests/test_oracle.py):
   tile add        the memory test's own golden (z[slices] = x[slices] + y[slices],
   (memory ops)    test_memory_ops.py:104-114) on all its cases; clipping by hand.
   broadcast_rows  torch.broadcast_to / reshape (test_shape_ops.py's goldens).
+  block_add       the asc1 vadd test's golden (x + y, test_vadd.py:85-92) at its launch
+                  parameters, a literal walk of the body's tile loop, hand-worked gaps.
   atomic tiles    the atomic test's golden (torch add / maximum / minimum folded over
                   the blocks, test_atomic_ops.py:62-67); closed forms: the column sum
                   plus n_tiles * addend (integers), the column max / min plus addend.
@@ -99,6 +101,21 @@ def vadd(x: np.ndarray, y: np.ndarray, out: np.ndarray, size: int, tile_size: in
     res = out.copy()
     n = vadd_covered(size, tile_size, tile_per_block, grid)
     res[:n] = add_elements(x[:n], y[:n], dtype)
+    return res
+
+
+def block_add(x: np.ndarray, y: np.ndarray, z: np.ndarray, grid: int, block_stride: int, block_cover: int,
+              dtype: str = "float32") -> np.ndarray:
+    """The asc1 vadd bodies (python/test/kernels/test_vadd.py:16-35; python/tutorials/01_add/
+    add.py:29-70, 02_add_framework/add_framework.py:29-80): block b < grid views x, y, z from
+    b * block_stride and adds ``block_cover`` elements (TILE_NUM tiles of TILE_LENGTH).
+    Returns a copy of z with the union of the blocks written, clipped at z's length."""
+    res = np.asarray(z).copy()
+    n = res.size
+    starts = np.arange(grid, dtype=np.int64) * block_stride
+    idx = (starts[:, None] + np.arange(block_cover, dtype=np.int64)[None, :]).reshape(-1)
+    idx = np.unique(idx[idx < n])
+    res[idx] = add_elements(np.asarray(x)[idx], np.asarray(y)[idx], dtype)
     return res
 
 

@@ -24,8 +24,9 @@ __version__ = "0.1.0"
 
 
 def install_aliases() -> None:
-    """Makes ``import asc``, ``import asc2`` and ``import asc.runtime.config`` resolve to this
-    package, so code written against the reference imports unchanged."""
+    """Makes ``import asc``, ``import asc2``, ``import asc.runtime.config`` and
+    ``import asc.lib.runtime`` resolve to this package, so code written against the
+    reference imports unchanged."""
     from .asc import runtime
     from .asc.runtime import config, jit, launcher
     sys.modules.setdefault("asc", asc)
@@ -33,4 +34,8 @@ def install_aliases() -> None:
     sys.modules.setdefault("asc.runtime.config", config)
     sys.modules.setdefault("asc.runtime.jit", jit)
     sys.modules.setdefault("asc.runtime.launcher", launcher)
+    from .asc import lib
+    from .asc.lib import runtime as lib_runtime
+    sys.modules.setdefault("asc.lib", lib)
+    sys.modules.setdefault("asc.lib.runtime", lib_runtime)
     sys.modules.setdefault("asc2", asc2)

@@ -67,6 +67,37 @@ class GlobalAddress:
         return f"GlobalAddress(dtype={self.dtype}, handle=...)"
 
 
+class _BodyOnlyName:
+    """A name of asc1's on-chip API (python/asc/language/core/tensor.py, fwk/tpipe.py) that
+    kernel signatures use as an annotation (``z_gm: asc.GlobalTensor``, ``in_queue: asc.TQue``).
+    The annotation evaluates; constructing one raises, since kernel bodies are not executed
+    here: each registered kernel signature runs a native gfx950 kernel."""
+
+    def __init__(self, *args, **kwargs):
+        raise RuntimeError(f"asc.{type(self).__name__} can only appear inside an @asc.jit kernel body; bodies are "
+                           "not executed here, each registered kernel signature runs a native gfx950 kernel")
+
+
+class GlobalTensor(_BodyOnlyName):
+    """Global-memory tensor view of asc1 (python/asc/language/core/tensor.py)."""
+
+
+class LocalTensor(_BodyOnlyName):
+    """On-chip tensor of asc1 (python/asc/language/core/tensor.py)."""
+
+
+class TQue(_BodyOnlyName):
+    """Pipeline queue of asc1 (python/asc/language/fwk/tpipe.py)."""
+
+
+class TBuf(_BodyOnlyName):
+    """Scratch buffer of asc1 (python/asc/language/fwk/tpipe.py)."""
+
+
+class TPipe(_BodyOnlyName):
+    """Buffer manager of asc1 (python/asc/language/fwk/tpipe.py)."""
+
+
 class DataType:
     """Element type named like numpy/torch (``float16``, ``bfloat16``, ``int8`` ...)."""
 
@@ -155,7 +186,8 @@ def as_torch_dtype(dtype: Union[DataType, Any]):
 
 
 __all__ = [
-    "ConstExpr", "require_constexpr", "GlobalAddress", "DataType", "ceildiv", "as_torch_dtype", "void", "int1",
+    "ConstExpr", "require_constexpr", "GlobalAddress", "GlobalTensor", "LocalTensor", "TQue", "TBuf", "TPipe",
+    "DataType", "ceildiv", "as_torch_dtype", "void", "int1",
     "int8", "int16", "int32", "int64", "float16", "bfloat16", "float32", "float64", "uint8", "uint16", "uint32",
     "uint64", "bit", "bool_", "int_", "half", "float_", "double"
 ]

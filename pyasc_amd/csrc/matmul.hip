@@ -15,8 +15,10 @@
 // The epilogue applies the fixpipe relu and the RNE cast to fp16/bf16, or
 // stores fp32 as is.
 //
-// fp32 inputs (test_matmul_fixpipe.py's float32 case) use a plain LDS-tiled
-// FMA kernel.
+// fp32 inputs (test_matmul_fixpipe.py's float32 case; the asc1 kernels of
+// python/test/kernels/test_matmul.py, test_matmul_torch.py) run on
+// v_mfma_f32_16x16x4_f32 up to 2048x2048 outputs, and on a plain LDS-tiled FMA
+// kernel beyond that.
 #include "common.h"
 #include "gemm_common.h"
 #include "gemm_core.h"
@@ -200,7 +202,68 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
   }
 }
 
-// ---- fp32 inputs: LDS-tiled FMA kernel (64x64 tile, 256 threads, 4x4 per thread)
+// ---- fp32 inputs, small outputs: v_mfma_f32_16x16x4_f32.  A 256-thread workgroup
+// owns one 16x16 output block and splits K over its four waves: wave w takes the
+// 16-value k-groups w, w+4, ...; the four partial blocks meet in LDS and wave 0 sums
+// them in wave order, then runs the epilogue.  Operands come from global memory (L2)
+// straight into registers.  Lane l holds row l%16 of A and column l%16 of B; in
+// k-group g, MFMA step j uses k = 16g + 4*(l/16) + j in both operands, so the four
+// steps of a group cover its 16 values once (the order of k within a sum is free).
+// D layout: lane l holds rows 4*(l/16) + r (r = 0..3) of column l%16.
+// Out-of-range rows, columns and k read a clamped in-bounds address and use 0.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kF32MfmaMaxBlocks = 16384;  // 16x16 output blocks: up to 2048 x 2048 outputs
+
+template <int kOut>
+__global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float* __restrict__ a,
+                                                            const float* __restrict__ b, void* c, int M, int N,
+                                                            int K, int64_t lda, int64_t ldb, int64_t ldc,
+                                                            Epilogue epi) {
+  __shared__ f32x4 partial[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+  const int r = lane & 15, q = lane >> 4;
+  const bool a_ok = m0 + r < M, b_ok = n0 + r < N;
+  const float* arow = a + static_cast<int64_t>(a_ok ? m0 + r : 0) * lda;
+  const float* bcol = b + (b_ok ? n0 + r : 0);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int groups = (K + 15) / 16;
+#pragma unroll 4
+  for (int g = wave; g < groups; g += 4) {
+    const int kb = 16 * g + 4 * q;
+    float av[4], bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool k_ok = kb + j < K;
+      const int k = k_ok ? kb + j : 0;
+      av[j] = a_ok && k_ok ? arow[k] : 0.f;
+      bv[j] = b_ok && k_ok ? bcol[static_cast<int64_t>(k) * ldb] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc, 0, 0, 0);
+  }
+  partial[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  acc = partial[0][lane];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) acc += partial[w][lane];
+  const int n = n0 + r;
+  if (n >= N) return;
+  const float bias_n = epi.bias_at(n);
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int m = m0 + 4 * q + rr;
+    if (m >= M) continue;
+    const float v = epi(acc[rr], bias_n);
+    const int64_t off = static_cast<int64_t>(m) * ldc + n;
+    if constexpr (kOut == kOutF32) static_cast<float*>(c)[off] = v;
+    else if constexpr (kOut == kOutF16) static_cast<uint16_t*>(c)[off] = asc::f32_to_f16_rne(v);
+    else static_cast<uint16_t*>(c)[off] = asc::f32_to_bf16_rne(v);
+  }
+}
+
+// ---- fp32 inputs, large outputs: LDS-tiled FMA kernel (64x64 tile, 256 threads, 4x4 per thread)
 template <int kOut>
 __global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                        void* c, int M, int N, int K, int64_t lda, int64_t ldb,
@@ -276,12 +339,33 @@ int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const vo
               "asc_matmul: leading dimensions (%lld, %lld, %lld) smaller than the rows", (long long)lda,
               (long long)ldb, (long long)ldc);
   if (M == 0 || N == 0) return ASC_OK;
-  ASC_REQUIRE(a && b && c, ASC_ERR_INVALID_ARG, "asc_matmul: null buffer");
+  // with K == 0 no operand element is read (C receives the epilogue of 0)
+  ASC_REQUIRE(c && (K == 0 || (a && b)), ASC_ERR_INVALID_ARG, "asc_matmul: null buffer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (in_dtype == ASC_DT_FLOAT32) {
-    dim3 grid(static_cast<uint32_t>((N + 63) / 64), static_cast<uint32_t>((M + 63) / 64));
     const float* af = static_cast<const float*>(a);
     const float* bf = static_cast<const float*>(b);
+    const int64_t blocks16 = ((M + 15) / 16) * ((N + 15) / 16);
+    if (blocks16 <= kF32MfmaMaxBlocks) {
+      const dim3 grid16(static_cast<uint32_t>((N + 15) / 16), static_cast<uint32_t>((M + 15) / 16));
+      switch (out_dtype) {
+        case ASC_DT_FLOAT32:
+          hipLaunchKernelGGL(gemm_f32_mfma_kernel<kOutF32>, grid16, dim3(256), 0, s, af, bf, c, (int)M, (int)N,
+                             (int)K, lda, ldb, ldc, epi);
+          break;
+        case ASC_DT_FLOAT16:
+          hipLaunchKernelGGL(gemm_f32_mfma_kernel<kOutF16>, grid16, dim3(256), 0, s, af, bf, c, (int)M, (int)N,
+                             (int)K, lda, ldb, ldc, epi);
+          break;
+        case ASC_DT_BFLOAT16:
+          hipLaunchKernelGGL(gemm_f32_mfma_kernel<kOutBF16>, grid16, dim3(256), 0, s, af, bf, c, (int)M, (int)N,
+                             (int)K, lda, ldb, ldc, epi);
+          break;
+        default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
+      }
+      return asc::check_launch("asc_matmul");
+    }
+    dim3 grid(static_cast<uint32_t>((N + 63) / 64), static_cast<uint32_t>((M + 63) / 64));
     switch (out_dtype) {
       case ASC_DT_FLOAT32:
         hipLaunchKernelGGL(gemm_f32_kernel<kOutF32>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,

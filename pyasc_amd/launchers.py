@@ -11,7 +11,7 @@ from typing import List, Tuple
 import torch
 
 from . import kernels
-from .asc.core import as_torch_dtype
+from .asc.core import as_torch_dtype, ceildiv
 from .registry import KernelCall, register
 
 
@@ -501,3 +501,89 @@ def _broadcast_dup(call: KernelCall) -> None:
     for d in call.consts["shape"]:
         n *= int(d)
     kernels.fill(call.args["out_ptr"].reshape(-1), 777, n, call.stream)
+
+
+# --------------------------------------------------------------- asc1 kernels (python/test/kernels, tutorials)
+# asc1 kernels address the Ascend pipeline explicitly (GlobalTensor views, TQue queues,
+# data_copy); what they compute is registered here by signature, like the asc2 kernels.
+
+def _block_add(call: KernelCall, block_stride: int, block_cover: int) -> None:
+    """z[b*stride + j] = x[..] + y[..] for blocks b < grid and j < cover: the asc1 vadd
+    bodies, where block b views x, y, z from b*stride and adds ``cover`` elements.  The
+    union of the blocks is clipped at z's length (the NPU copy does not clip)."""
+    x, y, z = (call.args[k].reshape(-1) for k in ("x", "y", "z"))
+    n = z.numel()
+    grid = call.grid
+    if block_stride <= 0 or block_cover < 0:
+        raise ValueError(f"invalid block length {block_stride} / elements per block {block_cover}")
+    if block_cover >= block_stride:
+        covered = min(n, (grid - 1) * block_stride + block_cover)
+        if covered > 0:
+            tile = min(covered, 1 << 30)
+            kernels.vadd(x, y, z, covered, tile, ceildiv(covered, tile), 1, call.stream)
+        return
+    full = min(grid, n // block_stride)  # blocks whose whole stride lies inside z
+    if full > 0 and block_cover > 0:
+        kernels.tile_binary(x, y, z, "add", [full, block_stride], [full, block_cover], [0, 0], call.stream)
+    start = full * block_stride
+    if full < grid and start < n and block_cover > 0:
+        kernels.tile_binary(x, y, z, "add", [n], [block_cover], [start], call.stream)
+
+
+@register("vadd_kernel", ("x", "y", "z", "BLOCK_LENGTH", "BUFFER_NUM", "TILE_LENGTH", "TILE_NUM"),
+          "python/test/kernels/test_vadd.py:16-35")
+def _asc1_vadd(call: KernelCall) -> None:
+    # TILE_NUM tiles of TILE_LENGTH from each block's start (BUFFER_NUM only sizes the queues)
+    _block_add(call, int(call.consts["BLOCK_LENGTH"]), int(call.consts["TILE_NUM"]) * int(call.consts["TILE_LENGTH"]))
+
+
+@register("vadd_kernel", ("x", "y", "z", "block_length"), "python/tutorials/01_add/add.py:29-70")
+def _tutorial_add(call: KernelCall) -> None:
+    # TILE_NUM * BUFFER_NUM = 8 * 2 tiles of block_length // 16 elements (add.py:21-23, 40)
+    bl = int(call.args["block_length"])
+    _block_add(call, bl, 16 * (bl // 16))
+
+
+@register("vadd_kernel", ("x", "y", "z", "block_length", "tile_length"),
+          "python/tutorials/02_add_framework/add_framework.py:29-80")
+def _tutorial_add_framework(call: KernelCall) -> None:
+    # TILE_NUM * BUFFER_NUM = 8 * 2 tiles of tile_length elements (add_framework.py:21-23, 47-50)
+    _block_add(call, int(call.args["block_length"]), 16 * int(call.consts["tile_length"]))
+
+
+def _asc1_matmul(call: KernelCall, tiles_m: int, tiles_n: int, bias) -> None:
+    a, b, c = call.args["a"], call.args["b"], call.args["c"]
+    if a.dim() != 2 or b.dim() != 2 or c.dim() != 2:
+        raise ValueError("a, b and c must be 2-D")
+    if call.grid < tiles_m * tiles_n:
+        raise NotImplementedError(f"{call.grid} blocks for {tiles_m * tiles_n} output tiles: only launches that "
+                                  "cover every tile are provided")
+    kernels.matmul(a, b, c, bias=None if bias is None else bias.reshape(-1),
+                   leaky_alpha=_scalar(call.args["alpha"]), stream=call.stream)
+
+
+@register("matmul_kernel", ("a", "b", "c", "alpha", "tiling", "bias", "workspace"),
+          "python/test/kernels/test_matmul.py:17-79")
+def _asc1_matmul_bias(call: KernelCall) -> None:
+    """c = leaky_relu(a @ b + bias, alpha), fp32 accumulation.  Block b computes the
+    single_core_m x single_core_n tile of calc_offsets (test_matmul.py:67-79); a launch
+    must cover every tile, as the test's used_core_num does."""
+    t = call.args["tiling"]
+    M, N = call.args["a"].shape[0], call.args["b"].shape[1]
+    _asc1_matmul(call, ceildiv(M, int(t.single_core_m)), ceildiv(N, int(t.single_core_n)), call.args["bias"])
+
+
+@register("matmul_kernel", ("a", "b", "c", "alpha", "size_m", "size_k", "size_n", "size_base_m", "size_base_k",
+                            "size_base_n", "size_single_m", "size_single_k", "size_single_n", "used_core_num",
+                            "workspace"),
+          "python/test/kernels/test_matmul_torch.py:20-85")
+def _asc1_matmul_torch(call: KernelCall) -> None:
+    """c = leaky_relu(a @ b, alpha), fp32 accumulation (the same kernel without bias, tiling
+    given as ConstExprs)."""
+    k = call.consts
+    if (int(k["size_m"]), int(k["size_k"])) != tuple(call.args["a"].shape) or \
+            (int(k["size_k"]), int(k["size_n"])) != tuple(call.args["b"].shape):
+        raise ValueError(f"size_m/size_k/size_n ({k['size_m']}, {k['size_k']}, {k['size_n']}) do not match a "
+                         f"{tuple(call.args['a'].shape)} and b {tuple(call.args['b'].shape)}")
+    _asc1_matmul(call, ceildiv(int(k["size_m"]), int(k["size_single_m"])),
+                 ceildiv(int(k["size_n"]), int(k["size_single_n"])), None)

@@ -101,3 +101,44 @@ def test_config_8192_sampled_rows(device, dtype):
     ref = a[rows].float() @ b.float()
     torch.testing.assert_close(c[rows.to(device)].cpu().float(), ref.to(dtype).float(), atol=TOL, rtol=TOL)
     assert torch.isfinite(c).all()
+
+
+# fp32 inputs: the MFMA kernel up to 4096 output tiles of 32x32, the LDS FMA kernel beyond
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (17, 33, 5), (256, 256, 256), (100, 300, 1000), (31, 2, 17),
+                                   (2048, 2048, 48), (2100, 2100, 40), (64, 64, 0)])
+def test_f32_inputs_integer_valued_exact(device, M, N, K):
+    # entries in [-4, 4]: every partial sum is an integer below 2^24, exact in any order
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randint(-4, 5, (M, K), generator=g).float()
+    b = torch.randint(-4, 5, (K, N), generator=g).float()
+    c = torch.full((M, N), float("nan"), device=device)
+    kernels.matmul(a.to(device), b.to(device), c)
+    torch.cuda.synchronize()
+    assert torch.equal(c.cpu(), (a.double() @ b.double()).float())
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("act", ["none", "relu", "leaky"])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (77, 50, 33), (2100, 64, 2100)])
+def test_f32_inputs_epilogues_vs_fp64(device, out_dtype, act, M, N, K):
+    g = torch.Generator().manual_seed(7)
+    a = torch.randn(M, K, generator=g) * 3
+    b = torch.randn(K, N, generator=g) * 3
+    bias = torch.randn(N, generator=g) * 10
+    c = torch.empty(M, N, dtype=out_dtype, device=device)
+    kw = {"bias": bias.to(device)}
+    if act == "relu":
+        kw["relu"] = True
+    elif act == "leaky":
+        kw["leaky_alpha"] = 0.01
+    kernels.matmul(a.to(device), b.to(device), c, **kw)
+    torch.cuda.synchronize()
+    ref = a.double() @ b.double() + bias.double()
+    if act == "relu":
+        ref = ref.relu()
+    elif act == "leaky":
+        ref = torch.where(ref >= 0, ref, ref * 0.01)
+    # fp32 accumulation: error below K * 2^-24 * sum|a b| per element, then the output rounding
+    bound = K * 2.0 ** -24 * (a.double().abs() @ b.double().abs()) + ref.abs() * {
+        torch.float32: 0.0, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[out_dtype] + 1e-6
+    assert bool(((c.cpu().double() - ref).abs() <= bound).all())

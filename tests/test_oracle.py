@@ -655,3 +655,38 @@ def test_fill_matches_torch_full(dtype):
     ref = torch.full((3, 32), 777, dtype=td).reshape(-1)
     ref_np = ref.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else ref.numpy()
     np.testing.assert_array_equal(O.fill(96, 777, dtype), ref_np)
+
+
+def _asc1_body_walk(x, y, z, grid, block_length, tile_length, tile_num):
+    """Literal walk of python/test/kernels/test_vadd.py:19-35: per block, TILE_NUM tiles of
+    TILE_LENGTH from the block's start, with Python float32 scalars, clipped at len(z)."""
+    res = list(z)
+    for b in range(grid):
+        for i in range(tile_num):
+            for j in range(tile_length):
+                e = b * block_length + i * tile_length + j
+                if e < len(res):
+                    res[e] = np.float32(x[e]) + np.float32(y[e])
+    return np.array(res, dtype=np.float32)
+
+
+@pytest.mark.parametrize("size, grid, tile_num", [(8192, 16, 8), (8191, 16, 8), (100, 3, 4), (37, 5, 2)])
+def test_block_add_matches_asc1_body_walk(size, grid, tile_num):
+    rng = np.random.default_rng(size)
+    x, y = rng.random(size, dtype=np.float32), rng.random(size, dtype=np.float32)
+    z = np.full(size, -3.0, dtype=np.float32)
+    block_length = (size + grid - 1) // grid          # the test's launch helper (test_vadd.py:72-80)
+    tile_length = (block_length + tile_num - 1) // tile_num
+    np.testing.assert_array_equal(O.block_add(x, y, z, grid, block_length, tile_num * tile_length),
+                                  _asc1_body_walk(x, y, z, grid, block_length, tile_length, tile_num))
+
+
+def test_block_add_reference_golden_and_gaps():
+    # test_vadd.py:85-92: the launch covers everything, golden x + y
+    rng = np.random.default_rng(seed=2025)
+    x, y = rng.random(8192, dtype=np.float32), rng.random(8192, dtype=np.float32)
+    np.testing.assert_array_equal(O.block_add(x, y, np.zeros(8192, np.float32), 16, 512, 8 * 64), x + y)
+    # two blocks of stride 4 adding 3 elements each over 10: elements 3, 7, 8, 9 untouched
+    x, y = np.arange(10, dtype=np.float32), np.full(10, 100, dtype=np.float32)
+    got = O.block_add(x, y, np.zeros(10, np.float32), 2, 4, 3)
+    np.testing.assert_array_equal(got, [100, 101, 102, 0, 104, 105, 106, 0, 0, 0])

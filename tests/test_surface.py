@@ -133,7 +133,11 @@ def test_kernel_called_without_grid():
 def test_registry_contents():
     names = {(n, p[-1]) for n, p in registry.entries()}
     assert ("softmax_kernel", "tile_size") in names and ("softmax_kernel", "block_size") in names
-    assert sum(1 for n, _ in names if n == "matmul_kernel") == 4
+    # four asc2 matmul tests and two asc1 ones (python/test/kernels/test_matmul.py, test_matmul_torch.py)
+    assert sum(1 for n, _ in registry.entries() if n == "matmul_kernel") == 6
+    vadds = {p for n, p in registry.entries() if n == "vadd_kernel"}
+    assert ("x", "y", "z", "BLOCK_LENGTH", "BUFFER_NUM", "TILE_LENGTH", "TILE_NUM") in vadds  # asc1 test_vadd.py
+    assert ("x", "y", "z", "block_length") in vadds and ("x", "y", "z", "block_length", "tile_length") in vadds
     assert ("flash_attention_fwd_kernel", "block_n") in names
     assert ("matmul_dequant_kernel", "c_shape") in names
     assert ("leaky_relu_kernel", "tile_per_block") in names and ("vmuladd_kernel", "buffer_factor") in names
@@ -290,3 +294,24 @@ def test_string_annotations_with_local_import(recorded):
     k[2](x, x, x, 64, 8, 4, always_compile=True)
     assert [r[3] for r in recorded] == [{"tile_size": 8, "tile_per_block": 4}] * 2
     assert list(recorded[0][2]) == ["x_ptr", "y_ptr", "out_ptr", "size"]
+
+
+def test_asc1_signatures_evaluate_and_runtime_checks():
+    # asc1 helper signatures annotate with asc.TQue / asc.GlobalTensor
+    # (python/test/kernels/test_vadd.py:38-64); the names exist, constructing them raises
+    import asc.lib.runtime as rt
+
+    @asc.jit
+    def copy_out(i: int, z_gm: asc.GlobalTensor, out_queue_z: asc.TQue, TILE_LENGTH: asc.ConstExpr[int]):
+        pass
+
+    assert copy_out.fn_name == "copy_out"
+    with pytest.raises(RuntimeError, match="only appear inside"):
+        asc.TQue()
+    assert rt.default_device() == 0
+    rt.check_device_handle(3)
+    for bad in (-1, "0", 1.0, True):
+        with pytest.raises(RuntimeError, match="int >= 0"):
+            rt.check_device_handle(bad)
+    with pytest.raises(ValueError, match="priority 0"):
+        rt.create_stream(priority=-1)
