@@ -25,7 +25,7 @@ __version__ = "0.1.0"
 
 def install_aliases() -> None:
     """Makes ``import asc``, ``import asc2``, ``import asc.runtime.config`` and
-    ``import asc.lib.runtime`` resolve to this package, so code written against the
+    ``import asc.lib.runtime`` / ``asc.lib.host`` resolve to this package, so code written against the
     reference imports unchanged."""
     from .asc import runtime
     from .asc.runtime import config, jit, launcher
@@ -35,7 +35,8 @@ def install_aliases() -> None:
     sys.modules.setdefault("asc.runtime.jit", jit)
     sys.modules.setdefault("asc.runtime.launcher", launcher)
     from .asc import lib
-    from .asc.lib import runtime as lib_runtime
+    from .asc.lib import host as lib_host, runtime as lib_runtime
     sys.modules.setdefault("asc.lib", lib)
     sys.modules.setdefault("asc.lib.runtime", lib_runtime)
+    sys.modules.setdefault("asc.lib.host", lib_host)
     sys.modules.setdefault("asc2", asc2)

@@ -272,7 +272,8 @@ class JITFunction:
 
     def _run(self, *args, **kwargs) -> None:
         resolved, runtime_args, constexprs = self.resolve(*args, **kwargs)
-        Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs)
+        options = {**self.default_options, **{k: v for k, v in kwargs.items() if k in COMPILE_OPTIONS}}
+        Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs, options)
 
 
 def jit(fn: Callable = None, **options):

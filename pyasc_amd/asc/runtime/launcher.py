@@ -98,7 +98,7 @@ class Launcher:
         return device_args, copy_back
 
     def run(self, entry: KernelEntry, function_name: str, runtime_args: Dict[str, Any],
-            constexprs: Dict[str, Any]) -> None:
+            constexprs: Dict[str, Any], options: Optional[Dict[str, Any]] = None) -> None:
         if os.environ.get("DRY_RUN"):
             return
         if self.options.core_num <= 0:
@@ -106,7 +106,8 @@ class Launcher:
         require_device()
         device_args, copy_back = self.prepare(runtime_args)
         stream = stream_handle(self.options.stream)
-        call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream)
+        call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream,
+                          {"options": dict(options or {})})
         entry.launch(call)
         if copy_back:
             from ... import _native

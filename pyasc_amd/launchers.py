@@ -265,11 +265,17 @@ def _matmul_chained(call: KernelCall) -> None:
 def _matmul_leakyrelu(call: KernelCall) -> None:
     """c = leaky_relu(a @ b + bias, alpha) in fp32 (the tutorial's Matmul + set_bias + asc.leaky_relu).
     Shapes come from the tensors: a [M, K], b [K, N], c [M, N], bias N elements.  The
-    tiling argument (the CANN tiling library's per-core split) and the workspace are
-    accepted and not used: the MI355X kernel picks its own tiles."""
+    MI355X kernel picks its own tiles; a tiling that carries a per-core split
+    (single_core_m / single_core_n, as asc.lib.host fills it) must describe a launch that
+    covers the whole output.  The workspace is not used."""
     a, b, c, bias = call.args["a"], call.args["b"], call.args["c"], call.args["bias"]
     if a.dim() != 2 or b.dim() != 2 or c.dim() != 2:
         raise ValueError("a, b and c must be 2-D")
+    t = call.args["tiling"]
+    if hasattr(t, "single_core_m") and hasattr(t, "single_core_n"):
+        # a tiling with a split (asc.lib.host): the launch must cover every tile
+        _asc1_matmul(call, *_tiles_of(call), bias, call.args["alpha"], getattr(t, "used_core_num", None))
+        return
     kernels.matmul(a, b, c, bias=bias.reshape(-1), leaky_alpha=_scalar(call.args["alpha"]), stream=call.stream)
 
 
@@ -551,15 +557,36 @@ def _tutorial_add_framework(call: KernelCall) -> None:
     _block_add(call, int(call.args["block_length"]), 16 * int(call.consts["tile_length"]))
 
 
-def _asc1_matmul(call: KernelCall, tiles_m: int, tiles_n: int, bias) -> None:
+def _matmul_instances(call: KernelCall) -> int:
+    """Kernel instances a launch of ``grid`` blocks runs for an asc1 Matmul kernel: a mixed
+    cube + vector kernel runs as MIX_AIC_1_2, one cube core and two vector cores per block,
+    and get_block_idx counts the vector cores; with matmul_cube_only it runs as AIC_ONLY,
+    one instance per block (python/asc/runtime/compiler.py:291-299)."""
+    return call.grid * (1 if call.extra.get("options", {}).get("matmul_cube_only") else 2)
+
+
+def _asc1_matmul(call: KernelCall, tiles_m: int, tiles_n: int, bias, alpha=None, used_core_num=None) -> None:
+    """c = act(a @ b + bias) over the whole output, for asc1 kernels whose instance i computes
+    one single_core_m x single_core_n tile when i < used_core_num: the launch must cover
+    every tile (min(instances, used_core_num) >= the tile count), as the reference's
+    launches do."""
     a, b, c = call.args["a"], call.args["b"], call.args["c"]
     if a.dim() != 2 or b.dim() != 2 or c.dim() != 2:
         raise ValueError("a, b and c must be 2-D")
-    if call.grid < tiles_m * tiles_n:
-        raise NotImplementedError(f"{call.grid} blocks for {tiles_m * tiles_n} output tiles: only launches that "
-                                  "cover every tile are provided")
+    blocks = _matmul_instances(call)
+    if used_core_num is not None:
+        blocks = min(blocks, int(used_core_num))
+    if blocks < tiles_m * tiles_n:
+        raise NotImplementedError(f"{blocks} computing blocks for {tiles_m * tiles_n} output tiles: only launches "
+                                  "that cover every tile are provided")
     kernels.matmul(a, b, c, bias=None if bias is None else bias.reshape(-1),
-                   leaky_alpha=_scalar(call.args["alpha"]), stream=call.stream)
+                   leaky_alpha=None if alpha is None else _scalar(alpha), stream=call.stream)
+
+
+def _tiles_of(call: KernelCall):
+    t = call.args["tiling"]
+    M, N = call.args["a"].shape[0], call.args["b"].shape[1]
+    return ceildiv(M, int(t.single_core_m)), ceildiv(N, int(t.single_core_n))
 
 
 @register("matmul_kernel", ("a", "b", "c", "alpha", "tiling", "bias", "workspace"),
@@ -568,9 +595,7 @@ def _asc1_matmul_bias(call: KernelCall) -> None:
     """c = leaky_relu(a @ b + bias, alpha), fp32 accumulation.  Block b computes the
     single_core_m x single_core_n tile of calc_offsets (test_matmul.py:67-79); a launch
     must cover every tile, as the test's used_core_num does."""
-    t = call.args["tiling"]
-    M, N = call.args["a"].shape[0], call.args["b"].shape[1]
-    _asc1_matmul(call, ceildiv(M, int(t.single_core_m)), ceildiv(N, int(t.single_core_n)), call.args["bias"])
+    _asc1_matmul(call, *_tiles_of(call), call.args["bias"], call.args["alpha"])
 
 
 @register("matmul_kernel", ("a", "b", "c", "alpha", "size_m", "size_k", "size_n", "size_base_m", "size_base_k",
@@ -586,4 +611,22 @@ def _asc1_matmul_torch(call: KernelCall) -> None:
         raise ValueError(f"size_m/size_k/size_n ({k['size_m']}, {k['size_k']}, {k['size_n']}) do not match a "
                          f"{tuple(call.args['a'].shape)} and b {tuple(call.args['b'].shape)}")
     _asc1_matmul(call, ceildiv(int(k["size_m"]), int(k["size_single_m"])),
-                 ceildiv(int(k["size_n"]), int(k["size_single_n"])), None)
+                 ceildiv(int(k["size_n"]), int(k["size_single_n"])), None, call.args["alpha"],
+                 int(k["used_core_num"]))
+
+
+@register("matmul_kernel", ("a", "b", "c", "tiling", "workspace"), "python/tutorials/03_matmul_mix/matmul_mix.py:31-77")
+def _tutorial_matmul_mix(call: KernelCall) -> None:
+    """c = a @ b, fp32 accumulation and output (Matmul.iterate_all without bias); blocks
+    below tiling.used_core_num compute one tile each (matmul_mix.py:47-52)."""
+    _asc1_matmul(call, *_tiles_of(call), None, None, call.args["tiling"].used_core_num)
+
+
+@register("matmul_kernel", ("a", "b", "c", "bias", "tiling", "workspace"),
+          "python/tutorials/04_matmul_cube_only/matmul_cube_only.py:32-85")
+def _tutorial_matmul_cube_only(call: KernelCall) -> None:
+    """c = a @ b (+ bias when tiling.is_bias), fp32 accumulation and output
+    (matmul_cube_only.py:53-60)."""
+    t = call.args["tiling"]
+    _asc1_matmul(call, *_tiles_of(call), call.args["bias"] if int(getattr(t, "is_bias", 0)) else None, None,
+                 t.used_core_num)

@@ -150,10 +150,13 @@ def test_asc1_matmul_reference_case(device, m, k, n):
 
 
 def test_asc1_matmul_partial_launch_is_rejected(device):
+    # four 64x64 tiles; a mixed kernel runs two instances per block, so one block misses two
     a = np.ones((128, 64), np.float32)
     b = np.ones((64, 128), np.float32)
     with pytest.raises(NotImplementedError, match="cover every tile"):
-        matmul_launch(a, b, np.zeros((1, 128), np.float32), 0.1, cores=3)
+        matmul_launch(a, b, np.zeros((1, 128), np.float32), 0.1, cores=1)
+    c = matmul_launch(a, b, np.zeros((1, 128), np.float32), 0.1, cores=2)  # 4 instances: complete
+    np.testing.assert_array_equal(c, np.full((128, 128), 64, np.float32))
 
 
 @asc.jit
@@ -195,3 +198,118 @@ def test_runtime_streams(device):
     assert rt.current_platform() == "gfx950" and rt.device_count() >= 1 and rt.current_device() == 0
     rt.destroy_stream(s)
     rt.synchronize_device()
+
+
+@asc.jit(always_compile=True)
+def matmul_mix_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress, tiling: asc.adv.TCubeTiling,
+                      workspace: asc.GlobalAddress):
+    raise AssertionError("kernel bodies are not executed")
+
+
+matmul_mix_kernel.fn_name = "matmul_kernel"  # python/tutorials/03_matmul_mix/matmul_mix.py:32
+
+
+@asc.jit(matmul_cube_only=True, always_compile=True)
+def matmul_cube_only_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress,
+                            bias: asc.GlobalAddress, tiling: asc.adv.TCubeTiling, workspace: asc.GlobalAddress):
+    raise AssertionError("kernel bodies are not executed")
+
+
+matmul_cube_only_kernel.fn_name = "matmul_kernel"  # python/tutorials/04_matmul_cube_only/matmul_cube_only.py:33
+
+
+def _generate_tiling(m, n, k, cores, bias):
+    # generate_tiling of the tutorials (matmul_mix.py:90-106, matmul_cube_only.py:97-115)
+    import asc.lib.host as host
+    t = host.MultiCoreMatmulTiling(host.get_ascendc_platform())
+    t.set_a_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT16, False)
+    t.set_b_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT16, False)
+    t.set_c_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT)
+    t.set_bias_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT)
+    t.set_dim(cores)
+    t.set_org_shape(m, n, k)
+    t.set_shape(m, n, k)
+    t.enable_bias(bias)
+    t.set_buffer_space(-1, -1, -1)
+    tiling = asc.adv.TCubeTiling()
+    t.get_tiling(tiling)
+    return tiling
+
+
+def test_tutorial_matmul_mix(device):
+    # matmul_mix.py:109-121: USE_CORE_NUM 48, launched on USE_CORE_NUM // 2 blocks
+    m, k, n = 512, 512, 1024
+    a = torch.randint(-5, 5, (m, k)).to(torch.float16)
+    b = torch.randint(-5, 5, (k, n)).to(torch.float16)
+    matmul = torch.matmul(a.to(torch.float32), b.to(torch.float32)).to(torch.float32)
+    tiling = _generate_tiling(m, n, k, 48, False)
+    c = torch.zeros((m, n), dtype=torch.float32)
+    workspace = torch.zeros(16 * 1024 * 1024, dtype=torch.uint8)
+    matmul_mix_kernel[48 // 2, rt.current_stream()](a, b, c, tiling, workspace)
+    assert torch.allclose(c, matmul, rtol=1e-3, atol=1e-3)
+    assert torch.equal(c, matmul)  # integer-valued products: exact
+
+
+@pytest.mark.parametrize("enable_bias", [False, True])
+def test_tutorial_matmul_cube_only(device, enable_bias):
+    # matmul_cube_only.py:118-135: USE_CORE_NUM 24, launched on tiling.used_core_num blocks
+    m, k, n = 128, 64, 30720
+    a = torch.randint(-5, 5, (m, k)).to(torch.float16)
+    b = torch.randint(-5, 5, (k, n)).to(torch.float16)
+    bias = torch.randint(-5, 5, (1, n)).to(torch.float32)
+    matmul = torch.matmul(a.to(torch.float32), b.to(torch.float32)).to(torch.float32)
+    if enable_bias:
+        matmul = matmul + bias
+    tiling = _generate_tiling(m, n, k, 24, enable_bias)
+    c = torch.zeros((m, n), dtype=torch.float32)
+    workspace = torch.zeros(16 * 1024 * 1024, dtype=torch.uint8)
+    matmul_cube_only_kernel[tiling.used_core_num, rt.current_stream()](a, b, c, bias, tiling, workspace)
+    assert torch.allclose(c, matmul, rtol=1e-3, atol=1e-3)
+    assert torch.equal(c, matmul)
+
+
+def test_tutorial_matmul_too_few_blocks(device):
+    # a mixed kernel runs two instances per block: (used_core_num - 1) // 2 blocks miss a tile
+    tiling = _generate_tiling(512, 1024, 64, 48, False)
+    assert tiling.used_core_num >= 4
+    a, b = torch.ones(512, 64, dtype=torch.float16), torch.ones(64, 1024, dtype=torch.float16)
+    with pytest.raises(NotImplementedError, match="cover every tile"):
+        matmul_mix_kernel[(tiling.used_core_num - 1) // 2](a, b, torch.zeros(512, 1024), tiling, torch.zeros(16))
+
+
+@asc.jit
+def matmul_leakyrelu_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress,
+                            bias: asc.GlobalAddress, alpha: float, tiling: asc.adv.TCubeTiling,
+                            workspace: asc.GlobalAddress):
+    raise AssertionError("kernel bodies are not executed")
+
+
+def test_tutorial_matmul_leakyrelu_host_tiling(device):
+    # matmul_leakyrelu.py:86-131 as written: host tiling with set_dim(2), FIRSTM traverse,
+    # fix split 256x128, launched on used_core_num // 2 blocks
+    import asc.lib.host as host
+    m, k, n = 1024, 256, 640
+    a = torch.randint(-5, 5, (m, k)).to(torch.float16)
+    b = torch.randint(-5, 5, (k, n)).to(torch.float16)
+    bias = torch.randint(-5, 5, (1, n)).to(torch.float32)
+    alpha = 0.001
+    matmul = (torch.matmul(a.to(torch.float32), b.to(torch.float32)).to(torch.float32) + bias).to(torch.float32)
+    mt = host.MultiCoreMatmulTiling(host.get_ascendc_platform())
+    mt.set_a_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT16, False)
+    mt.set_b_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT16, False)
+    mt.set_c_type(host.TPosition.VECCALC, host.CubeFormat.ND, host.DataType.DT_FLOAT)
+    mt.set_bias_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT)
+    mt.set_dim(2)
+    mt.set_org_shape(m, n, k)
+    mt.set_shape(m, n, k)
+    mt.enable_bias(True)
+    mt.set_traverse(host.MatrixTraverse.FIRSTM)
+    mt.set_fix_split(256, 128, -1)
+    mt.set_buffer_space(-1, -1, -1)
+    tiling = asc.adv.TCubeTiling()
+    mt.get_tiling(tiling)
+    assert (tiling.base_m, tiling.base_n) == (256, 128) and tiling.used_core_num == 2
+    c = torch.zeros((m, n), dtype=torch.float32)
+    workspace = torch.zeros(16 * 1024 * 1024, dtype=torch.uint8)
+    matmul_leakyrelu_kernel[tiling.used_core_num // 2, rt.current_stream()](a, b, c, bias, alpha, tiling, workspace)
+    assert torch.allclose(c, torch.where(matmul >= 0, matmul, matmul * alpha), rtol=1e-3, atol=1e-3)

@@ -26,8 +26,8 @@ def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc
 def recorded(monkeypatch):
     calls = []
 
-    def fake_run(self, entry, function_name, runtime_args, constexprs):
-        calls.append((entry, function_name, runtime_args, constexprs, self.options))
+    def fake_run(self, entry, function_name, runtime_args, constexprs, options=None):
+        calls.append((entry, function_name, runtime_args, constexprs, self.options, options))
 
     monkeypatch.setattr(launcher_mod.Launcher, "run", fake_run)
     return calls
@@ -36,7 +36,7 @@ def recorded(monkeypatch):
 def test_dispatch_by_signature(recorded):
     x = np.zeros(8192, np.float32)
     vadd_kernel[16](x, x, x, 8192, 128, 4)
-    entry, name, rt, ce, opts = recorded[0]
+    entry, name, rt, ce, opts, _ = recorded[0]
     assert name == "vadd_kernel" and entry.params[-1] == "tile_per_block"
     assert entry.reference.startswith("python/test/asc2/kernels/test_vadd.py")
     assert list(rt) == ["x_ptr", "y_ptr", "out_ptr", "size"] and ce == {"tile_size": 128, "tile_per_block": 4}
@@ -133,8 +133,9 @@ def test_kernel_called_without_grid():
 def test_registry_contents():
     names = {(n, p[-1]) for n, p in registry.entries()}
     assert ("softmax_kernel", "tile_size") in names and ("softmax_kernel", "block_size") in names
-    # four asc2 matmul tests and two asc1 ones (python/test/kernels/test_matmul.py, test_matmul_torch.py)
-    assert sum(1 for n, _ in registry.entries() if n == "matmul_kernel") == 6
+    # four asc2 matmul tests, two asc1 ones (python/test/kernels/test_matmul.py, test_matmul_torch.py),
+    # tutorials 03 and 04
+    assert sum(1 for n, _ in registry.entries() if n == "matmul_kernel") == 8
     vadds = {p for n, p in registry.entries() if n == "vadd_kernel"}
     assert ("x", "y", "z", "BLOCK_LENGTH", "BUFFER_NUM", "TILE_LENGTH", "TILE_NUM") in vadds  # asc1 test_vadd.py
     assert ("x", "y", "z", "block_length") in vadds and ("x", "y", "z", "block_length", "tile_length") in vadds
@@ -162,7 +163,7 @@ def test_scalar_and_bare_constexpr_arguments(recorded):
     x = torch.zeros(256, dtype=torch.bfloat16)
     alpha = torch.tensor(0.1, dtype=torch.bfloat16)
     leaky_relu_kernel[16](x, alpha, x, 256, 128, 1)
-    entry, name, rt, ce, _ = recorded[0]
+    entry, name, rt, ce, _, _ = recorded[0]
     assert entry.params[1] == "alpha" and rt["alpha"] is alpha and ce == {"tile_size": 128, "tile_per_block": 1}
     assert launcher_mod.Launcher.scalar_value(rt["alpha"]) == float(alpha.item())
     gelu_kernel[16](torch.zeros(2, 8), torch.zeros(2, 8), 2, 8, 8, True)
@@ -315,3 +316,36 @@ def test_asc1_signatures_evaluate_and_runtime_checks():
             rt.check_device_handle(bad)
     with pytest.raises(ValueError, match="priority 0"):
         rt.create_stream(priority=-1)
+
+
+@pytest.mark.parametrize("m, n, k, dim", [(512, 1024, 512, 48), (128, 30720, 64, 24), (1, 1, 1, 1), (7, 5, 3, 2),
+                                          (4096, 4096, 64, 512), (300, 17, 9, 7)])
+def test_host_tiling_covers_the_output(m, n, k, dim):
+    # the split is build-defined; what a launch needs is that used_core_num instances of
+    # single_core_m x single_core_n tiles cover m x n, with at most dim instances
+    import asc.lib.host as host
+    t = host.MultiCoreMatmulTiling(host.get_ascendc_platform())
+    assert t.set_a_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT16, False) == 0
+    assert t.set_c_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT) == 0
+    assert t.set_dim(dim) == 0 and t.set_org_shape(m, n, k) == 0 and t.set_shape(m, n, k) == 0
+    assert t.enable_bias(True) == 0 and t.set_buffer_space(-1, -1, -1) == 0
+    tiling = asc.adv.TCubeTiling()
+    assert t.get_tiling(tiling) == 0
+    tiles = -(-m // tiling.single_core_m) * -(-n // tiling.single_core_n)
+    assert tiles == tiling.used_core_num <= dim
+    assert (tiling.m, tiling.n, tiling.k_a, tiling.k_b, tiling.is_bias) == (m, n, k, k, 1)
+    assert tiling.single_core_m % 16 == 0 and tiling.single_core_n % 16 == 0
+    assert host.DataType.DT_BFLOAT16 is host.DataType.DT_BF16
+
+
+def test_compile_options_reach_the_launch(recorded):
+    # matmul_cube_only decides how many instances an asc1 Matmul launch runs
+    # (python/asc/runtime/compiler.py:291-299); it travels with the call
+    @asc.jit(matmul_cube_only=True)
+    def matmul_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress, bias: asc.GlobalAddress,
+                      tiling: asc.adv.TCubeTiling, workspace: asc.GlobalAddress):
+        pass
+
+    a = np.zeros((4, 4), np.float16)
+    matmul_kernel[3](a, a, np.zeros((4, 4), np.float32), np.zeros(4, np.float32), asc.adv.TCubeTiling(), a)
+    assert recorded[-1][-1]["matmul_cube_only"] is True
