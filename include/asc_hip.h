@@ -284,6 +284,23 @@ int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k,
 /* out[i] = op(x[i]), fp32 (libm-accurate; rsqrt is 1 / sqrt, relu maps negative to +0). */
 int32_t asc_unary_f32(int32_t op, const float* x, float* out, int64_t n,
                       asc_stream_t stream);
+/* The same on float32 / float16 / bfloat16 elements: 16-bit elements widen to fp32,
+ * take the fp32 op and round once (RNE).  asc2 unary ops on f16 tiles
+ * (python/asc/language/tile/unary_ops.py); asc.sqrt of
+ * python/test/generalization/basic/test_vsqrt.py. */
+int32_t asc_unary(int32_t op, int32_t dtype, const void* x, void* out, int64_t n,
+                  asc_stream_t stream);
+/* dst[i] = src[i] * scalar + dst[i] (asc.axpy, python/asc/language/basic/
+ * vec_ternary_scalar.py; python/test/generalization/basic/test_axpy.py):
+ * float32 / float16 / bfloat16, the scalar rounded to the element type, fp32 math,
+ * one rounding of the result. */
+int32_t asc_axpy(int32_t dtype, const void* src, void* dst, double scalar, int64_t n,
+                 asc_stream_t stream);
+/* z[b, c, r] = x[b, r, c] for row-major [batch, rows, cols] of 2- or 4-byte elements
+ * (asc.transpose of 16x16 tiles, python/test/generalization/basic/test_transpose.py).
+ * x and z must not overlap. */
+int32_t asc_transpose_batched(int32_t elem_bytes, const void* x, void* z, int64_t batch,
+                              int64_t rows, int64_t cols, asc_stream_t stream);
 
 #define ASC_BIN_ADD 0
 #define ASC_BIN_SUB 1

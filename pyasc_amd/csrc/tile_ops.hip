@@ -7,6 +7,7 @@
 //   rows    python/test/asc2/operations/test_shape_ops.py:47-55    broadcast_to / reshape data movement
 //   atomic  python/test/asc2/operations/test_atomic_ops.py:33-40   z[j] = op(z[j], x[b, j] + c), atomically
 //   fill    python/test/asc2/operations/test_shape_ops.py:64-78    z = full([1], c).broadcast_to(shape)
+//   axpy, transpose: asc1 vector intrinsics of python/test/generalization/basic/
 //
 // Semantics follow the op definitions (python/asc/language/tile/binary_ops.py,
 // unary_ops.py; dtype inference utils.py:73-94): a scalar operand takes the
@@ -86,11 +87,14 @@ __device__ __forceinline__ float unary_f32(int op, float x) {
   }
 }
 
-__global__ void __launch_bounds__(kThreads) unary_f32_kernel(int op, const float* __restrict__ x,
-                                                             float* __restrict__ out, int64_t n) {
+// fp32 elements directly; 16-bit float elements widen to fp32, take the fp32 op and
+// round once (RNE) to the element type.
+template <class E>
+__global__ void __launch_bounds__(kThreads) unary_kernel(int op, const typename E::T* __restrict__ x,
+                                                         typename E::T* __restrict__ out, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * kThreads)
-    out[i] = unary_f32(op, x[i]);
+    out[i] = E::out(unary_f32(op, E::in(x[i])));
 }
 
 // ---- binary: op codes of ASC_BIN_* in asc_hip.h
@@ -305,6 +309,35 @@ __global__ void __launch_bounds__(kThreads) atomic_tiles_kernel(int op, const ty
     atomic_combine<E>(op, z + (k - (k / tile_len) * tile_len), binary_op<E>(0, x[k], c));
 }
 
+// ---- axpy (python/asc/language/basic/vec_ternary_scalar.py, asc.axpy; the kernel of
+// python/test/generalization/basic/test_axpy.py): dst[i] = src[i] * s + dst[i], with s
+// in the element type (Axpy's scalar has the source type), computed in fp32 and
+// rounded once to the element type (-ffp-contract=off: product and sum each rounded
+// in fp32).
+template <class E>
+__global__ void __launch_bounds__(kThreads) axpy_kernel(const typename E::T* __restrict__ src,
+                                                        typename E::T* __restrict__ dst, float s_f, int64_t n) {
+  const float s = E::in(element_of<E>(s_f, 0));
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    dst[i] = E::out(E::in(src[i]) * s + E::in(dst[i]));
+}
+
+// ---- batched transpose: z[b, c, r] = x[b, r, c] for [batch, rows, cols] row-major
+// (asc.transpose of a 16x16 tile of 2-byte elements, python/test/generalization/basic/
+// test_transpose.py, is batch = tiles, rows = cols = 16).
+template <class T>
+__global__ void __launch_bounds__(kThreads) transpose_kernel(const T* __restrict__ x, T* __restrict__ z,
+                                                             int64_t rows, int64_t cols, int64_t n) {
+  const int64_t rc = rows * cols;
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < n;
+       k += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t b = k / rc, rem = k - b * rc;
+    const int64_t r = rem / cols, c = rem - r * cols;
+    z[b * rc + c * rows + r] = x[k];
+  }
+}
+
 // ---- fill: every element of z takes the scalar c converted to the element type
 template <class E>
 __global__ void __launch_bounds__(kThreads) fill_kernel(typename E::T* __restrict__ z, int64_t n, float c_f,
@@ -342,14 +375,84 @@ int32_t launch_where(int cmp, int mode, const void* x, const void* y, void* out,
 
 }  // namespace
 
-extern "C" int32_t asc_unary_f32(int32_t op, const float* x, float* out, int64_t n, asc_stream_t stream) {
-  ASC_REQUIRE(op >= 0 && op <= 17, ASC_ERR_INVALID_ARG, "asc_unary_f32: unknown op code %d", op);
-  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_unary_f32: negative length");
+extern "C" int32_t asc_unary(int32_t op, int32_t dtype, const void* x, void* out, int64_t n,
+                             asc_stream_t stream) {
+  ASC_REQUIRE(op >= 0 && op <= 17, ASC_ERR_INVALID_ARG, "asc_unary: unknown op code %d", op);
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_unary: negative length");
   if (n == 0) return ASC_OK;
-  ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_unary_f32: null buffer");
-  hipLaunchKernelGGL(unary_f32_kernel, dim3(grid_for(n)), dim3(kThreads), 0, static_cast<hipStream_t>(stream), op,
-                     x, out, n);
-  return asc::check_launch("asc_unary_f32");
+  ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_unary: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n));
+  switch (dtype) {
+    case ASC_DT_FLOAT32:
+      hipLaunchKernelGGL(unary_kernel<F32>, grid, dim3(kThreads), 0, s, op, static_cast<const float*>(x),
+                         static_cast<float*>(out), n);
+      break;
+    case ASC_DT_FLOAT16:
+      hipLaunchKernelGGL(unary_kernel<F16>, grid, dim3(kThreads), 0, s, op, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(out), n);
+      break;
+    case ASC_DT_BFLOAT16:
+      hipLaunchKernelGGL(unary_kernel<BF16>, grid, dim3(kThreads), 0, s, op, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(out), n);
+      break;
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_unary: unsupported dtype code %d", dtype);
+  }
+  return asc::check_launch("asc_unary");
+}
+
+extern "C" int32_t asc_unary_f32(int32_t op, const float* x, float* out, int64_t n, asc_stream_t stream) {
+  return asc_unary(op, ASC_DT_FLOAT32, x, out, n, stream);
+}
+
+extern "C" int32_t asc_axpy(int32_t dtype, const void* src, void* dst, double scalar, int64_t n,
+                            asc_stream_t stream) {
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_axpy: negative length");
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(src && dst, ASC_ERR_INVALID_ARG, "asc_axpy: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n));
+  switch (dtype) {
+    case ASC_DT_FLOAT32:
+      hipLaunchKernelGGL(axpy_kernel<F32>, grid, dim3(kThreads), 0, s, static_cast<const float*>(src),
+                         static_cast<float*>(dst), static_cast<float>(scalar), n);
+      break;
+    case ASC_DT_FLOAT16:
+      hipLaunchKernelGGL(axpy_kernel<F16>, grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(src),
+                         static_cast<uint16_t*>(dst), static_cast<float>(scalar), n);
+      break;
+    case ASC_DT_BFLOAT16:
+      hipLaunchKernelGGL(axpy_kernel<BF16>, grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(src),
+                         static_cast<uint16_t*>(dst), static_cast<float>(scalar), n);
+      break;
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_axpy: unsupported dtype code %d", dtype);
+  }
+  return asc::check_launch("asc_axpy");
+}
+
+extern "C" int32_t asc_transpose_batched(int32_t elem_bytes, const void* x, void* z, int64_t batch, int64_t rows,
+                                         int64_t cols, asc_stream_t stream) {
+  ASC_REQUIRE(batch >= 0 && rows >= 0 && cols >= 0, ASC_ERR_INVALID_ARG, "asc_transpose_batched: negative shape");
+  ASC_REQUIRE(rows == 0 || cols == 0 || batch <= INT64_MAX / rows / cols, ASC_ERR_INVALID_ARG,
+              "asc_transpose_batched: size overflows");
+  const int64_t n = batch * rows * cols;
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(x && z && x != z, ASC_ERR_INVALID_ARG, "asc_transpose_batched: null or aliased buffers");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n));
+  switch (elem_bytes) {
+    case 2:
+      hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(z), rows, cols, n);
+      break;
+    case 4:
+      hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(x),
+                         static_cast<uint32_t*>(z), rows, cols, n);
+      break;
+    default:
+      return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_transpose_batched: element size %d not supported", elem_bytes);
+  }
+  return asc::check_launch("asc_transpose_batched");
 }
 
 extern "C" int32_t asc_binary(int32_t op, int32_t dtype, const void* x, const void* y, void* out, int64_t n,

@@ -391,6 +391,46 @@ def unary_f32(x: torch.Tensor, out: torch.Tensor, op: str, n: Optional[int] = No
     _native.call("asc_unary_f32", UNARY_OPS.index(op), x.data_ptr(), out.data_ptr(), n, _stream(stream))
 
 
+_FLOAT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def unary(x: torch.Tensor, out: torch.Tensor, op: str, n: Optional[int] = None, stream=None) -> None:
+    """out[:n] = op(x[:n]) on float32 / float16 / bfloat16 (16-bit: fp32 op, one RNE rounding)."""
+    if op not in UNARY_OPS:
+        raise ValueError(f"unknown unary op {op!r}; expected one of {UNARY_OPS}")
+    n = x.numel() if n is None else int(n)
+    code = _code(x, "x", _FLOAT_DTYPES)
+    if out.dtype != x.dtype:
+        raise TypeError(f"'out' must be {x.dtype}, got {out.dtype}")
+    _flat(x, "x", n)
+    _flat(out, "out", n)
+    _native.call("asc_unary", UNARY_OPS.index(op), code, x.data_ptr(), out.data_ptr(), n, _stream(stream))
+
+
+def axpy(src: torch.Tensor, dst: torch.Tensor, scalar: float, n: Optional[int] = None, stream=None) -> None:
+    """dst[:n] = src[:n] * scalar + dst[:n] (asc.axpy): float32 / float16 / bfloat16, the
+    scalar rounded to the element type, fp32 math, one rounding of the result."""
+    n = src.numel() if n is None else int(n)
+    code = _code(src, "src", _FLOAT_DTYPES)
+    if dst.dtype != src.dtype:
+        raise TypeError(f"'dst' must be {src.dtype}, got {dst.dtype}")
+    _flat(src, "src", n)
+    _flat(dst, "dst", n)
+    _native.call("asc_axpy", code, src.data_ptr(), dst.data_ptr(), float(_scalar_parts(scalar, src.dtype)[0]), n,
+                 _stream(stream))
+
+
+def transpose_batched(x: torch.Tensor, z: torch.Tensor, batch: int, rows: int, cols: int, stream=None) -> None:
+    """z[b, c, r] = x[b, r, c] for row-major [batch, rows, cols] of 2- or 4-byte elements."""
+    n = int(batch) * int(rows) * int(cols)
+    _flat(x, "x", n)
+    _flat(z, "z", n)
+    if z.dtype != x.dtype:
+        raise TypeError(f"'z' must be {x.dtype}, got {z.dtype}")
+    _native.call("asc_transpose_batched", x.element_size(), x.data_ptr(), z.data_ptr(), int(batch), int(rows),
+                 int(cols), _stream(stream))
+
+
 def binary(x: Any, y: Any, out: torch.Tensor, op: str, n: Optional[int] = None, stream=None) -> None:
     """out[:n] = op(x, y) with either operand a tensor or a scalar (asc2 binary ops,
     python/asc/language/tile/binary_ops.py); the result dtype is the tensor operand's."""

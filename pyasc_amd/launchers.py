@@ -513,27 +513,29 @@ def _broadcast_dup(call: KernelCall) -> None:
 # asc1 kernels address the Ascend pipeline explicitly (GlobalTensor views, TQue queues,
 # data_copy); what they compute is registered here by signature, like the asc2 kernels.
 
-def _block_add(call: KernelCall, block_stride: int, block_cover: int) -> None:
-    """z[b*stride + j] = x[..] + y[..] for blocks b < grid and j < cover: the asc1 vadd
-    bodies, where block b views x, y, z from b*stride and adds ``cover`` elements.  The
-    union of the blocks is clipped at z's length (the NPU copy does not clip)."""
-    x, y, z = (call.args[k].reshape(-1) for k in ("x", "y", "z"))
-    n = z.numel()
-    grid = call.grid
+def _block_ranges(n: int, grid: int, block_stride: int, block_cover: int) -> List[Tuple[int, int]]:
+    """[start, end) ranges written by asc1 blocks b < grid that each process ``block_cover``
+    elements from b * block_stride (TILE_NUM tiles of TILE_LENGTH), clipped at n (the NPU
+    copy does not clip).  One range when the blocks tile the data without gaps."""
     if block_stride <= 0 or block_cover < 0:
         raise ValueError(f"invalid block length {block_stride} / elements per block {block_cover}")
+    if grid <= 0 or block_cover == 0:
+        return []
     if block_cover >= block_stride:
-        covered = min(n, (grid - 1) * block_stride + block_cover)
-        if covered > 0:
-            tile = min(covered, 1 << 30)
-            kernels.vadd(x, y, z, covered, tile, ceildiv(covered, tile), 1, call.stream)
-        return
-    full = min(grid, n // block_stride)  # blocks whose whole stride lies inside z
-    if full > 0 and block_cover > 0:
-        kernels.tile_binary(x, y, z, "add", [full, block_stride], [full, block_cover], [0, 0], call.stream)
-    start = full * block_stride
-    if full < grid and start < n and block_cover > 0:
-        kernels.tile_binary(x, y, z, "add", [n], [block_cover], [start], call.stream)
+        end = min(n, (grid - 1) * block_stride + block_cover)
+        return [(0, end)] if end > 0 else []
+    return [(b * block_stride, min(n, b * block_stride + block_cover)) for b in range(grid) if b * block_stride < n]
+
+
+def _block_add(call: KernelCall, block_stride: int, block_cover: int) -> None:
+    """z = x + y over the blocks' ranges (the asc1 vadd bodies)."""
+    x, y, z = (call.args[k].reshape(-1) for k in ("x", "y", "z"))
+    for s, e in _block_ranges(z.numel(), call.grid, block_stride, block_cover):
+        if x.dtype in (torch.float32, torch.float16, torch.bfloat16, torch.int32):
+            tile = min(e - s, 1 << 30)
+            kernels.vadd(x[s:e], y[s:e], z[s:e], e - s, tile, ceildiv(e - s, tile), 1, call.stream)
+        else:
+            kernels.binary(x[s:e], y[s:e], z[s:e], "add", stream=call.stream)
 
 
 @register("vadd_kernel", ("x", "y", "z", "BLOCK_LENGTH", "BUFFER_NUM", "TILE_LENGTH", "TILE_NUM"),
@@ -630,3 +632,88 @@ def _tutorial_matmul_cube_only(call: KernelCall) -> None:
     t = call.args["tiling"]
     _asc1_matmul(call, *_tiles_of(call), call.args["bias"] if int(getattr(t, "is_bias", 0)) else None, None,
                  t.used_core_num)
+
+
+# ------------------------------------------- asc1 generalization tests (python/test/generalization/basic)
+# Each kernel body processes tile_num tiles of tile_length from b * block_length (block b).
+
+def _gen_ranges(call: KernelCall, out: torch.Tensor):
+    c = call.consts
+    return _block_ranges(out.numel(), call.grid, int(c["block_length"]), int(c["tile_num"]) * int(c["tile_length"]))
+
+
+@register("vadd_kernel", ("x", "y", "z", "block_length", "buffer_num", "tile_length", "tile_num"),
+          "python/test/generalization/basic/test_vadd.py:21-70 (also test_vadd_bits.py, test_vadd_l0.py, "
+          "test_vadd_sw.py, whose one-repeat adds cover their 64-element tiles)")
+def _gen_vadd(call: KernelCall) -> None:
+    _block_add(call, int(call.consts["block_length"]), int(call.consts["tile_num"]) * int(call.consts["tile_length"]))
+
+
+@register("vadds_kernel", ("x", "scalar", "z", "block_length", "buffer_num", "tile_length", "tile_num"),
+          "python/test/generalization/basic/test_vadds.py:21-61")
+def _gen_vadds(call: KernelCall) -> None:
+    # asc.adds: z = x + scalar, the scalar in x's element type
+    x, z = call.args["x"].reshape(-1), call.args["z"].reshape(-1)
+    for s, e in _gen_ranges(call, z):
+        kernels.binary(x[s:e], call.args["scalar"], z[s:e], "add", stream=call.stream)
+
+
+@register("vsqrt_kernel", ("x", "z", "block_length", "buffer_num", "tile_length", "tile_num"),
+          "python/test/generalization/basic/test_vsqrt.py:21-61")
+def _gen_vsqrt(call: KernelCall) -> None:
+    x, z = call.args["x"].reshape(-1), call.args["z"].reshape(-1)
+    for s, e in _gen_ranges(call, z):
+        kernels.unary(x[s:e], z[s:e], "sqrt", stream=call.stream)
+
+
+@register("duplicate_kernel", ("scalar", "z", "block_length", "buffer_num", "tile_length", "tile_num"),
+          "python/test/generalization/basic/test_duplicate.py:21-46")
+def _gen_duplicate(call: KernelCall) -> None:
+    # asc.duplicate: every element takes the scalar, in z's element type
+    z = call.args["z"].reshape(-1)
+    scalar = call.args["scalar"]
+    scalar = scalar.item() if isinstance(scalar, torch.Tensor) else scalar
+    for s, e in _gen_ranges(call, z):
+        kernels.fill(z[s:e], scalar, stream=call.stream)
+
+
+@register("axpy_kernel", ("x", "y", "z", "scalar", "block_length", "buffer_num", "tile_length", "tile_num"),
+          "python/test/generalization/basic/test_axpy.py:21-76")
+def _gen_axpy(call: KernelCall) -> None:
+    # asc.axpy(z_local, y_local, scalar): z = y * scalar + z (x is loaded and unused)
+    y, z = call.args["y"].reshape(-1), call.args["z"].reshape(-1)
+    for s, e in _gen_ranges(call, z):
+        kernels.axpy(y[s:e], z[s:e], _scalar(call.args["scalar"]), stream=call.stream)
+
+
+@register("copy_kernel", ("x", "z", "data_size"), "python/test/generalization/basic/test_copy.py:21-67")
+def _gen_copy(call: KernelCall) -> None:
+    """z[0:data_size] = 0, then asc.copy with mask 64, 4 repeats of 8 blocks (256 bytes):
+    repeat r copies 64 elements from r * (256 / element size), for the repeats that fit
+    in data_size (the test's golden, test_copy.py:107-122)."""
+    x, z = call.args["x"].reshape(-1), call.args["z"].reshape(-1)
+    n = int(call.consts["data_size"])
+    if n > min(x.numel(), z.numel()):
+        raise ValueError(f"data_size {n} exceeds the tensors ({x.numel()}, {z.numel()} elements)")
+    kernels.fill(z, 0, n, call.stream)
+    stride = 256 // z.element_size()
+    for r in range(4):
+        s = r * stride
+        if s + 64 > n:
+            break
+        kernels.broadcast_rows(x[s:s + 64], z[s:s + 64], 1, 64, call.stream)
+
+
+@register("transpose_kernel", ("x", "z", "block_length", "buffer_num", "tile_length", "tile_num"),
+          "python/test/generalization/basic/test_transpose.py:21-67")
+def _gen_transpose(call: KernelCall) -> None:
+    """asc.transpose of each 16 x 16 tile of 2-byte elements (tile_length 256)."""
+    x, z = call.args["x"].reshape(-1), call.args["z"].reshape(-1)
+    if int(call.consts["tile_length"]) != 256 or z.element_size() != 2:
+        raise NotImplementedError("asc.transpose takes 16x16 tiles of 2-byte elements (tile_length 256)")
+    if int(call.consts["block_length"]) % 256:
+        raise NotImplementedError("block_length must be a multiple of 256 so that every tile is a whole 16x16 tile")
+    for s, e in _gen_ranges(call, z):
+        if (e - s) % 256:
+            raise ValueError(f"elements [{s}, {e}) do not hold whole 16x16 tiles")
+        kernels.transpose_batched(x[s:e], z[s:e], (e - s) // 256, 16, 16, call.stream)

@@ -349,3 +349,18 @@ def test_compile_options_reach_the_launch(recorded):
     a = np.zeros((4, 4), np.float16)
     matmul_kernel[3](a, a, np.zeros((4, 4), np.float32), np.zeros(4, np.float32), asc.adv.TCubeTiling(), a)
     assert recorded[-1][-1]["matmul_cube_only"] is True
+
+
+@pytest.mark.parametrize("n, grid, stride, cover", [(8192, 16, 512, 512), (8191, 16, 512, 1024), (100, 3, 40, 7),
+                                                    (10, 5, 4, 3), (5, 16, 1, 8), (0, 4, 4, 4), (50, 0, 4, 4)])
+def test_block_ranges_match_oracle_coverage(n, grid, stride, cover):
+    # the launchers' asc1 block ranges write exactly the elements the oracle's block_add writes
+    from oracle import asc2_oracle as O
+    from pyasc_amd.launchers import _block_ranges
+    mask = np.zeros(n, bool)
+    for s, e in _block_ranges(n, grid, stride, cover):
+        assert 0 <= s < e <= n
+        mask[s:e] = True
+    written = O.block_add(np.ones(n, np.float32), np.ones(n, np.float32), np.zeros(n, np.float32), grid, stride,
+                          cover) != 0
+    np.testing.assert_array_equal(mask, written)
