@@ -301,6 +301,12 @@ int32_t asc_axpy(int32_t dtype, const void* src, void* dst, double scalar, int64
  * x and z must not overlap. */
 int32_t asc_transpose_batched(int32_t elem_bytes, const void* x, void* z, int64_t batch,
                               int64_t rows, int64_t cols, asc_stream_t stream);
+/* dst[i] = saturate_int8(rint(src[i] * scale + offset)) (asc.adv.quant,
+ * python/asc/language/adv/quantization.py:18-36; python/test/generalization/adv/
+ * test_quant.py): float32 / float16 / bfloat16 src; scale and offset converted to the
+ * source dtype and the multiply and add each rounded to it; ties to even; NaN -> 0. */
+int32_t asc_quant_i8(int32_t dtype, const void* src, int8_t* dst, double scale, double offset,
+                     int64_t n, asc_stream_t stream);
 
 #define ASC_BIN_ADD 0
 #define ASC_BIN_SUB 1

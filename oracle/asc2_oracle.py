@@ -41,6 +41,9 @@ How each function is pinned (tests/test_oracle.py):
                   the blocks, test_atomic_ops.py:62-67); closed forms: the column sum
                   plus n_tiles * addend (integers), the column max / min plus addend.
   fill            torch.full (test_shape_ops.py:75-78).
+  quant_i8        the quant test's golden torch.round(src * 2.0 + 0.9).to(int8) on its
+                  recipe (test_quant.py:79-104; fp32 exact by construction), ties to even,
+                  saturation and NaN by hand.
   softmax f16     torch.softmax on float16 (within one float16 ulp), constant row
                   -> 1/n rounded, two-point rows.
   rms_norm        torch.nn.functional.rms_norm in float64, constant rows (closed
@@ -519,6 +522,21 @@ def atomic_tiles(x: np.ndarray, z: np.ndarray, op: str, n_tiles: int, tile_len: 
         tile = binary_elements(x[b * tile_len:(b + 1) * tile_len], c, "add", dtype)
         res = binary_elements(res, tile, op, dtype)
     return res
+
+
+def quant_i8(src: np.ndarray, scale: float, offset: float, dtype: str) -> np.ndarray:
+    """asc.adv.quant (python/asc/language/adv/quantization.py:18-36; test_quant.py's kernel):
+    scale and offset materialized in the source dtype (quantization.py:28-29), the multiply
+    and the add each rounded to that dtype, then rint (ties to even), clamped to the int8
+    range; NaN gives 0 (build-defined).  bfloat16 as uint16 bit patterns."""
+    def rnd(v):
+        return _to_f32(_from_f32(v, dtype), dtype)
+    sc = rnd(np.full(1, scale, np.float32))[0]
+    of = rnd(np.full(1, offset, np.float32))[0]
+    with np.errstate(invalid="ignore"):
+        v = rnd(rnd(_to_f32(src, dtype) * sc) + of)
+        r = np.clip(np.rint(v), -128, 127)
+        return np.where(np.isnan(v), 0, r).astype(np.int8)
 
 
 def fill(n: int, value, dtype: str) -> np.ndarray:

@@ -65,6 +65,7 @@ SIGNATURES = {
     "asc_unary": [_c_i32, _c_i32, _c_p, _c_p, _c_i64, _c_p],
     "asc_axpy": [_c_i32, _c_p, _c_p, _c_f64, _c_i64, _c_p],
     "asc_transpose_batched": [_c_i32, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
+    "asc_quant_i8": [_c_i32, _c_p, _c_p, _c_f64, _c_f64, _c_i64, _c_p],
 }
 # entry points returning a C string
 STRING_FUNCS = ("asc_last_error", "asc_version")

@@ -163,6 +163,28 @@ class MatmulApiTiling:
     def set_split_range(self, *args, **kwargs) -> int:
         return 0
 
+    def set_a_layout(self, b: int, s: int, n: int, g: int, d: int) -> int:
+        self.a_layout = (int(b), int(s), int(n), int(g), int(d))
+        return 0
+
+    def set_b_layout(self, b: int, s: int, n: int, g: int, d: int) -> int:
+        self.b_layout = (int(b), int(s), int(n), int(g), int(d))
+        return 0
+
+    def set_c_layout(self, b: int, s: int, n: int, g: int, d: int) -> int:
+        self.c_layout = (int(b), int(s), int(n), int(g), int(d))
+        return 0
+
+    def set_batch_num(self, batch: int) -> int:
+        self.batch_num = int(batch)
+        return 0
+
+    def set_batch_info_for_normal(self, batch_a: int, batch_b: int, m: int, n: int, k: int) -> int:
+        self.set_a_layout(batch_a, m, 1, 1, k)
+        self.set_b_layout(batch_b, k, 1, 1, n)
+        self.set_c_layout(max(int(batch_a), int(batch_b)), m, 1, 1, n)
+        return 0
+
     def set_matmul_config_params(self, *args, **kwargs) -> int:
         return 0
 
@@ -188,6 +210,14 @@ class MatmulApiTiling:
                       org_ka=org[2], org_kb=org[3], single_core_m=single_m, single_core_n=single_n,
                       single_core_k=self.k, base_m=base_m, base_n=base_n, base_k=base_k, depth_a1=1, depth_b1=1,
                       step_m=1, step_n=1, step_ka=1, step_kb=1, is_bias=int(self.is_bias), share_mode=0)
+        # batch layouts (TCubeTiling's ALayoutInfo* / BLayoutInfo* / CLayoutInfo* / BatchNum;
+        # -1 when not set, as the struct's defaults, python/asc/language/adv/tiling.py:45-60)
+        for prefix, names, layout in (("a", "bsngd", getattr(self, "a_layout", None)),
+                                      ("b", "bsngd", getattr(self, "b_layout", None)),
+                                      ("c", ("b", "s1", "n", "g", "s2"), getattr(self, "c_layout", None))):
+            for i, name in enumerate(names):
+                fields[f"{prefix}_layout_info_{name}"] = layout[i] if layout else -1
+        fields["batch_num"] = getattr(self, "batch_num", -1)
         for key, value in fields.items():
             setattr(tiling, key, value)
         return 0

@@ -53,6 +53,22 @@ class CompilationArch(Enum):
         return self.value
 
 
+class KernelType(Enum):
+    """Core mix a kernel runs on (python/asc/runtime/config.py:54-62), accepted as the
+    ``kernel_type`` jit option.  On MI355X every kernel runs on the same compute units; the
+    value matters only where it fixes how many instances a launch runs: an asc1 Matmul
+    kernel as MIX_AIC_1_2 runs two per block (one cube core, two vector cores), any other
+    type one."""
+    AIV_ONLY = 0
+    AIC_ONLY = 1
+    MIX_AIV_HARD_SYNC = 2
+    MIX_AIC_HARD_SYNC = 3
+    MIX_AIV_1_0 = 4
+    MIX_AIC_1_0 = 5
+    MIX_AIC_1_1 = 6
+    MIX_AIC_1_2 = 7
+
+
 _state = {"backend": Backend.HIP, "platform": Platform.MI355X, "device_id": 0}
 
 

@@ -338,6 +338,24 @@ __global__ void __launch_bounds__(kThreads) transpose_kernel(const T* __restrict
   }
 }
 
+// ---- quantization to int8 (asc.adv.quant, python/asc/language/adv/quantization.py:18-36;
+// the kernel of python/test/generalization/adv/test_quant.py):
+// dst = saturate_int8(rint(src * scale + offset)) with scale and offset materialized in the
+// source dtype (quantization.py:28-29), the multiply and the add each rounded to that
+// dtype, rint rounding half to even, results clamped to [-128, 127], NaN giving 0.
+template <class E>
+__global__ void __launch_bounds__(kThreads) quant_i8_kernel(const typename E::T* __restrict__ src,
+                                                            int8_t* __restrict__ dst, float scale_f, float offset_f,
+                                                            int64_t n) {
+  const float sc = E::in(element_of<E>(scale_f, 0)), of = E::in(element_of<E>(offset_f, 0));
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const float v = E::in(E::out(E::in(E::out(E::in(src[i]) * sc)) + of));
+    const float r = fminf(fmaxf(rintf(v), -128.0f), 127.0f);
+    dst[i] = v != v ? int8_t(0) : static_cast<int8_t>(r);
+  }
+}
+
 // ---- fill: every element of z takes the scalar c converted to the element type
 template <class E>
 __global__ void __launch_bounds__(kThreads) fill_kernel(typename E::T* __restrict__ z, int64_t n, float c_f,
@@ -608,4 +626,29 @@ extern "C" int32_t asc_fill(int32_t dtype, void* z, int64_t n, double c_f, int64
     default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_fill: unsupported dtype code %d", dtype);
   }
 #undef ASC_FILL
+}
+
+extern "C" int32_t asc_quant_i8(int32_t dtype, const void* src, int8_t* dst, double scale, double offset, int64_t n,
+                                asc_stream_t stream) {
+  ASC_REQUIRE(n >= 0, ASC_ERR_INVALID_ARG, "asc_quant_i8: negative length");
+  if (n == 0) return ASC_OK;
+  ASC_REQUIRE(src && dst, ASC_ERR_INVALID_ARG, "asc_quant_i8: null buffer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n));
+  switch (dtype) {
+    case ASC_DT_FLOAT32:
+      hipLaunchKernelGGL(quant_i8_kernel<F32>, grid, dim3(kThreads), 0, s, static_cast<const float*>(src), dst,
+                         static_cast<float>(scale), static_cast<float>(offset), n);
+      break;
+    case ASC_DT_FLOAT16:
+      hipLaunchKernelGGL(quant_i8_kernel<F16>, grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(src), dst,
+                         static_cast<float>(scale), static_cast<float>(offset), n);
+      break;
+    case ASC_DT_BFLOAT16:
+      hipLaunchKernelGGL(quant_i8_kernel<BF16>, grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(src), dst,
+                         static_cast<float>(scale), static_cast<float>(offset), n);
+      break;
+    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_quant_i8: unsupported dtype code %d", dtype);
+  }
+  return asc::check_launch("asc_quant_i8");
 }

@@ -431,6 +431,20 @@ def transpose_batched(x: torch.Tensor, z: torch.Tensor, batch: int, rows: int, c
                  int(cols), _stream(stream))
 
 
+def quant_i8(src: torch.Tensor, dst: torch.Tensor, scale: float, offset: float, n: Optional[int] = None,
+             stream=None) -> None:
+    """dst[:n] = saturate_int8(rint(src * scale + offset)) (asc.adv.quant): scale and offset
+    in src's dtype, each operation rounded to it, ties to even, NaN -> 0."""
+    n = src.numel() if n is None else int(n)
+    code = _code(src, "src", _FLOAT_DTYPES)
+    if dst.dtype != torch.int8:
+        raise TypeError(f"'dst' must be int8, got {dst.dtype}")
+    _flat(src, "src", n)
+    _flat(dst, "dst", n)
+    _native.call("asc_quant_i8", code, src.data_ptr(), dst.data_ptr(), float(scale), float(offset), n,
+                 _stream(stream))
+
+
 def binary(x: Any, y: Any, out: torch.Tensor, op: str, n: Optional[int] = None, stream=None) -> None:
     """out[:n] = op(x, y) with either operand a tensor or a scalar (asc2 binary ops,
     python/asc/language/tile/binary_ops.py); the result dtype is the tensor operand's."""

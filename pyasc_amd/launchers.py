@@ -563,8 +563,13 @@ def _matmul_instances(call: KernelCall) -> int:
     """Kernel instances a launch of ``grid`` blocks runs for an asc1 Matmul kernel: a mixed
     cube + vector kernel runs as MIX_AIC_1_2, one cube core and two vector cores per block,
     and get_block_idx counts the vector cores; with matmul_cube_only it runs as AIC_ONLY,
-    one instance per block (python/asc/runtime/compiler.py:291-299)."""
-    return call.grid * (1 if call.extra.get("options", {}).get("matmul_cube_only") else 2)
+    one instance per block (python/asc/runtime/compiler.py:291-299).  An explicit
+    kernel_type option decides instead."""
+    options = call.extra.get("options", {})
+    kernel_type = options.get("kernel_type")
+    if kernel_type is not None:
+        return call.grid * (2 if getattr(kernel_type, "name", str(kernel_type)) == "MIX_AIC_1_2" else 1)
+    return call.grid * (1 if options.get("matmul_cube_only") else 2)
 
 
 def _asc1_matmul(call: KernelCall, tiles_m: int, tiles_n: int, bias, alpha=None, used_core_num=None) -> None:
@@ -617,11 +622,45 @@ def _asc1_matmul_torch(call: KernelCall) -> None:
                  int(k["used_core_num"]))
 
 
-@register("matmul_kernel", ("a", "b", "c", "tiling", "workspace"), "python/tutorials/03_matmul_mix/matmul_mix.py:31-77")
-def _tutorial_matmul_mix(call: KernelCall) -> None:
-    """c = a @ b, fp32 accumulation and output (Matmul.iterate_all without bias); blocks
-    below tiling.used_core_num compute one tile each (matmul_mix.py:47-52)."""
-    _asc1_matmul(call, *_tiles_of(call), None, None, call.args["tiling"].used_core_num)
+@register("matmul_kernel", ("a", "b", "c", "tiling", "workspace"),
+          "python/tutorials/03_matmul_mix/matmul_mix.py:31-77; python/test/generalization/adv/"
+          "test_matmul_iterate_all.py:23-47 and test_matmul_iterate_batch.py:28-51")
+def _matmul_tiling(call: KernelCall) -> None:
+    """Matmul.iterate_all without bias (the tutorial and iterate_all test): c = a @ b with fp32
+    accumulation and output, or int8 a, b -> exact int32 c; instances below
+    tiling.used_core_num compute one tile each (matmul_mix.py:47-52).  A tiling that carries
+    a batch (batch_num and the A/B layouts, as test_matmul_iterate_batch.py's generate_tiling
+    sets them) selects that test's Matmul.iterate_batch body instead."""
+    t = call.args["tiling"]
+    if int(getattr(t, "batch_num", -1)) > 0:
+        _matmul_batched(call, t)
+        return
+    a, b, c = call.args["a"], call.args["b"], call.args["c"]
+    if a.dtype == torch.int8:
+        tiles_m, tiles_n = _tiles_of(call)
+        if min(_matmul_instances(call), int(t.used_core_num)) < tiles_m * tiles_n:
+            raise NotImplementedError("the launch does not cover every tile")
+        kernels.matmul_i8(a, b, c, stream=call.stream)
+        return
+    _asc1_matmul(call, *_tiles_of(call), None, None, t.used_core_num)
+
+
+def _matmul_batched(call: KernelCall, t) -> None:
+    """Matmul.iterate_batch (test_matmul_iterate_batch.py:47-49, golden :116-141): A holds
+    batch_a [m, k] matrices stacked by rows, B batch_b [k, n], C batch_num [m, n]; output
+    matrix i is A[i // (batch / batch_a)] @ B[i // (batch / batch_b)] in fp32."""
+    a, b, c = (call.args[k].reshape(-1) for k in ("a", "b", "c"))
+    batch = int(t.batch_num)
+    ba, m, k = int(t.a_layout_info_b), int(t.a_layout_info_s), int(t.a_layout_info_d)
+    bb, k2, n = int(t.b_layout_info_b), int(t.b_layout_info_s), int(t.b_layout_info_d)
+    if min(ba, bb, m, k, n) <= 0 or k2 != k or batch % ba or batch % bb:
+        raise ValueError(f"inconsistent batch layout: batch {batch}, A {ba}x[{m},{k}], B {bb}x[{k2},{n}]")
+    if a.numel() < ba * m * k or b.numel() < bb * k * n or c.numel() < batch * m * n:
+        raise ValueError("a, b or c holds fewer elements than the batch layout describes")
+    for i in range(batch):
+        ia, ib = i // (batch // ba), i // (batch // bb)
+        kernels.matmul(a[ia * m * k:(ia + 1) * m * k].view(m, k), b[ib * k * n:(ib + 1) * k * n].view(k, n),
+                       c[i * m * n:(i + 1) * m * n].view(m, n), stream=call.stream)
 
 
 @register("matmul_kernel", ("a", "b", "c", "bias", "tiling", "workspace"),
@@ -717,3 +756,13 @@ def _gen_transpose(call: KernelCall) -> None:
         if (e - s) % 256:
             raise ValueError(f"elements [{s}, {e}) do not hold whole 16x16 tiles")
         kernels.transpose_batched(x[s:e], z[s:e], (e - s) // 256, 16, 16, call.stream)
+
+
+
+@register("quant_kernel", ("src_gm", "dst_gm", "size", "tmp_min_bytes", "use_config"),
+          "python/test/generalization/adv/test_quant.py:22-57")
+def _gen_quant(call: KernelCall) -> None:
+    """asc.adv.quant with the body's scale 2.0 and offset 0.9 on the first ``size`` elements;
+    the temporary buffer size and the QuantConfig do not change the result."""
+    n = int(call.args["size"])
+    kernels.quant_i8(call.args["src_gm"].reshape(-1), call.args["dst_gm"].reshape(-1), 2.0, 0.9, n, call.stream)

@@ -9,6 +9,7 @@ import torch
 
 import asc
 import asc.lib.runtime as rt
+import asc.runtime.config as config
 
 pytestmark = pytest.mark.gpu
 
@@ -184,3 +185,129 @@ def test_transpose_many_tiles(device):
     z = torch.zeros_like(x)
     transpose_kernel[8](x, z, 1024, 1, 256, 4)
     assert torch.equal(z, x.reshape(-1, 16, 16).transpose(1, 2).reshape(-1))
+
+
+# ------------------------------------------------------------------- python/test/generalization/adv
+
+def _adv_tiling(m, n, k, dtype, bias=False, batch=None):
+    # generate_tiling of test_matmul.py:94-113 / test_matmul_iterate_all.py:70-87 /
+    # test_matmul_iterate_batch.py:73-95
+    import asc.lib.host as host
+    t = host.MultiCoreMatmulTiling(host.get_ascendc_platform())
+    host_dtype = host.DataType.DT_FLOAT if dtype == torch.float32 else host.DataType.DT_FLOAT16
+    t.set_a_type(host.TPosition.GM, host.CubeFormat.ND, host_dtype, False)
+    t.set_b_type(host.TPosition.GM, host.CubeFormat.ND, host_dtype, False)
+    t.set_c_type(host.TPosition.VECCALC, host.CubeFormat.ND, host.DataType.DT_FLOAT)
+    t.set_bias_type(host.TPosition.GM, host.CubeFormat.ND, host.DataType.DT_FLOAT)
+    t.set_dim(16)
+    t.set_org_shape(m, n, k)
+    t.set_shape(m, n, k)
+    if bias:
+        t.enable_bias(True)
+    t.set_traverse(host.MatrixTraverse.FIRSTM)
+    t.set_buffer_space(-1, -1, -1)
+    if batch:
+        t.set_a_layout(batch, m, 1, 1, k)
+        t.set_b_layout(batch, k, 1, 1, n)
+        t.set_c_layout(batch, m, 1, 1, n)
+        t.set_batch_num(batch)
+    tiling = asc.adv.TCubeTiling()
+    t.get_tiling(tiling)
+    return tiling
+
+
+@asc.jit
+def matmul_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress, alpha: float,
+                  tiling: asc.adv.TCubeTiling, bias: asc.GlobalAddress, workspace: asc.GlobalAddress):
+    raise AssertionError("kernel bodies are not executed")
+
+
+def test_adv_matmul(device):
+    # test_matmul.py:126-145: fp32 1024x256x512 (m, k, n), bias, leaky relu 0.01
+    m, k, n = 1024, 256, 512
+    a = (torch.rand((m, k)) - .5) * 10
+    b = (torch.rand((k, n)) - .5) * 10
+    bias = (torch.rand((1, n)) - .5) * 10
+    c = torch.zeros((m, n))
+    workspace = torch.zeros(16 * 1024 * 1024, dtype=torch.uint8)
+    matmul = a @ b + bias
+    tiling = _adv_tiling(m, n, k, torch.float32, bias=True)
+    matmul_kernel[tiling.used_core_num, rt.current_stream()](a, b, c, 0.01, tiling, bias, workspace)
+    assert torch.allclose(c, torch.where(matmul >= 0, matmul, matmul * 0.01), atol=1e-3)
+
+
+@asc.jit
+def iterate_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress, tiling: asc.adv.TCubeTiling,
+                   workspace: asc.GlobalAddress):
+    raise AssertionError("kernel bodies are not executed")
+
+
+iterate_kernel.fn_name = "matmul_kernel"  # test_matmul_iterate_all.py:24, test_matmul_iterate_batch.py:29
+
+
+@pytest.mark.parametrize("dtype, size", [(torch.float16, (256, 64, 128)), (torch.int8, (256, 64, 128)),
+                                         (torch.int8, (300, 96, 200))], ids=str)
+def test_adv_matmul_iterate_all(device, dtype, size):
+    # test_matmul_iterate_all.py:100-120 (its body also takes int8 -> int32)
+    m, k, n = size
+    if dtype == torch.float16:
+        a = (torch.rand((m, k), dtype=dtype) - 0.5) * 10
+        b = (torch.rand((k, n), dtype=dtype) - 0.5) * 10
+        c = torch.zeros((m, n), dtype=torch.float32)
+        matmul = a.to(torch.float32) @ b.to(torch.float32)
+    else:
+        a = torch.randint(-5, 5, (m, k), dtype=dtype)
+        b = torch.randint(-5, 5, (k, n), dtype=dtype)
+        c = torch.zeros((m, n), dtype=torch.int32)
+        matmul = a.to(torch.int32) @ b.to(torch.int32)
+    workspace = torch.zeros(16 * 1024 * 1024, dtype=torch.uint8)
+    tiling = _adv_tiling(m, n, k, dtype)
+    iterate_kernel[tiling.used_core_num, rt.current_stream()](a, b, c, tiling, workspace)
+    assert torch.allclose(c, matmul, atol=1e-3)
+    if dtype == torch.int8:
+        assert torch.equal(c, matmul)
+
+
+@pytest.mark.parametrize("dtype, size", [(torch.float32, (64, 64, 64)), (torch.float16, (32, 32, 32))], ids=str)
+def test_adv_matmul_iterate_batch(device, dtype, size):
+    # test_matmul_iterate_batch.py:109-150, BATCH_A = BATCH_B = BATCH = 2
+    m, k, n = size
+    a = torch.vstack([(torch.rand((m, k), dtype=dtype) - .5) * 10 for _ in range(2)])
+    b = torch.vstack([(torch.rand((k, n), dtype=dtype) - .5) * 10 for _ in range(2)])
+    matmul = torch.vstack([a[i * m:(i + 1) * m].float() @ b[i * k:(i + 1) * k].float() for i in range(2)])
+    c = torch.zeros((2 * m, n), dtype=torch.float32)
+    workspace = torch.zeros(16 * 1024 * 1024, dtype=torch.uint8)
+    tiling = _adv_tiling(m, n, k, dtype, batch=2)
+    iterate_kernel[tiling.used_core_num, rt.current_stream()](a, b, c, tiling, workspace)
+    assert torch.allclose(c, matmul, atol=1e-3)
+
+
+@asc.jit(kernel_type=config.KernelType.AIV_ONLY)
+def quant_kernel(src_gm: asc.GlobalAddress, dst_gm: asc.GlobalAddress, size: int, tmp_min_bytes: int,
+                 use_config: asc.ConstExpr[bool]):
+    raise AssertionError("kernel bodies are not executed")
+
+
+@pytest.mark.parametrize("use_config", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_adv_quant(device, dtype, use_config):
+    # test_quant.py:94-104
+    src = torch.rand((32,), dtype=dtype) * 8.0 - 4.0
+    dst = torch.zeros_like(src, dtype=torch.int8)
+    quant_kernel[1, rt.current_stream()](src, dst, src.numel(), 512, use_config)
+    assert torch.allclose(dst, torch.round((src * 2.0) + 0.9).to(torch.int8))
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_quant_vs_oracle(device, dtype):
+    from pyasc_amd import kernels
+    from oracle import asc2_oracle as O
+    g = torch.Generator().manual_seed(9)
+    n = (1 << 20) + 11
+    src = (torch.randn(n, generator=g) * 60).to(getattr(torch, dtype))
+    src[:6] = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.05, -0.45, 63.2])
+    dst = torch.empty(n, dtype=torch.int8, device=device)
+    kernels.quant_i8(src.to(device), dst, 2.0, 0.9)
+    torch.cuda.synchronize()
+    host = src.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else src.numpy()
+    np.testing.assert_array_equal(dst.cpu().numpy(), O.quant_i8(host, 2.0, 0.9, dtype))

@@ -690,3 +690,24 @@ def test_block_add_reference_golden_and_gaps():
     x, y = np.arange(10, dtype=np.float32), np.full(10, 100, dtype=np.float32)
     got = O.block_add(x, y, np.zeros(10, np.float32), 2, 4, 3)
     np.testing.assert_array_equal(got, [100, 101, 102, 0, 104, 105, 106, 0, 0, 0])
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_quant_matches_quant_test_golden(dtype):
+    # test_quant.py:79-104: src = rand * 8 - 4, golden torch.round(src * 2.0 + 0.9).to(int8)
+    td = getattr(torch, dtype)
+    g = torch.Generator().manual_seed(21)
+    src = (torch.rand(4096, generator=g) * 8.0 - 4.0).to(td)
+    golden = torch.round((src * 2.0) + 0.9).to(torch.int8).numpy()
+    np.testing.assert_array_equal(O.quant_i8(src.numpy(), 2.0, 0.9, dtype), golden)
+
+
+def test_quant_known_answers():
+    x = np.array([0.5, 1.5, 2.5, -0.5, -1.5, 127.4, 127.6, 1000.0, -128.4, -1000.0, np.nan, np.inf, -np.inf],
+                 np.float32)
+    np.testing.assert_array_equal(O.quant_i8(x, 1.0, 0.0, "float32"),
+                                  np.array([0, 2, 2, 0, -2, 127, 127, 127, -128, -128, 0, 127, -128], np.int8))
+    # the offset is rounded to the source dtype first: fp16(0.1) = 0.0999755859375
+    np.testing.assert_array_equal(O.quant_i8(np.array([2.4], np.float16), 1.0, 0.1, "float16"), [2])
+    bits = O.f32_to_bf16_bits(np.array([3.0, -3.0], np.float32))
+    np.testing.assert_array_equal(O.quant_i8(bits, 0.5, 0.0, "bfloat16"), [2, -2])  # 1.5 -> 2, -1.5 -> -2

@@ -364,3 +364,19 @@ def test_block_ranges_match_oracle_coverage(n, grid, stride, cover):
     written = O.block_add(np.ones(n, np.float32), np.ones(n, np.float32), np.zeros(n, np.float32), grid, stride,
                           cover) != 0
     np.testing.assert_array_equal(mask, written)
+
+
+def test_matmul_instances_per_kernel_type():
+    # MIX_AIC_1_2 (the default for mixed Matmul kernels) runs two instances per block,
+    # AIC_ONLY / matmul_cube_only and the other types one (python/asc/runtime/compiler.py:291-299)
+    from pyasc_amd.launchers import _matmul_instances
+    from pyasc_amd.registry import KernelCall
+    import asc.runtime.config as config
+
+    def call(**options):
+        return KernelCall("matmul_kernel", {}, {}, 12, 0, {"options": options})
+    assert _matmul_instances(call()) == 24
+    assert _matmul_instances(call(matmul_cube_only=True)) == 12
+    assert _matmul_instances(call(kernel_type=config.KernelType.MIX_AIC_1_2)) == 24
+    assert _matmul_instances(call(kernel_type=config.KernelType.AIC_ONLY)) == 12
+    assert _matmul_instances(call(kernel_type=config.KernelType.MIX_AIC_1_1)) == 12
