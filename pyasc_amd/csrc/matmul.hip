@@ -228,7 +228,6 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float* __restr
   const float* bcol = b + (b_ok ? n0 + r : 0);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int groups = (K + 15) / 16;
-#pragma unroll 4
   for (int g = wave; g < groups; g += 4) {
     const int kb = 16 * g + 4 * q;
     float av[4], bv[4];
