@@ -38,6 +38,7 @@ COMPILE_OPTIONS = ("debug", "strip_loc", "verify_sync", "print_ir_before_all", "
                    "opt_level", "run_asc2_passes", "densify_load_store", "insert_sync", "reuse_ub",
                    "reuse_ub_in_out", "static_alloc", "vf_fusion")
 LAUNCH_OPTIONS = ("core_num", "stream")
+_CONFIG_KEYWORDS = frozenset(CODEGEN_OPTIONS + COMPILE_OPTIONS + LAUNCH_OPTIONS)
 
 
 class ArgType:
@@ -95,6 +96,9 @@ class JITFunction:
         self.default_options: Dict[str, Any] = options
         self.launch_options = LaunchOptions()
         self.kernel_cache: Dict[str, ResolvedKernel] = {}
+        # first level in front of kernel_cache: a tuple of cheap per-call facts that determine
+        # the same cache factors (see _quick_key); it maps to the entry of kernel_cache
+        self._quick_cache: Dict[tuple, ResolvedKernel] = {}
         self._const_names: Optional[FrozenSet[str]] = None  # ConstExpr parameters, from the annotations
         self._hash: Optional[str] = None
         # plain positional calls can skip inspect.Signature.bind
@@ -233,9 +237,10 @@ class JITFunction:
 
     def _fast_bind(self, args: tuple, kwargs: Dict[str, Any]) -> Tuple[Dict[str, Any], Dict[str, Any], Dict[str, Any]]:
         """Binding and ConstExpr split without validation (validation runs on a cache miss)."""
-        if self.default_options:
-            kwargs = {**self.default_options, **kwargs}
-        options = {k: kwargs.pop(k) for k in list(kwargs) if k in self.get_config_keywords()} if kwargs else {}
+        options = dict(self.default_options)
+        if kwargs:
+            for k in [k for k in kwargs if k in _CONFIG_KEYWORDS]:
+                options[k] = kwargs.pop(k)
         if not kwargs and self._positional_only_call and len(args) == len(self.params):
             bound = dict(zip(self.params, args))
         else:
@@ -252,6 +257,34 @@ class JITFunction:
                 runtime_args[name] = value
         return runtime_args, constexprs, options
 
+    @staticmethod
+    def _quick_key(runtime_args: Dict[str, Any], constexprs: Dict[str, Any], call_options: Dict[str, Any]):
+        """A hashable tuple that determines the same cache factors as _gen_cache_factors, built
+        without string formatting: per runtime argument its class, and for tensors the dtype
+        and whether it is 0-dim (the pointer / by-value split); ConstExpr values and the options
+        given at the call tagged with their types (so 1, True and 1.0 stay distinct, as their
+        reprs are).  The decorator's options are the same for every call of this function and
+        the quick cache is per function, so they need no place in the key.  None when an
+        argument or value has no cheap form; the caller then takes the full path."""
+        parts = []
+        for value in runtime_args.values():
+            cls = value.__class__
+            if cls is int or cls is float or cls is bool:
+                parts.append(cls)
+            elif cls.__module__ == "torch" and cls.__name__ in ("Tensor", "Parameter"):
+                parts.append((value.dtype, value.dim() == 0))
+            else:
+                return None
+        try:
+            consts = tuple(_tagged(v) for v in constexprs.values())
+            opts = tuple(sorted((k, _tagged(v)) for k, v in call_options.items() if k not in LAUNCH_OPTIONS)) \
+                if call_options else ()
+            key = (tuple(parts), consts, opts)
+            hash(key)
+        except TypeError:
+            return None
+        return key
+
     def resolve(self, *args, **kwargs) -> Tuple[ResolvedKernel, Dict[str, Any], Dict[str, Any]]:
         """(cached specialisation, runtime args, constexprs) of one call, without launching."""
         if kwargs.get("always_compile", self.default_options.get("always_compile", False)):
@@ -259,21 +292,39 @@ class JITFunction:
             runtime_args, constexprs, _ = self.bind(*args, **kwargs)
             return ResolvedKernel(registry.lookup(self.fn_name, self.params), ""), runtime_args, constexprs
         runtime_args, constexprs, options = self._fast_bind(args, dict(kwargs))
+        quick = self._quick_key(runtime_args, constexprs,
+                                {k: v for k, v in kwargs.items() if k in options} if kwargs else {})
+        if quick is not None:
+            hit = self._quick_cache.get(quick)
+            if hit is not None:
+                return hit, runtime_args, constexprs
         arg_kinds = {name: self.arg_kind(value) for name, value in runtime_args.items()}
         key = get_mem_cache_key(self._gen_cache_factors(arg_kinds, constexprs, options))
         hit = self.kernel_cache.get(key)
         if hit is not None:
+            if quick is not None:
+                self._quick_cache[quick] = hit
             return hit, runtime_args, constexprs
         # miss: full validation (ConstExpr types, argument types), then the registry
         runtime_args, constexprs, _ = self.bind(*args, **kwargs)
         resolved = ResolvedKernel(registry.lookup(self.fn_name, self.params), key)
         self.kernel_cache[key] = resolved
+        if quick is not None:
+            self._quick_cache[quick] = resolved
         return resolved, runtime_args, constexprs
 
     def _run(self, *args, **kwargs) -> None:
         resolved, runtime_args, constexprs = self.resolve(*args, **kwargs)
         options = {**self.default_options, **{k: v for k, v in kwargs.items() if k in COMPILE_OPTIONS}}
         Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs, options)
+
+
+def _tagged(value: Any):
+    """Hashable, type-tagged form of a ConstExpr value or option (lists and tuples element-wise)."""
+    cls = value.__class__
+    if cls is list or cls is tuple:
+        return (cls, tuple(_tagged(v) for v in value))
+    return (cls, value)
 
 
 def jit(fn: Callable = None, **options):

@@ -51,11 +51,19 @@ def is_pointer_arg(value: Any) -> bool:
         return False
 
 
+_device_seen = False
+
+
 def require_device() -> None:
+    """Raises unless a HIP device is visible (checked until one is, then remembered)."""
+    global _device_seen
+    if _device_seen:
+        return
     import torch
     if not torch.cuda.is_available():
         raise RuntimeError("No HIP device is available: asc2 kernels run only on the MI355X (gfx950) device "
                            "through libasc_hip.so; there is no CPU fallback.")
+    _device_seen = True
 
 
 class Launcher:

@@ -380,3 +380,30 @@ def test_matmul_instances_per_kernel_type():
     assert _matmul_instances(call(kernel_type=config.KernelType.MIX_AIC_1_2)) == 24
     assert _matmul_instances(call(kernel_type=config.KernelType.AIC_ONLY)) == 12
     assert _matmul_instances(call(kernel_type=config.KernelType.MIX_AIC_1_1)) == 12
+
+
+def test_quick_key_keeps_cache_factors_apart(recorded):
+    # 1, True and 1.0 are equal in Python but distinct cache factors (their reprs differ);
+    # the quick key tags values with their types, so each gets its own specialisation
+    @asc2.jit
+    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                    tile_size: asc.ConstExpr, tile_per_block: asc.ConstExpr):
+        pass
+
+    import torch
+    for x in (np.zeros(8, np.float32), torch.zeros(8)):  # numpy takes the full path, torch the quick key
+        keys = set()
+        for tpb in (1, True, 1.0, 1, True):
+            resolved, _, consts = vadd_kernel.resolve(x, x, x, 8, 8, tpb)
+            keys.add(resolved.cache_key)
+            assert consts["tile_per_block"] == tpb and type(consts["tile_per_block"]) is type(tpb)
+        assert len(keys) == 3
+    t = torch.zeros(8)
+    assert vadd_kernel.resolve(t, t, t, 8, 8, 1)[0].cache_key != \
+        vadd_kernel.resolve(t.half(), t, t, 8, 8, 1)[0].cache_key
+    assert vadd_kernel.resolve(t, t, t, 8, 8, 1)[0].cache_key != \
+        vadd_kernel.resolve(t, t, t, torch.tensor(8), 8, 1)[0].cache_key
+    # a different dtype or a 0-dim tensor in a pointer slot is a different specialisation
+    a = vadd_kernel.resolve(x, x, x, 8, 8, 1)[0].cache_key
+    b = vadd_kernel.resolve(x.astype(np.float16), x, x, 8, 8, 1)[0].cache_key
+    assert a != b
