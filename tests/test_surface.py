@@ -403,7 +403,3 @@ def test_quick_key_keeps_cache_factors_apart(recorded):
         vadd_kernel.resolve(t.half(), t, t, 8, 8, 1)[0].cache_key
     assert vadd_kernel.resolve(t, t, t, 8, 8, 1)[0].cache_key != \
         vadd_kernel.resolve(t, t, t, torch.tensor(8), 8, 1)[0].cache_key
-    # a different dtype or a 0-dim tensor in a pointer slot is a different specialisation
-    a = vadd_kernel.resolve(x, x, x, 8, 8, 1)[0].cache_key
-    b = vadd_kernel.resolve(x.astype(np.float16), x, x, 8, 8, 1)[0].cache_key
-    assert a != b
