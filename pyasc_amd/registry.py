@@ -74,5 +74,5 @@ _loaded: Optional[bool] = None
 def _ensure_loaded() -> None:
     global _loaded
     if not _loaded:
-        from . import launchers  # noqa: F401  (registers the entries)
+        from . import launchers, launchers_asc1  # noqa: F401  (register the entries)
         _loaded = True

@@ -356,7 +356,7 @@ def test_compile_options_reach_the_launch(recorded):
 def test_block_ranges_match_oracle_coverage(n, grid, stride, cover):
     # the launchers' asc1 block ranges write exactly the elements the oracle's block_add writes
     from oracle import asc2_oracle as O
-    from pyasc_amd.launchers import _block_ranges
+    from pyasc_amd.launchers_asc1 import _block_ranges
     mask = np.zeros(n, bool)
     for s, e in _block_ranges(n, grid, stride, cover):
         assert 0 <= s < e <= n
@@ -369,7 +369,7 @@ def test_block_ranges_match_oracle_coverage(n, grid, stride, cover):
 def test_matmul_instances_per_kernel_type():
     # MIX_AIC_1_2 (the default for mixed Matmul kernels) runs two instances per block,
     # AIC_ONLY / matmul_cube_only and the other types one (python/asc/runtime/compiler.py:291-299)
-    from pyasc_amd.launchers import _matmul_instances
+    from pyasc_amd.launchers_asc1 import _matmul_instances
     from pyasc_amd.registry import KernelCall
     import asc.runtime.config as config
 
