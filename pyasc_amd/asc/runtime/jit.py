@@ -182,6 +182,7 @@ class JITFunction:
         runtime_args, constexprs = self.split_args(dict(call_args.arguments), _annotations(self.fn))
         for value in runtime_args.values():
             self.get_arg_type(value)
+        _check_compile_options(options)
         return runtime_args, constexprs, options
 
     # ------------------------------------------------------------------------------------ cache
@@ -317,6 +318,18 @@ class JITFunction:
         resolved, runtime_args, constexprs = self.resolve(*args, **kwargs)
         options = {**self.default_options, **{k: v for k, v in kwargs.items() if k in COMPILE_OPTIONS}}
         Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs, options)
+
+
+def _check_compile_options(options: Dict[str, Any]) -> None:
+    """The compiler's option check, run where the reference builds its Compiler (a cache miss
+    or always_compile; python/asc/runtime/compiler.py:137-141, 322-329): opt_level must be
+    1, 2 or 3 and kernel_type None or a config.KernelType.  The SoC-version part of that
+    check is about Ascend targets and has no counterpart here."""
+    from .config import KernelType
+    kernel_type = options.get("kernel_type")
+    if options.get("opt_level", 3) not in (1, 2, 3) or not (kernel_type is None or
+                                                         isinstance(kernel_type, KernelType)):
+        raise RuntimeError("Please check input compile option")
 
 
 def _tagged(value: Any):

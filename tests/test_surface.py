@@ -403,3 +403,24 @@ def test_quick_key_keeps_cache_factors_apart(recorded):
         vadd_kernel.resolve(t.half(), t, t, 8, 8, 1)[0].cache_key
     assert vadd_kernel.resolve(t, t, t, 8, 8, 1)[0].cache_key != \
         vadd_kernel.resolve(t, t, t, torch.tensor(8), 8, 1)[0].cache_key
+
+
+def test_invalid_compile_option(recorded):
+    # python/test/unit/runtime/test_compiler.py:89-92: opt_level 0 is rejected when the kernel
+    # is compiled; here, when the call is resolved without a cached specialisation
+    for bad in ({"opt_level": 0}, {"kernel_type": 3}):
+        @asc.jit(**bad)
+        def copy_kernel(x: asc.GlobalAddress, z: asc.GlobalAddress, data_size: asc.ConstExpr[int]):
+            pass
+
+        x = np.zeros(8, np.float32)
+        with pytest.raises(RuntimeError, match="Please check input compile option"):
+            copy_kernel[1](x, x, 8)
+    import asc.runtime.config as config
+
+    @asc.jit(opt_level=2, kernel_type=config.KernelType.AIV_ONLY)
+    def copy_kernel(x: asc.GlobalAddress, z: asc.GlobalAddress, data_size: asc.ConstExpr[int]):
+        pass
+
+    copy_kernel[1](np.zeros(8, np.float32), np.zeros(8, np.float32), 8)
+    assert recorded[-1][-1]["opt_level"] == 2
