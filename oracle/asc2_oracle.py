@@ -37,6 +37,8 @@ How each function is pinned (tests/test_oracle.py):
   broadcast_rows  torch.broadcast_to / reshape (test_shape_ops.py's goldens).
   block_add       the asc1 vadd test's golden (x + y, test_vadd.py:85-92) at its launch
                   parameters, a literal walk of the body's tile loop, hand-worked gaps.
+  unary (16-bit)  torch's float16 / bfloat16 ops (fp32 math, one rounding) within one ulp;
+                  the exact ops (abs, neg, floor, ceil, sqrt, relu) bit for bit.
   atomic tiles    the atomic test's golden (torch add / maximum / minimum folded over
                   the blocks, test_atomic_ops.py:62-67); closed forms: the column sum
                   plus n_tiles * addend (integers), the column max / min plus addend.
@@ -392,6 +394,13 @@ def unary_f32(x: np.ndarray, op: str) -> np.ndarray:
     rounded once to float32."""
     with np.errstate(all="ignore"):
         return _UNARY_F64[op](np.asarray(x, dtype=np.float32).astype(np.float64)).astype(np.float32)
+
+
+def unary(x: np.ndarray, op: str, dtype: str) -> np.ndarray:
+    """The same op on a float32 / float16 / bfloat16 tile: the 16-bit elements widen
+    exactly to float32, the op's float32 value (the exact value rounded to float32) is
+    rounded (RNE) to the element type (bfloat16 as uint16 bits)."""
+    return _from_f32(unary_f32(_to_f32(x, dtype), op), dtype)
 
 
 _INT_BITS = {"int32": 32, "int16": 16}

@@ -323,9 +323,10 @@ def _op_name(op, allowed, what: str) -> str:
 
 @register("kernel", ("x_ptr", "z_ptr", "block_length", "op"), "python/test/asc2/operations/test_unary_ops.py:35-40")
 def _unary(call: KernelCall) -> None:
+    # float32 as the reference test runs it; float16 / bfloat16 tiles as asc2 allows them
     n = int(call.consts["block_length"])
-    kernels.unary_f32(call.args["x_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1),
-                      _op_name(call.consts["op"], kernels.UNARY_OPS, "unary op"), n, call.stream)
+    kernels.unary(call.args["x_ptr"].reshape(-1), call.args["z_ptr"].reshape(-1),
+                  _op_name(call.consts["op"], kernels.UNARY_OPS, "unary op"), n, call.stream)
 
 
 @register("kernel", ("x_ptr", "y_ptr", "z_ptr", "block_length", "fmt", "op"),

@@ -504,3 +504,29 @@ def test_fill_vs_oracle(device, dtype, value):
     got = z.cpu()
     _assert_same(got[:-1], O.fill(z.numel() - 1, value, dtype), dtype)
     assert _np(got[-1:], dtype).view(np.uint8).sum() == 0
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("op", kernels.UNARY_OPS)
+def test_unary_16bit_vs_oracle(device, op, dtype):
+    # fp32 op on the widened element, one RNE rounding: within one ulp of the element type
+    # (the fp32 libm error can move a value across a rounding boundary), exact ops bit for bit
+    td = getattr(torch, dtype)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(N, generator=g) * 4
+    if op in ("log", "log2", "rsqrt", "sqrt"):
+        x = x.abs() + 1e-3
+    if op in ("cosh", "sinh", "exp", "exp2"):
+        x = x.clamp(-10, 10)
+    x = x.to(td)
+    out = torch.empty(N, dtype=td, device=device)
+    unary_kernel[1](x.to(device), out, N, getattr(asc2, op))
+    torch.cuda.synchronize()
+    expected = O.unary(_np(x, dtype), op, dtype)
+    got = _np(out.cpu(), dtype)
+    as_f = (lambda a: O.bf16_bits_to_f32(a)) if dtype == "bfloat16" else (lambda a: a.astype(np.float32))
+    if op in ("abs", "ceil", "floor", "negative", "relu", "sqrt"):
+        np.testing.assert_array_equal(got, expected)
+    else:
+        ulp = 2.0 ** -10 if dtype == "float16" else 2.0 ** -7
+        np.testing.assert_allclose(as_f(got), as_f(expected), rtol=ulp, atol=1e-6)

@@ -711,3 +711,24 @@ def test_quant_known_answers():
     np.testing.assert_array_equal(O.quant_i8(np.array([2.4], np.float16), 1.0, 0.1, "float16"), [2])
     bits = O.f32_to_bf16_bits(np.array([3.0, -3.0], np.float32))
     np.testing.assert_array_equal(O.quant_i8(bits, 0.5, 0.0, "bfloat16"), [2, -2])  # 1.5 -> 2, -1.5 -> -2
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("op", ["abs", "ceil", "cos", "exp", "floor", "log", "negative", "relu", "rsqrt", "sin",
+                                "sqrt", "tanh", "erf"])
+def test_unary_16bit_matches_torch(op, dtype):
+    td = getattr(torch, dtype)
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(20000, generator=g) * 3).to(td)
+    if op in ("log", "rsqrt", "sqrt"):
+        x = x.abs() + 0.01
+    fn = {"negative": torch.neg, "relu": torch.relu}.get(op, getattr(torch, op, None))
+    ref = fn(x).float().numpy()
+    host = x.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else x.numpy()
+    got = O.unary(host, op, dtype)
+    got = O.bf16_bits_to_f32(got) if dtype == "bfloat16" else got.astype(np.float32)
+    ulp = 2.0 ** -10 if dtype == "float16" else 2.0 ** -7
+    if op in ("abs", "ceil", "floor", "negative", "relu", "sqrt"):
+        np.testing.assert_array_equal(got, ref)
+    else:
+        np.testing.assert_allclose(got, ref, rtol=ulp, atol=1e-6)
