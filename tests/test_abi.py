@@ -38,6 +38,21 @@ def test_version_string():
     ("asc_softmax_rows_f32", (0, 0, 4, 8, 16, 1, None), _native.ERR_UNSUPPORTED),
     ("asc_softmax_rows_f32", (0, 0, 4, 8, 0, 1, None), _native.ERR_INVALID_ARG),
     ("asc_softmax_blocks_f32", (0, 0, 4, 8, 1, 0, None), _native.ERR_INVALID_ARG),
+    ("asc_unary", (18, 0, 1, 1, 8, None), _native.ERR_INVALID_ARG),           # unknown op
+    ("asc_unary", (0, 3, 1, 1, 8, None), _native.ERR_UNSUPPORTED),           # int32 elements
+    ("asc_unary", (0, 0, 0, 1, 8, None), _native.ERR_INVALID_ARG),           # null buffer
+    ("asc_binary", (6, 0, 1, 1, 1, 8, 1, 0.0, 1, None), _native.ERR_UNSUPPORTED),  # float shift
+    ("asc_binary", (6, 3, 1, 1, 1, 8, 1, 0.0, 32, None), _native.ERR_INVALID_ARG),  # shift >= 32
+    ("asc_axpy", (3, 1, 1, 2.0, 8, None), _native.ERR_UNSUPPORTED),
+    ("asc_axpy", (0, 1, 1, 2.0, -1, None), _native.ERR_INVALID_ARG),
+    ("asc_transpose_batched", (2, 1, 1, 1, 16, 16, None), _native.ERR_INVALID_ARG),  # x aliases z
+    ("asc_transpose_batched", (8, 1, 2, 1, 16, 16, None), _native.ERR_UNSUPPORTED),
+    ("asc_quant_i8", (3, 1, 1, 2.0, 0.9, 8, None), _native.ERR_UNSUPPORTED),
+    ("asc_atomic_tiles", (1, 0, 1, 1, 4, 8, 0.0, 0, None), _native.ERR_INVALID_ARG),  # sub is not atomic
+    ("asc_atomic_tiles", (0, 0, 0, 1, 4, 8, 0.0, 0, None), _native.ERR_INVALID_ARG),  # null x
+    ("asc_fill", (0, 0, 8, 1.0, 0, None), _native.ERR_INVALID_ARG),
+    ("asc_rect_binary", (0, 0, 1, 1, 1, 8, 8, -1, 0, 2, 2, None), _native.ERR_INVALID_ARG),
+    ("asc_broadcast_rows", (3, 1, 1, 2, 2, None), _native.ERR_UNSUPPORTED),
 ])
 def test_argument_errors_are_reported(fn, args, code):
     lib = _native.load_library()
@@ -50,5 +65,12 @@ def test_argument_errors_are_reported(fn, args, code):
 
 def test_zero_sized_launch_is_a_noop():
     lib = _native.load_library()
+    # empty work returns before any launch, null buffers included
+    assert lib.asc_unary(0, 0, None, None, 0, None) == 0
+    assert lib.asc_axpy(0, None, None, 2.0, 0, None) == 0
+    assert lib.asc_fill(0, None, 0, 1.0, 0, None) == 0
+    assert lib.asc_atomic_tiles(0, 0, None, None, 0, 8, 0.0, 0, None) == 0
+    assert lib.asc_transpose_batched(2, None, None, 0, 16, 16, None) == 0
+    assert lib.asc_rect_binary(0, 0, None, None, None, 8, 8, 8, 0, 2, 2, None) == 0  # clipped to nothing
     assert lib.asc_vadd(0, None, None, None, 0, 128, 4, 16, None) == 0
     assert lib.asc_vadd(0, None, None, None, 100, 128, 0, 16, None) == 0  # tile_per_block 0 covers nothing
