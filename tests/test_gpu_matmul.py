@@ -142,3 +142,18 @@ def test_f32_inputs_epilogues_vs_fp64(device, out_dtype, act, M, N, K):
     bound = K * 2.0 ** -24 * (a.double().abs() @ b.double().abs()) + ref.abs() * {
         torch.float32: 0.0, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[out_dtype] + 1e-6
     assert bool(((c.cpu().double() - ref).abs() <= bound).all())
+
+
+def test_direct_path_repeat_runs_are_bit_identical(device):
+    # the direct-to-LDS loop orders its DMA and operand reads with waits and barriers only;
+    # repeated runs must agree bit for bit (a stage race would show here)
+    g = torch.Generator().manual_seed(12)
+    a = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16).to(device)
+    b = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16).to(device)
+    outs = []
+    for _ in range(3):
+        c = torch.empty(4096, 4096, dtype=torch.bfloat16, device=device)
+        kernels.matmul(a, b, c)
+        outs.append(c)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
