@@ -40,12 +40,15 @@ def dequant(acc: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return (acc.float() * scale).half()
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float, causal: bool) -> torch.Tensor:
-    """One (batch, head) slice [S, D] in fp32."""
-    s = (q.float() @ k.float().T) * sm_scale
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float, causal: bool,
+              rows: torch.Tensor | None = None) -> torch.Tensor:
+    """One (batch, head) slice [S, D] in fp32; with ``rows`` (query indices) only those
+    output rows, each with the same keys and causal mask as in the full computation."""
+    qr = q if rows is None else q[rows]
+    s = (qr.float() @ k.float().T) * sm_scale
     if causal:
-        n = s.shape[0]
-        s = s.masked_fill(torch.ones(n, s.shape[1], dtype=torch.bool).triu(1), float("-inf"))
+        qi = torch.arange(q.shape[0]) if rows is None else rows
+        s = s.masked_fill(torch.arange(k.shape[0])[None, :] > qi[:, None], float("-inf"))
     return torch.softmax(s, dim=-1) @ v.float()
 
 

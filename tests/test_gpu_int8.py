@@ -84,3 +84,8 @@ def test_config_shape_full(device):
     assert torch.equal(acc[rows.to(device)].cpu(), exact)
     acc_h = acc.cpu()
     np.testing.assert_array_equal(_f16_bits(out), O.dequant_f16(acc_h.numpy(), scale.numpy()).view(np.uint16))
+    # whole-matrix checksums, exact in int64 (linearity): C 1 = A (B 1) and 1^T C = (1^T A) B,
+    # so every accumulator of every tile enters an exact comparison
+    a64, b64, acc64 = a.numpy().astype(np.int64), b.numpy().astype(np.int64), acc_h.numpy().astype(np.int64)
+    np.testing.assert_array_equal(acc64.sum(axis=1), a64 @ b64.sum(axis=1))
+    np.testing.assert_array_equal(acc64.sum(axis=0), a64.sum(axis=0) @ b64)

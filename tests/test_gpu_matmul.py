@@ -87,9 +87,10 @@ def test_strided_views(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_config_8192_sampled_rows(device, dtype):
-    """BASELINE config: M=N=K=8192, randn/sqrt(K) inputs from seed 2; every column of
-    128 sampled rows is checked against the fp32 CPU product."""
+def test_config_8192_full(device, dtype):
+    """BASELINE config: M=N=K=8192, randn/sqrt(K) inputs from seed 2; all of C is checked
+    against the fp32 CPU product (python/test/asc2/kernels/test_matmul_tiled.py:49's golden)
+    rounded to the output dtype."""
     n = 8192
     g = torch.Generator().manual_seed(2)
     a = (torch.randn(n, n, generator=g) / np.sqrt(n)).to(dtype)
@@ -97,10 +98,8 @@ def test_config_8192_sampled_rows(device, dtype):
     c = torch.empty(n, n, dtype=dtype, device=device)
     kernels.matmul(a.to(device), b.to(device), c)
     torch.cuda.synchronize()
-    rows = torch.randperm(n, generator=torch.Generator().manual_seed(9))[:128]
-    ref = a[rows].float() @ b.float()
-    torch.testing.assert_close(c[rows.to(device)].cpu().float(), ref.to(dtype).float(), atol=TOL, rtol=TOL)
-    assert torch.isfinite(c).all()
+    ref = a.float() @ b.float()
+    torch.testing.assert_close(c.cpu().float(), ref.to(dtype).float(), atol=TOL, rtol=TOL)
 
 
 # fp32 inputs: the MFMA kernel up to 4096 output tiles of 32x32, the LDS FMA kernel beyond
