@@ -47,6 +47,7 @@ struct FaArgs {
   int64_t heads_total;  // batch * heads
   int seq;
   int n_qblocks;
+  int head_group;  // heads whose query blocks an XCD interleaves (see the block order)
   float scale_log2;  // sm_scale * log2(e)
   int causal;
 };
@@ -389,18 +390,30 @@ __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs 
 
   // Block order.  Workgroup b runs on XCD b % 8, and each XCD starts its
   // workgroups in order of b / 8.  When the (batch, head) count divides by 8,
-  // XCD x takes heads x, x+8, x+16, ... and runs all query blocks of one head
-  // back to back, so the workgroups resident on an XCD at once stream the same
-  // head's K/V through that XCD's L2 (fetched from HBM about once per head,
-  // instead of once per round of resident query blocks).  Otherwise: query-block
-  // major.  Causal runs a head's heavy (late) query blocks first.
+  // XCD x takes heads x, x+8, x+16, ... in groups of head_group heads and runs
+  // the query blocks of one group back to back, interleaving the group's heads
+  // block by block.  The workgroups resident on an XCD at once then stream the
+  // same few heads' K/V through that XCD's L2 (fetched from HBM about once per
+  // head, instead of once per round of resident query blocks).  Non-causal
+  // blocks are all alike and use groups of one head.  Causal blocks run heavy
+  // (late) query blocks first, and the host sizes the group so that one group's
+  // blocks fill the workgroup slots of the XCD twice over: the heaviest blocks of
+  // a group then start together and the lightest end the XCD's run, instead of
+  // the last head's heavy blocks starting behind the previous head's light ones.
+  // Otherwise: query-block major (heavy first over all heads when causal).
   const int64_t bid = blockIdx.x;
   int64_t bh;
   int qb;
   if (p.heads_total % 8 == 0) {
-    const int64_t slot = bid >> 3;
-    bh = (bid & 7) + 8 * (slot / p.n_qblocks);
-    qb = static_cast<int>(slot % p.n_qblocks);
+    const int64_t slot = bid >> 3;  // < heads_total / 8 * n_qblocks
+    const int64_t per_group = static_cast<int64_t>(p.head_group) * p.n_qblocks;
+    const int64_t grp = slot / per_group;
+    const int64_t r = slot - grp * per_group;
+    const int64_t g0 = grp * p.head_group;
+    const int64_t heads_left = (p.heads_total >> 3) - g0;  // >= 1; the last group may be partial
+    const int64_t gsz = heads_left < p.head_group ? heads_left : p.head_group;
+    bh = (bid & 7) + 8 * (g0 + r % gsz);
+    qb = static_cast<int>(r / gsz);
   } else {
     bh = bid % p.heads_total;
     qb = static_cast<int>(bid / p.heads_total);
@@ -511,6 +524,24 @@ template <int D, int kWaves>
 int32_t launch(FaArgs p, hipStream_t stream) {
   constexpr int BQ = 32 * kWaves;
   p.n_qblocks = static_cast<int>((p.seq + BQ - 1) / BQ);
+  p.head_group = 1;
+  if (p.causal) {
+    // workgroup slots of one XCD: its CUs x resident workgroups per CU
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) {
+      return asc::set_error(static_cast<int32_t>(e), "asc_flash_attention_fwd_bf16: cannot read the CU count: %s",
+                            hipGetErrorString(e));
+    }
+    // Twice the smallest group that fills them: at the bench shape (64 slots, 32
+    // blocks per head) groups of 1, 2, 4, 8, 16 heads measured 582-621, 569-591,
+    // 564-575, 572-578 and 581-586 us.
+    const int64_t slots = static_cast<int64_t>(cus) / 8 * (8 / kWaves);
+    const int64_t g = 2 * ((slots + p.n_qblocks - 1) / p.n_qblocks);
+    const int64_t heads_xcd = p.heads_total / 8;
+    p.head_group = static_cast<int>(g < 1 ? 1 : (g > heads_xcd && heads_xcd > 0 ? heads_xcd : g));
+  }
   const int64_t blocks = p.heads_total * p.n_qblocks;
   hipLaunchKernelGGL((fa_fwd_kernel<D, kWaves>), dim3(static_cast<uint32_t>(blocks)), dim3(kWaves * 64), 0, stream,
                      p);

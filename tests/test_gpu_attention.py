@@ -120,6 +120,21 @@ def test_xcd_block_order_all_heads(device, D, causal):
             torch.testing.assert_close(out[b, hh].float(), ref, atol=TOL, rtol=TOL)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_causal_head_groups_with_partial_last_group(device, D):
+    # causal blocks are interleaved over groups of heads per XCD; with 256 CUs and S = 2900
+    # (23 query blocks of 128) a group holds 2 * ceil(64 / 23) = 6 heads, so the 7 heads of
+    # each XCD (B * H = 56) form one full group and a partial group of one head
+    B, H, S = 7, 8, 2900
+    q, k, v = _qkv(B, H, S, D, 5 + D)
+    scale = 1 / math.sqrt(D)
+    out, _ = _run(q, k, v, scale, True, device)
+    for b in range(B):
+        for hh in range(H):
+            ref = cpu_golden.attention(q[b, hh], k[b, hh], v[b, hh], scale, True)
+            torch.testing.assert_close(out[b, hh].float(), ref, atol=TOL, rtol=TOL)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_repeat_runs_are_bit_identical(device, causal):
     # the kernel has no atomics or data-dependent scheduling: any difference between two
