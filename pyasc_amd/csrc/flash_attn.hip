@@ -5,8 +5,7 @@
 //
 // Design (gfx950, wave64, MFMA 32x32x16 bf16):
 //  - A wave owns 32 queries of one (batch, head); a workgroup has 4 waves
-//    (128 queries; causal and head_dim 64) or 8 waves (256 queries; non-causal
-//    head_dim 128).  Keys/values stream through LDS in tiles of 64,
+//    (128 queries; head_dim 64) or 8 waves (256 queries; head_dim 128).  Keys/values stream through LDS in tiles of 64,
 //    double-buffered.
 //  - Each wave computes S^T = K Q^T (keys x queries) instead of S = Q K^T:
 //    in the MFMA result layout a lane then holds ONE query column and 16 keys
@@ -359,8 +358,8 @@ __device__ __forceinline__ void fa_step(FaState<D, kWaves>& st, int j, int n_til
 // each K/V tile streamed once for twice the queries (half the DMA per query);
 // the two waves of a SIMD belong to one workgroup and would run their exp2 and
 // MFMA phases in lockstep, so waves 0-3 run at raised priority and their SIMD
-// partners fill in behind them (non-causal +3.6% over kWaves = 4; causal is
-// better with the finer 128-query blocks).
+// partners fill in behind them (non-causal +3.6% over kWaves = 4; causal with
+// the grouped block order 1.5-2% faster than with 128-query blocks).
 template <int D, int kWaves>
 __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs p) {
   using St = FaState<D, kWaves>;
@@ -579,5 +578,5 @@ extern "C" int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k, co
   p.causal = causal ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (head_dim == 64) return launch<64, 4>(p, s);
-  return p.causal ? launch<128, 4>(p, s) : launch<128, 8>(p, s);
+  return launch<128, 8>(p, s);
 }

@@ -122,9 +122,10 @@ def test_xcd_block_order_all_heads(device, D, causal):
 
 @pytest.mark.parametrize("D", [64, 128])
 def test_causal_head_groups_with_partial_last_group(device, D):
-    # causal blocks are interleaved over groups of heads per XCD; with 256 CUs and S = 2900
-    # (23 query blocks of 128) a group holds 2 * ceil(64 / 23) = 6 heads, so the 7 heads of
-    # each XCD (B * H = 56) form one full group and a partial group of one head
+    # causal blocks are interleaved over groups of heads per XCD; with 256 CUs and S = 2900 a
+    # group holds 6 heads (D = 128: 12 query blocks of 256, 32 slots, 2 * ceil(32 / 12);
+    # D = 64: 23 blocks of 128, 64 slots, 2 * ceil(64 / 23)), so the 7 heads of each XCD
+    # (B * H = 56) form one full group and a partial group of one head
     B, H, S = 7, 8, 2900
     q, k, v = _qkv(B, H, S, D, 5 + D)
     scale = 1 / math.sqrt(D)
