@@ -82,6 +82,15 @@ int32_t asc_vadd(int32_t dtype, const void* x, const void* y, void* out,
                  int64_t size, int32_t tile_size, int32_t tile_per_block,
                  int32_t grid, asc_stream_t stream);
 
+/* ---- plain copy (bandwidth reference) --------------------------------------
+ * dst[0, n_bytes) = src[0, n_bytes) with the streaming shape of the vadd kernel
+ * (non-temporal 16-byte vectors, four per thread in flight).  It has no
+ * counterpart among the reference's asc2 kernels: it is the copy that bounds
+ * every HBM-streaming kernel here, measured beside them by the bench.  Buffers
+ * and n_bytes must be multiples of 16 bytes (ASC_ERR_ALIGNMENT otherwise). */
+int32_t asc_copy_bytes(const void* src, void* dst, int64_t n_bytes,
+                       asc_stream_t stream);
+
 /* ---- leaky_relu / vmuladd ------------------------------------------------------
  * asc2 leaky_relu_kernel(x_ptr, alpha: float, out_ptr, size: int,
  *                        tile_size: ConstExpr[int], tile_per_block: ConstExpr[int])

@@ -1,0 +1,265 @@
+"""Summarises rocprofv3 output of bench.py runs into profiles/ (no GPU needed).
+
+    python profile_summary.py traffic DIR   # FETCH_SIZE / WRITE_SIZE passes -> profiles/traffic.json + hbm_traffic.md
+    python profile_summary.py mfma DIR      # MFMA-busy / clock passes -> profiles/mfma_counters.md
+
+DIR holds one rocprofv3 output folder per pass, written with ``-f csv -o run`` by
+the commands the summaries print:
+
+  traffic: DIR/<workload>_FETCH_SIZE and DIR/<workload>_WRITE_SIZE, from
+      rocprofv3 --pmc FETCH_SIZE -f csv -d DIR/<workload>_FETCH_SIZE -o run -- \
+          python3 bench.py --workload <workload> --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration
+  mfma: DIR/<workload>_MFMA, from
+      rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv \
+          -d DIR/<workload>_MFMA -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --steps 5 \
+          --warmup 1
+
+FETCH_SIZE and WRITE_SIZE are KiB per dispatch past the L2.  ``--copy-calibration``
+adds five torch device copies of exactly 256 MiB; their readings give the factor that
+turns each counter into bytes (factor = 262144 KiB / reading).
+"""
+from __future__ import annotations
+
+import collections
+import csv
+import glob
+import json
+import os
+import sys
+
+import bench
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PROFILES = os.path.join(REPO, "profiles")
+COPY_KIB = 262144.0
+SIMDS_PER_CU = 4
+
+
+def _rows(folder: str):
+    files = glob.glob(os.path.join(folder, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {folder}")
+    for path in files:
+        with open(path, newline="") as f:
+            yield from csv.DictReader(f)
+
+
+def _short(kernel: str) -> str:
+    name = kernel.replace("void (anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    depth, out = 0, []
+    for ch in name:  # keep the template arguments, drop the parameter list
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            break
+        out.append(ch)
+    return "".join(out).strip()
+
+
+def _is_library_kernel(kernel: str) -> bool:
+    return "at::native" not in kernel and not kernel.startswith("__amd") and "elementwise_kernel" not in kernel
+
+
+def _per_kernel(folder: str, counter: str):
+    """counter values per dispatch, keyed by kernel name."""
+    vals = collections.defaultdict(list)
+    for r in _rows(folder):
+        if r["Counter_Name"] == counter:
+            vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return vals
+
+
+def traffic(folder: str) -> int:
+    path = os.path.join(PROFILES, "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        table = {}
+    table.setdefault("workloads", {})
+    table["format"] = ("bytes per launch past the L2 (FETCH_SIZE + WRITE_SIZE, KiB per dispatch, each scaled by "
+                       "the reading of a 256 MiB device copy), stamped with the hash of the kernel sources")
+    for key, make in bench.WORKLOADS.items():
+        fetch_dir = os.path.join(folder, f"{key}_FETCH_SIZE")
+        write_dir = os.path.join(folder, f"{key}_WRITE_SIZE")
+        if not (os.path.isdir(fetch_dir) and os.path.isdir(write_dir)):
+            continue
+        w = make()
+        row = {}
+        for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+            vals = _per_kernel(d, counter)
+            # the calibration copies run as the runtime's blit kernel (__amd_rocclr_copyBuffer)
+            copy = [v for k, v in vals.items() if "copyBuffer" in k]
+            if len(copy) != 1:
+                raise RuntimeError(f"{d}: no calibration copy dispatches (run with --copy-calibration)")
+            lib = {k: v for k, v in vals.items() if _is_library_kernel(k) and w.kernel_hint in k}
+            if len(lib) != 1:
+                raise RuntimeError(f"{d}: expected one library kernel matching {w.kernel_hint!r}, got {list(lib)}")
+            (kname, kvals), = lib.items()
+            row["kernel"] = _short(kname)
+            row[counter.lower() + "_kib"] = round(sum(kvals) / len(kvals), 1)
+            row["copy_" + counter.lower() + "_kib"] = round(sum(copy[0]) / len(copy[0]), 1)
+        ff = COPY_KIB / row["copy_fetch_size_kib"]
+        wf = COPY_KIB / row["copy_write_size_kib"]
+        row.update({"fetch_factor": round(ff, 3), "write_factor": round(wf, 3),
+                    "bytes": int(round((row["fetch_size_kib"] * ff + row["write_size_kib"] * wf) * 1024)),
+                    "algorithmic_bytes": int(_algorithmic_bytes(w)),
+                    "sources_hash": bench.sources_hash(w.sources)})
+        table["workloads"][w.name] = row
+        print(f"{w.name}: {row['kernel']} {row['bytes'] / 1e6:.1f} MB "
+              f"({row['bytes'] / row['algorithmic_bytes']:.2f}x algorithmic)")
+    table["workloads"] = dict(sorted(table["workloads"].items()))
+    with open(path, "w") as f:
+        json.dump(table, f, indent=1)
+        f.write("\n")
+    _write_traffic_md(table)
+    return 0
+
+
+def _algorithmic_bytes(w) -> float:
+    """Minimum HBM bytes of one launch: every operand read once, every result written once."""
+    if w.bound in ("hbm", "latency"):
+        return w.work()
+    if isinstance(w, bench.Matmul):
+        return w.n * w.n * (2 + 2 + (4 if w.bias_leaky else 2)) + (4 * w.n if w.bias_leaky else 0)
+    if isinstance(w, bench.MatmulI8):
+        return w.M * w.K + w.K * w.N + 2 * w.M * w.N + 4 * w.N
+    if isinstance(w, bench.FlashAttention):
+        return 4 * 2 * w.B * w.H * w.S * w.D
+    raise TypeError(type(w).__name__)
+
+
+def _write_traffic_md(table: dict) -> None:
+    lines = [
+        "# HBM traffic per launch (rocprofv3 PMC), one MI355X", "",
+        "Generated by `python profile_summary.py traffic DIR` from two rocprofv3 passes per workload "
+        "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
+        "```",
+        "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc/${W}_FETCH_SIZE -o run -- python3 bench.py "
+        "--workload $W --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration",
+        "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc/${W}_WRITE_SIZE -o run -- python3 bench.py "
+        "--workload $W --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration",
+        "```", "",
+        "`FETCH_SIZE` and `WRITE_SIZE` count the bytes that pass the L2 (misses and write-backs, including "
+        "those the 256 MiB MALL then serves), so for kernels with operand reuse (the GEMMs) they bound HBM "
+        "traffic from above; for streaming kernels they equal it.  `--copy-calibration` adds five device "
+        "copies of exactly 256 MiB (read 262144 KiB, written 262144 KiB); factor = 262144 / the copy's "
+        "reading.  Values are KiB per dispatch, averaged over the library kernel's dispatches.  Each row "
+        "is stamped with the hash of the kernel sources it was measured on; bench.py reports "
+        "`roofline.traffic` only while the sources still match.", "",
+        "| Workload | Kernel | FETCH KiB | WRITE KiB | fetch factor | write factor | traffic MB | algorithmic MB "
+        "| ratio | sources |",
+        "|---|---|---:|---:|---:|---:|---:|---:|---:|---|",
+    ]
+    for name, r in table["workloads"].items():
+        lines.append(f"| `{name}` | `{r['kernel']}` | {r['fetch_size_kib']:.0f} | {r['write_size_kib']:.0f} | "
+                     f"{r['fetch_factor']:.3f} | {r['write_factor']:.3f} | {r['bytes'] / 1e6:.1f} | "
+                     f"{r['algorithmic_bytes'] / 1e6:.1f} | {r['bytes'] / r['algorithmic_bytes']:.2f} | "
+                     f"`{r['sources_hash']}` |")
+    with open(os.path.join(PROFILES, "hbm_traffic.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def mfma(folder: str) -> int:
+    """MFMA utilisation and clock of the MFMA kernels from one counter pass each.
+
+    SQ_VALU_MFMA_BUSY_CYCLES is summed over every SIMD; GRBM_GUI_ACTIVE is summed over
+    the XCDs (each counts the GPU-active cycles of its own clock).  So
+      cycles per XCD   = GRBM_GUI_ACTIVE / XCDs
+      clock            = cycles per XCD / kernel duration
+      MFMA busy        = SQ_VALU_MFMA_BUSY_CYCLES / (cycles per XCD x CUs x 4 SIMDs)
+    and the achieved rate at 100 % busy is the MFMA peak scaled by clock / 2.4 GHz."""
+    info = bench_device_info(folder)
+    lines = [
+        "# MFMA utilisation and shader clock (rocprofv3 PMC), one MI355X", "",
+        "Generated by `python profile_summary.py mfma DIR` from one counter pass per workload "
+        "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
+        "```",
+        "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv "
+        "-d gpurun_out/pmc/${W}_MFMA -o run -- python3 bench.py --workload $W --no-suite --no-cpu --steps 5 "
+        "--warmup 1",
+        "```", "",
+        f"Device: {info}.  `SQ_VALU_MFMA_BUSY_CYCLES` is summed over all SIMDs; `GRBM_GUI_ACTIVE` over the "
+        "XCDs, so cycles per XCD = GRBM_GUI_ACTIVE / XCDs.  clock = cycles per XCD / dispatch duration "
+        "(Start/End timestamps of the counter pass); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (cycles per XCD "
+        "x CUs x 4).  A `v_mfma_f32_32x32x16_bf16` (or `_i32_32x32x32_i8`) keeps a SIMD's MFMA unit busy 32 "
+        "cycles (8 passes of 4), so 100 % busy is the dense peak at that clock: peak x clock / 2.4 GHz.  "
+        "Durations here are under counter collection (serialised dispatches) and are a few percent above "
+        "the unprofiled bench times.", "",
+        "| Workload | Kernel | dispatches | duration us | clock GHz | MFMA busy % | CU busy % | "
+        "peak at this clock | achieved (bench FLOP / duration) | achieved / peak at this clock |",
+        "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    cus, xcds = info_cus(folder), 8
+    for key, make in bench.WORKLOADS.items():
+        d = os.path.join(folder, f"{key}_MFMA")
+        if not os.path.isdir(d):
+            continue
+        w = make()
+        per = collections.defaultdict(dict)
+        for r in _rows(d):
+            if not (_is_library_kernel(r["Kernel_Name"]) and w.kernel_hint in r["Kernel_Name"]):
+                continue
+            e = per[r["Dispatch_Id"]]
+            e["kernel"] = _short(r["Kernel_Name"])
+            e[r["Counter_Name"]] = float(r["Counter_Value"])
+            e["dur"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
+        disp = [e for e in per.values() if "SQ_VALU_MFMA_BUSY_CYCLES" in e and "GRBM_GUI_ACTIVE" in e]
+        if not disp:
+            raise RuntimeError(f"{d}: no dispatch of a kernel matching {w.kernel_hint!r}")
+        n = len(disp)
+        dur = sum(e["dur"] for e in disp) / n
+        gui = sum(e["GRBM_GUI_ACTIVE"] for e in disp) / n / xcds
+        busy = sum(e["SQ_VALU_MFMA_BUSY_CYCLES"] for e in disp) / n
+        cu_busy = sum(e.get("SQ_BUSY_CU_CYCLES", 0.0) for e in disp) / n
+        clock = gui / dur / 1e9
+        util = busy / (gui * cus * SIMDS_PER_CU)
+        peak_at_clock = w.peak * clock / 2.4
+        achieved = w.work() / dur / 1e12
+        lines.append(f"| `{w.name}` | `{disp[0]['kernel']}` | {n} | {dur * 1e6:.1f} | {clock:.3f} | "
+                     f"{100 * util:.1f} | {100 * cu_busy / (gui * cus):.1f} | {peak_at_clock:.0f} {w.unit} | "
+                     f"{achieved:.0f} {w.unit} | {achieved / peak_at_clock:.3f} |")
+        print(lines[-1])
+    with open(os.path.join(PROFILES, "mfma_counters.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    return 0
+
+
+def _agent_rows(folder: str):
+    for path in glob.glob(os.path.join(folder, "**", "*agent_info.csv"), recursive=True):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r.get("Agent_Type", r.get("Type", "")).upper().endswith("GPU") or "gfx" in json.dumps(r):
+                    return r
+    return {}
+
+
+def info_cus(folder: str) -> int:
+    for d in glob.glob(os.path.join(folder, "*")):
+        r = _agent_rows(d)
+        for key in ("Cu_Count", "CU_Count", "Compute_Unit_Count", "Cu_Count_Per_Xcc"):
+            if r.get(key):
+                v = int(r[key])
+                return v * 8 if key.endswith("Per_Xcc") else v
+    return 256
+
+
+def bench_device_info(folder: str) -> str:
+    for d in glob.glob(os.path.join(folder, "*")):
+        r = _agent_rows(d)
+        if r:
+            return f"{r.get('Name', r.get('Gfx_Target_Version', 'gfx950'))}, {info_cus(folder)} CUs, 8 XCDs"
+    return "gfx950, 256 CUs, 8 XCDs"
+
+
+def main(argv) -> int:
+    if len(argv) != 3 or argv[1] not in ("traffic", "mfma"):
+        print(__doc__, file=sys.stderr)
+        return 2
+    return {"traffic": traffic, "mfma": mfma}[argv[1]](argv[2])
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv))

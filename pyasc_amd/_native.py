@@ -39,6 +39,7 @@ SIGNATURES = {
                         ctypes.c_char_p],
     "asc_stream_synchronize": [_c_p],
     "asc_vadd": [_c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
+    "asc_copy_bytes": [_c_p, _c_p, _c_i64, _c_p],
     "asc_leaky_relu": [_c_i32, _c_p, _c_f32, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
     "asc_vmuladd": [_c_i32, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
     "asc_gelu_rows_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],

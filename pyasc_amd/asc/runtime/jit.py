@@ -11,9 +11,10 @@ Follows python/asc/runtime/jit.py:33-223 in its user-visible behaviour:
   - runtime argument types are classified as in jit.py:69-96 (TypeError for
     unsupported ones).
 Instead of compiling the body, the (name, parameter names) pair selects a
-registered native kernel (pyasc_amd.registry).  What a call resolves to is cached
-per JITFunction under the reference's cache factors (jit.py:139-186; see
-cache.py): a hit skips annotation evaluation, ConstExpr validation, argument
+registered native kernel (pyasc_amd.registry), provided the body is one that
+kernel implements (its fingerprint, pyasc_amd.fingerprint) or a declaration.
+What a call resolves to is cached per JITFunction under the reference's cache
+factors (jit.py:139-186; see cache.py): a hit skips annotation evaluation, ConstExpr validation, argument
 classification and the registry lookup.  ``always_compile=True`` bypasses the
 cache, as it bypasses the reference's.
 """
@@ -27,7 +28,7 @@ from typing import Any, Callable, Dict, FrozenSet, List, Optional, Tuple, Union,
 
 import numpy as np
 
-from ... import registry
+from ... import fingerprint, registry
 from ..core import ConstExpr, DataType, require_constexpr
 from .cache import get_mem_cache_key
 from .launcher import LaunchOptions, Launcher
@@ -39,6 +40,9 @@ COMPILE_OPTIONS = ("debug", "strip_loc", "verify_sync", "print_ir_before_all", "
                    "reuse_ub_in_out", "static_alloc", "vf_fusion")
 LAUNCH_OPTIONS = ("core_num", "stream")
 _CONFIG_KEYWORDS = frozenset(CODEGEN_OPTIONS + COMPILE_OPTIONS + LAUNCH_OPTIONS)
+
+
+_UNSET = object()
 
 
 class ArgType:
@@ -101,6 +105,7 @@ class JITFunction:
         self._quick_cache: Dict[tuple, ResolvedKernel] = {}
         self._const_names: Optional[FrozenSet[str]] = None  # ConstExpr parameters, from the annotations
         self._hash: Optional[str] = None
+        self._fingerprint: Any = _UNSET
         # plain positional calls can skip inspect.Signature.bind
         self._positional_only_call = all(
             p.kind in (inspect.Parameter.POSITIONAL_ONLY, inspect.Parameter.POSITIONAL_OR_KEYWORD)
@@ -199,6 +204,14 @@ class JITFunction:
             self._hash = hashlib.sha256(f"{self.fn.__module__}.{self.fn.__qualname__}\n{src}".encode()).hexdigest()
         return self._hash
 
+    @property
+    def body_fingerprint(self) -> Optional[str]:
+        """Fingerprint of the decorated body (pyasc_amd.fingerprint): the registry runs
+        the native kernel only for a body it implements, or for a declaration body."""
+        if self._fingerprint is _UNSET:
+            self._fingerprint = fingerprint.fingerprint_of(self.fn)
+        return self._fingerprint
+
     @staticmethod
     def arg_kind(value: Any) -> str:
         """``kind:dtype`` of a runtime argument, the reference's per-argument cache factor
@@ -291,7 +304,8 @@ class JITFunction:
         if kwargs.get("always_compile", self.default_options.get("always_compile", False)):
             # no lookup and no store (jit.py:164-186): resolve from scratch
             runtime_args, constexprs, _ = self.bind(*args, **kwargs)
-            return ResolvedKernel(registry.lookup(self.fn_name, self.params), ""), runtime_args, constexprs
+            return ResolvedKernel(registry.lookup(self.fn_name, self.params, self.body_fingerprint), ""), \
+                runtime_args, constexprs
         runtime_args, constexprs, options = self._fast_bind(args, dict(kwargs))
         quick = self._quick_key(runtime_args, constexprs,
                                 {k: v for k, v in kwargs.items() if k in options} if kwargs else {})
@@ -308,7 +322,7 @@ class JITFunction:
             return hit, runtime_args, constexprs
         # miss: full validation (ConstExpr types, argument types), then the registry
         runtime_args, constexprs, _ = self.bind(*args, **kwargs)
-        resolved = ResolvedKernel(registry.lookup(self.fn_name, self.params), key)
+        resolved = ResolvedKernel(registry.lookup(self.fn_name, self.params, self.body_fingerprint), key)
         self.kernel_cache[key] = resolved
         if quick is not None:
             self._quick_cache[quick] = resolved

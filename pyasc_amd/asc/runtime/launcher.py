@@ -9,7 +9,9 @@ Mirrors python/asc/runtime/launcher.py:
   - Host buffers (CPU torch tensors, numpy arrays) are copied to the device, the
     kernel runs, the stream is synchronised and every pointer argument is copied
     back (launcher.py:176-195).  ROCm torch tensors are passed zero-copy and the
-    launch stays asynchronous on the chosen stream.
+    launch stays asynchronous on the chosen stream; they must be contiguous
+    (a strided device view raises ValueError instead of being written through
+    a temporary copy).
 """
 from __future__ import annotations
 
@@ -66,6 +68,16 @@ def require_device() -> None:
     _device_seen = True
 
 
+def require_contiguous(name: str, value: Any) -> Any:
+    """A device tensor is passed by its address (zero-copy): the kernel sees contiguous
+    memory from data_ptr(), so any other layout is refused rather than written through
+    a temporary copy the caller never sees."""
+    if not value.is_contiguous():
+        raise ValueError(f"argument '{name}' is a non-contiguous device tensor (shape {tuple(value.shape)}, "
+                         f"stride {tuple(value.stride())}); pass a contiguous tensor")
+    return value
+
+
 class Launcher:
 
     def __init__(self, options: LaunchOptions):
@@ -96,7 +108,7 @@ class Launcher:
                 copy_back.append((value, dev))
             elif isinstance(value, torch.Tensor) and value.dim() > 0:
                 if value.device.type == "cuda":
-                    device_args[name] = value
+                    device_args[name] = require_contiguous(name, value)
                 else:
                     dev = value.contiguous().to("cuda")
                     device_args[name] = dev

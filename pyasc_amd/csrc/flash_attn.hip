@@ -542,6 +542,11 @@ int32_t launch(FaArgs p, hipStream_t stream) {
     p.head_group = static_cast<int>(g < 1 ? 1 : (g > heads_xcd && heads_xcd > 0 ? heads_xcd : g));
   }
   const int64_t blocks = p.heads_total * p.n_qblocks;
+  // one workgroup per (head, query block): the grid's x dimension and its thread count
+  // (blocks x kWaves x 64) must fit 32 bits
+  ASC_REQUIRE(blocks <= (int64_t{1} << 31) - 1 && blocks * kWaves * 64 < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED,
+              "asc_flash_attention_fwd_bf16: %lld heads x %d query blocks exceed the launch grid limit",
+              static_cast<long long>(p.heads_total), p.n_qblocks);
   hipLaunchKernelGGL((fa_fwd_kernel<D, kWaves>), dim3(static_cast<uint32_t>(blocks)), dim3(kWaves * 64), 0, stream,
                      p);
   return asc::check_launch("asc_flash_attention_fwd_bf16");

@@ -118,7 +118,43 @@ int32_t launch(const void* xv, const void* yv, void* outv, int64_t covered, hipS
   return ASC_OK;
 }
 
+// dst[v] = src[v] for 16-byte vectors v < n_vec: the same streaming shape as
+// vadd_vec_kernel (4 non-temporal vectors per thread in flight) with one operand,
+// the bandwidth reference the streaming kernels are compared with.
+__global__ void __launch_bounds__(kThreads) copy_vec_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                            int64_t n_vec) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
+  if (base + (kUnroll - 1) * kThreads < n_vec) {
+    u32x4 a[kUnroll];
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) a[j] = __builtin_nontemporal_load(src + base + j * kThreads);
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) __builtin_nontemporal_store(a[j], dst + base + j * kThreads);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) {
+      const int64_t v = base + j * kThreads;
+      if (v < n_vec) dst[v] = src[v];
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int32_t asc_copy_bytes(const void* src, void* dst, int64_t n_bytes, asc_stream_t stream) {
+  ASC_REQUIRE(n_bytes >= 0, ASC_ERR_INVALID_ARG, "asc_copy_bytes: negative size");
+  if (n_bytes == 0) return ASC_OK;
+  ASC_REQUIRE(src && dst, ASC_ERR_INVALID_ARG, "asc_copy_bytes: null buffer");
+  ASC_REQUIRE(asc::aligned16(src) && asc::aligned16(dst) && n_bytes % 16 == 0, ASC_ERR_ALIGNMENT,
+              "asc_copy_bytes: buffers and size must be multiples of 16 bytes");
+  const int64_t n_vec = n_bytes / 16;
+  const int64_t blocks = asc::ceil_div(n_vec, kThreads * kUnroll);
+  ASC_REQUIRE(blocks <= (int64_t{1} << 31) - 1, ASC_ERR_UNSUPPORTED, "asc_copy_bytes: size too large");
+  hipLaunchKernelGGL(copy_vec_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src), static_cast<u32x4*>(dst),
+                     n_vec);
+  return asc::check_launch("asc_copy_bytes");
+}
 
 extern "C" int32_t asc_vadd(int32_t dtype, const void* x, const void* y, void* out, int64_t size, int32_t tile_size,
                             int32_t tile_per_block, int32_t grid, asc_stream_t stream) {

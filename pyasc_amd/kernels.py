@@ -246,11 +246,16 @@ def rms_norm(x: torch.Tensor, gamma: torch.Tensor, out: torch.Tensor, num_rows: 
 # -------------------------------------------------------------------------------------------- matmul
 
 def _row_major_2d(t: torch.Tensor, name: str) -> int:
-    """Leading dimension of a 2-D row-major (unit inner stride) tensor."""
+    """Leading dimension of a 2-D row-major (unit inner stride) tensor.  Rows must not
+    overlap: a row stride below the row length (an expanded or as_strided view) would
+    make the kernel read or write past the tensor's storage, and is refused."""
     if t.dim() != 2:
         raise ValueError(f"'{name}' must be 2-D, got shape {tuple(t.shape)}")
     if t.stride(1) != 1 and t.shape[1] > 1:
         raise ValueError(f"'{name}' must have unit stride along its last dimension")
+    if t.shape[0] > 1 and t.stride(0) < t.shape[1]:
+        raise ValueError(f"'{name}' has row stride {t.stride(0)} below its row length {t.shape[1]}: "
+                         "overlapping or expanded rows are not supported")
     return max(t.stride(0), t.shape[1], 1)
 
 
@@ -471,8 +476,13 @@ def binary(x: Any, y: Any, out: torch.Tensor, op: str, n: Optional[int] = None, 
     else:
         mode, scalar = 2, x
         _flat(y, "y", n)
-    if op in ("left_shift", "right_shift") and (mode != 1 or ref.dtype.is_floating_point):
-        raise TypeError(f"{op} takes an integer tensor and a scalar shift amount")
+    if op in ("left_shift", "right_shift"):
+        if mode != 1 or ref.dtype.is_floating_point:
+            raise TypeError(f"{op} takes an integer tensor and a scalar shift amount")
+        bits = torch.iinfo(ref.dtype).bits
+        shift = int(scalar.item()) if isinstance(scalar, torch.Tensor) else int(scalar)
+        if not 0 <= shift < bits:
+            raise ValueError(f"{op} amount {shift} is outside [0, {bits}) for {ref.dtype}")
     s_f, s_i = _scalar_parts(scalar, ref.dtype) if scalar is not None else (0.0, 0)
     # an unused operand slot gets the output buffer (valid for n elements), never NULL
     _native.call("asc_binary", BINARY_OPS.index(op), code, x.data_ptr() if x_t else out.data_ptr(),

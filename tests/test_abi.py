@@ -53,6 +53,10 @@ def test_version_string():
     ("asc_fill", (0, 0, 8, 1.0, 0, None), _native.ERR_INVALID_ARG),
     ("asc_rect_binary", (0, 0, 1, 1, 1, 8, 8, -1, 0, 2, 2, None), _native.ERR_INVALID_ARG),
     ("asc_broadcast_rows", (3, 1, 1, 2, 2, None), _native.ERR_UNSUPPORTED),
+    ("asc_copy_bytes", (16, 32, -16, None), _native.ERR_INVALID_ARG),
+    ("asc_copy_bytes", (0, 32, 16, None), _native.ERR_INVALID_ARG),  # null src
+    ("asc_copy_bytes", (16, 32, 24, None), _native.ERR_ALIGNMENT),  # size not a multiple of 16
+    ("asc_copy_bytes", (8, 32, 16, None), _native.ERR_ALIGNMENT),  # unaligned src
 ])
 def test_argument_errors_are_reported(fn, args, code):
     lib = _native.load_library()
@@ -73,4 +77,5 @@ def test_zero_sized_launch_is_a_noop():
     assert lib.asc_transpose_batched(2, None, None, 0, 16, 16, None) == 0
     assert lib.asc_rect_binary(0, 0, None, None, None, 8, 8, 8, 0, 2, 2, None) == 0  # clipped to nothing
     assert lib.asc_vadd(0, None, None, None, 0, 128, 4, 16, None) == 0
+    assert lib.asc_copy_bytes(None, None, 0, None) == 0
     assert lib.asc_vadd(0, None, None, None, 100, 128, 0, 16, None) == 0  # tile_per_block 0 covers nothing

@@ -31,7 +31,7 @@ def _launch_shape(total, cores, tile_length):
 @asc.jit
 def vadd_kernel(x: asc.GlobalAddress, y: asc.GlobalAddress, z: asc.GlobalAddress, block_length: asc.ConstExpr[int],
                 buffer_num: asc.ConstExpr[int], tile_length: asc.ConstExpr[int], tile_num: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("tile_length", [512, 64])  # test_vadd.py / test_vadd_sw.py: 512; _bits / _l0: 64
@@ -48,7 +48,7 @@ def test_vadd_family(device, dtype, size, tile_length):
 @asc.jit
 def vadds_kernel(x: asc.GlobalAddress, scalar, z: asc.GlobalAddress, block_length: asc.ConstExpr[int],
                  buffer_num: asc.ConstExpr[int], tile_length: asc.ConstExpr[int], tile_num: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype, size", PARAMS, ids=str)
@@ -67,7 +67,7 @@ def test_vadds(device, dtype, size):
 @asc.jit
 def vsqrt_kernel(x: asc.GlobalAddress, z: asc.GlobalAddress, block_length: asc.ConstExpr[int],
                  buffer_num: asc.ConstExpr[int], tile_length: asc.ConstExpr[int], tile_num: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype, size", [(torch.float16, (2048,)), (torch.float32, (5000,)), (torch.float32, (9999,)),
@@ -85,7 +85,7 @@ def test_vsqrt(device, dtype, size):
 @asc.jit
 def duplicate_kernel(scalar, z: asc.GlobalAddress, block_length: asc.ConstExpr[int], buffer_num: asc.ConstExpr[int],
                      tile_length: asc.ConstExpr[int], tile_num: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype, size", [(torch.float32, (1000,)), (torch.float32, (1,)), (torch.float16, (2048,)),
@@ -105,7 +105,7 @@ def test_duplicate(device, dtype, size):
 def axpy_kernel(x: asc.GlobalAddress, y: asc.GlobalAddress, z: asc.GlobalAddress, scalar: float,
                 block_length: asc.ConstExpr[int], buffer_num: asc.ConstExpr[int], tile_length: asc.ConstExpr[int],
                 tile_num: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype, size", [(torch.float32, (4096,)), (torch.float32, (8192,)), (torch.float16, (8192,)),
@@ -144,7 +144,7 @@ def test_axpy_accumulates_vs_fp64(device, dtype):
 
 @asc.jit
 def copy_kernel(x: asc.GlobalAddress, z: asc.GlobalAddress, data_size: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype, size", [(torch.float32, (1000,)), (torch.float32, (1,)), (torch.float32, (9999,)),
@@ -167,7 +167,7 @@ def test_copy(device, dtype, size):
 @asc.jit
 def transpose_kernel(x: asc.GlobalAddress, z: asc.GlobalAddress, block_length: asc.ConstExpr[int],
                      buffer_num: asc.ConstExpr[int], tile_length: asc.ConstExpr[int], tile_num: asc.ConstExpr[int]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.int16])
@@ -219,7 +219,7 @@ def _adv_tiling(m, n, k, dtype, bias=False, batch=None):
 @asc.jit
 def matmul_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress, alpha: float,
                   tiling: asc.adv.TCubeTiling, bias: asc.GlobalAddress, workspace: asc.GlobalAddress):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 def test_adv_matmul(device):
@@ -239,7 +239,7 @@ def test_adv_matmul(device):
 @asc.jit
 def iterate_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress, tiling: asc.adv.TCubeTiling,
                    workspace: asc.GlobalAddress):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 iterate_kernel.fn_name = "matmul_kernel"  # test_matmul_iterate_all.py:24, test_matmul_iterate_batch.py:29
@@ -285,7 +285,7 @@ def test_adv_matmul_iterate_batch(device, dtype, size):
 @asc.jit(kernel_type=config.KernelType.AIV_ONLY)
 def quant_kernel(src_gm: asc.GlobalAddress, dst_gm: asc.GlobalAddress, size: int, tmp_min_bytes: int,
                  use_config: asc.ConstExpr[bool]):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("use_config", [True, False])

@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 def matmul_leakyrelu_kernel(a: asc.GlobalAddress, b: asc.GlobalAddress, c: asc.GlobalAddress,
                             bias: asc.GlobalAddress, alpha: float, tiling: asc.adv.TCubeTiling,
                             workspace: asc.GlobalAddress):
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 def test_tutorial_recipe(device):

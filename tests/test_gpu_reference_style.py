@@ -92,3 +92,222 @@ def test_softmax_fused(device):
     block_size = (64 + core_num - 1) // core_num
     softmax_kernel[core_num](x, out, 64, 1024, block_size)
     torch.testing.assert_close(out, torch.softmax(x, dim=1))
+
+
+# ------------------------------------------------------------------------------------ matmul
+# The reference's asc2 matmul tests, kernels with their bodies as written and launched as
+# matmul_kernel[grid](...) on CPU tensors (the reference's host-tensor path: copied in,
+# launched, copied back), each against its own golden and tolerance
+# (python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py).
+
+def _mnblock_kernel():
+    @asc2.jit(always_compile=True)
+    def matmul_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                      a_shape: asc.ConstExpr, b_shape: asc.ConstExpr, c_shape: asc.ConstExpr,
+                      m_tile: asc.ConstExpr[int], m_tiles_per_block: asc.ConstExpr[int],
+                      n_tile: asc.ConstExpr[int], n_tiles_per_block: asc.ConstExpr[int]):
+        a_gm = asc2.tensor(a_ptr, a_shape)
+        b_gm = asc2.tensor(b_ptr, b_shape)
+        c_gm = asc2.tensor(c_ptr, c_shape)
+        blockId = asc2.block_idx()
+        m_elems_per_block = m_tile * m_tiles_per_block
+        m_base_off = (m_elems_per_block * blockId) % a_shape[0]
+        n_base_off = ((m_elems_per_block * blockId) // a_shape[0]) * (n_tile * n_tiles_per_block)
+        for j in range(n_tiles_per_block):
+            b_offset = n_base_off + j * n_tile
+            b_j = asc2.load(b_gm, [b_shape[0], n_tile], offsets=[0, b_offset], location=asc2.TileLocation.L0B)
+            for i in range(m_tiles_per_block):
+                a_offset = m_base_off + i * m_tile
+                a_i = asc2.load(a_gm, [m_tile, a_shape[1]], offsets=[a_offset, 0], location=asc2.TileLocation.L0A)
+                c_ij = a_i @ b_j
+                asc2.store(c_ij, c_gm, offsets=[a_offset, b_offset])
+
+    return matmul_kernel
+
+
+matmul_mnblock_kernel = _mnblock_kernel()
+
+
+def _m_tiles_per_block(m, k, n, core_num, m_tile, n_tile, n_tiles_per_block):
+    # eval_tiles of test_matmul_mnblock.py: the even split its asserts require
+    tiles_per_core = (m // m_tile) * (n // n_tile) // core_num
+    return tiles_per_core // n_tiles_per_block
+
+
+@pytest.mark.parametrize("m, k, n, core_num, m_tile, n_tile, n_tiles_per_block", [
+    (16, 16, 16, 1, 16, 16, 1),
+    (16, 160, 16, 1, 16, 16, 1),
+    (32, 16, 16, 2, 16, 16, 1),
+    (16, 16, 32, 2, 16, 16, 1),
+    (32, 16, 32, 2, 16, 16, 1),
+    (32, 16, 32, 2, 16, 16, 2),
+    (32, 16, 32, 4, 16, 16, 1),
+    (480, 224, 1344, 30, 48, 32, 7),
+])
+def test_matmul_mnblock(device, m, k, n, core_num, m_tile, n_tile, n_tiles_per_block):
+    torch.manual_seed(m * 7 + n)
+    a = torch.rand((m, k), dtype=torch.float16)
+    b = torch.rand((k, n), dtype=torch.float16)
+    c = torch.zeros((m, n), dtype=torch.float32)
+    mtpb = _m_tiles_per_block(m, k, n, core_num, m_tile, n_tile, n_tiles_per_block)
+    matmul_mnblock_kernel[core_num](a, b, c, a.shape, b.shape, c.shape, m_tile, mtpb, n_tile, n_tiles_per_block)
+    torch.testing.assert_close(c, a.to(torch.float32) @ b.to(torch.float32))
+
+
+def _tiled_kernel():
+    @asc2.jit(always_compile=True)
+    def matmul_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                      a_shape: asc.ConstExpr, b_shape: asc.ConstExpr, c_shape: asc.ConstExpr,
+                      k_tiles: asc.ConstExpr):
+        a_gm = asc2.tensor(a_ptr, a_shape)
+        b_gm = asc2.tensor(b_ptr, b_shape)
+        c_gm = asc2.tensor(c_ptr, c_shape)
+        acc = asc2.zeros_acc(c_shape, dtype=asc.float32)
+        k_offset = a_shape[1] // k_tiles
+        a_l1 = asc2.load(a_gm, a_shape, offsets=[0, 0], location=asc2.TileLocation.L1)
+        b_l1 = asc2.load(b_gm, b_shape, offsets=[0, 0], location=asc2.TileLocation.L1)
+        for i in range(k_tiles, unroll_factor=2, parallel=True):
+            a_i = asc2.copy(a_l1, [a_shape[0], k_offset], offsets=[0, i * k_offset], location=asc2.TileLocation.L0A)
+            b_i = asc2.copy(b_l1, [k_offset, b_shape[1]], offsets=[i * k_offset, 0], location=asc2.TileLocation.L0B)
+            asc2.matmul_acc(a_i, b_i, acc)
+        asc2.store(acc, c_gm, offsets=[0, 0])
+
+    return matmul_kernel
+
+
+matmul_tiled_kernel = _tiled_kernel()
+
+
+@pytest.mark.parametrize("k_tiles", [2, 4, 8])
+def test_matmul_tiled(device, k_tiles):
+    torch.manual_seed(k_tiles)
+    m, k, n = 64, 128, 256
+    a = torch.rand((m, k), dtype=torch.float16)
+    b = torch.rand((k, n), dtype=torch.float16)
+    c = torch.zeros((m, n), dtype=torch.float32)
+    matmul_tiled_kernel[1](a, b, c, a.shape, b.shape, c.shape, k_tiles)
+    torch.testing.assert_close(c, a.to(torch.float32) @ b.to(torch.float32))
+
+
+def _fixpipe_kernel():
+    @asc2.jit(always_compile=True)
+    def matmul_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                      a_shape: asc.ConstExpr, b_shape: asc.ConstExpr, c_shape: asc.ConstExpr):
+        a_gm = asc2.tensor(a_ptr, a_shape)
+        b_gm = asc2.tensor(b_ptr, b_shape)
+        c_gm = asc2.tensor(c_ptr, c_shape)
+        a = asc2.load(a_gm, a_shape, offsets=[0, 0], location=asc2.TileLocation.L0A)
+        b = asc2.load(b_gm, b_shape, offsets=[0, 0], location=asc2.TileLocation.L0B)
+        c = a @ b
+        c = asc2.relu(c).to(asc.float16)
+        asc2.store(c, c_gm, offsets=[0, 0])
+
+    return matmul_kernel
+
+
+matmul_fixpipe_kernel = _fixpipe_kernel()
+
+
+@pytest.mark.parametrize("m, k, n, dtype", [
+    (64, 128, 128, torch.float32),
+    (64, 128, 256, torch.float16),
+    (64, 128, 256, torch.bfloat16),
+])
+def test_matmul_fixpipe(device, m, k, n, dtype):
+    torch.manual_seed(n)
+    a = (torch.rand((m, k), dtype=dtype) - .5) * 10
+    b = (torch.rand((k, n), dtype=dtype) - .5) * 10
+    c = torch.zeros((m, n), dtype=torch.float16)
+    matmul_fixpipe_kernel[1](a, b, c, a.shape, b.shape, c.shape)
+    c_ref = (a.to(torch.float32) @ b.to(torch.float32)).relu().to(torch.float16)
+    torch.testing.assert_close(c, c_ref, atol=1e-3, rtol=1e-3)
+
+
+def _chained_kernel():
+    @asc2.jit(always_compile=True)
+    def matmul_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                      a_shape: asc.ConstExpr, b_shape: asc.ConstExpr, c_shape: asc.ConstExpr,
+                      dtype: asc.ConstExpr):
+        a_gm = asc2.tensor(a_ptr, a_shape)
+        b_gm = asc2.tensor(b_ptr, b_shape)
+        c_gm = asc2.tensor(c_ptr, c_shape)
+        a = asc2.load(a_gm, a_shape, offsets=[0, 0], location=asc2.TileLocation.L0A)
+        b = asc2.load(b_gm, b_shape, offsets=[0, 0], location=asc2.TileLocation.L0B)
+        c = a @ b
+        c = c.to(dtype)
+        c_l1 = asc2.copy(c, c_shape, offsets=[0, 0], location=asc2.TileLocation.L1)
+        c_l0a = asc2.copy(c_l1, c_shape, offsets=[0, 0], location=asc2.TileLocation.L0A)
+        result = c_l0a @ b
+        asc2.store(result, c_gm, offsets=[0, 0])
+
+    return matmul_kernel
+
+
+matmul_chained_kernel = _chained_kernel()
+
+
+@pytest.mark.parametrize("m, k, n, torch_dtype, pyasc_dtype", [
+    (32, 64, 64, torch.float16, asc.float16),
+    (64, 64, 64, torch.bfloat16, asc.bfloat16),
+])
+def test_matmul_l0c_to_l1(device, m, k, n, torch_dtype, pyasc_dtype):
+    torch.manual_seed(0)
+    a = (torch.rand((m, k), dtype=torch_dtype) - .5) * 10
+    b = (torch.rand((k, n), dtype=torch_dtype) - .5) * 10
+    c = torch.zeros((m, n), dtype=torch.float32)
+    matmul_chained_kernel[1](a, b, c, a.shape, b.shape, c.shape, pyasc_dtype)
+    c_ref = (a.to(torch.float32) @ b.to(torch.float32)).to(torch_dtype)
+    c_ref = c_ref.to(torch.float32) @ b.to(torch.float32)
+    torch.testing.assert_close(c, c_ref, atol=1e-3, rtol=1e-3)
+
+
+def test_matmul_mnblock_device_tensors(device):
+    # the same launch on device tensors: zero-copy, asynchronous on the current stream
+    m, k, n, core_num, m_tile, n_tile, ntpb = 480, 224, 1344, 30, 48, 32, 7
+    g = torch.Generator().manual_seed(5)
+    a = torch.rand((m, k), generator=g).to(torch.float16)
+    b = torch.rand((k, n), generator=g).to(torch.float16)
+    c = torch.full((m, n), -1.0, device=device)
+    mtpb = _m_tiles_per_block(m, k, n, core_num, m_tile, n_tile, ntpb)
+    matmul_mnblock_kernel[core_num](a.to(device), b.to(device), c, a.shape, b.shape, c.shape, m_tile, mtpb, n_tile,
+                                    ntpb)
+    torch.testing.assert_close(c.cpu(), a.float() @ b.float())
+
+
+def test_matmul_noncontiguous_device_output_is_refused(device):
+    a = torch.rand((64, 128), device=device).to(torch.float16)
+    b = torch.rand((128, 64), device=device).to(torch.float16)
+    c = torch.zeros((64, 64), device=device).t()  # a transposed view
+    with pytest.raises(ValueError, match="non-contiguous device tensor"):
+        matmul_tiled_kernel[1](a, b, c, a.shape, b.shape, c.shape, 2)
+
+
+# int8 kernels (build-defined asc2-style signatures), declared by signature, on the
+# reference quant test's recipe (tests/golden/matmul_quant.npz: randint(-5, 5) int8,
+# golden gen_golden of python/test/generalization/adv/test_matmul_quant.py:94-106)
+
+@asc2.jit
+def matmul_int8_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                       a_shape: asc.ConstExpr, b_shape: asc.ConstExpr, c_shape: asc.ConstExpr):
+    """c (int32) = a (int8) @ b (int8), exact."""
+
+
+@asc2.jit
+def matmul_dequant_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                          quant_ptr: asc.GlobalAddress, a_shape: asc.ConstExpr, b_shape: asc.ConstExpr,
+                          c_shape: asc.ConstExpr, trunc_scale: asc.ConstExpr):
+    """c (fp16) = fp16(fp32(a @ b) * scale[n]); trunc_scale clears the scale's low 13 mantissa bits."""
+
+
+@pytest.mark.parametrize("idx", [0, 1, 2])
+def test_matmul_int8_and_dequant_on_quant_fixture(device, idx):
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "matmul_quant.npz"))
+    a, b, scale = f[f"a{idx}"], f[f"b{idx}"], f[f"scale{idx}"]
+    M, N = a.shape[0], b.shape[1]
+    acc = np.zeros((M, N), np.int32)
+    matmul_int8_kernel[16](a, b, acc, a.shape, b.shape, acc.shape)
+    np.testing.assert_array_equal(acc, f[f"acc{idx}"])
+    out = np.zeros((M, N), np.float16)
+    matmul_dequant_kernel[16](a, b, out, scale, a.shape, b.shape, out.shape, True)
+    np.testing.assert_array_equal(out.view(np.uint16), f[f"golden{idx}"].view(np.uint16))

@@ -95,12 +95,12 @@ import asc2  # noqa: E402
 
 @asc2.jit(always_compile=True)
 def softmax_1d_kernel(dst_ptr, src_ptr, length: asc.ConstExpr) -> None:
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @asc2.jit(always_compile=True)
 def softmax_2d_kernel(dst_ptr, src_ptr, shape: asc.ConstExpr) -> None:
-    raise AssertionError("kernel bodies are not executed")
+    ...  # declaration: binds the registered native kernel by signature
 
 
 @pytest.mark.parametrize("dtype, shape", [(torch.float16, [1, 16]), (torch.float16, [4, 1024]),

@@ -18,8 +18,7 @@ from pyasc_amd.launchers import mnblock_rectangles
 @asc2.jit(always_compile=True)
 def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
                 tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
-    x_gm = asc2.tensor(x_ptr, [size])  # never executed
-    asc2.store(x_gm, x_gm, offsets=[0])
+    """Declaration: binds the registered vadd kernel by its signature."""
 
 
 @pytest.fixture
@@ -209,9 +208,9 @@ def lookups(monkeypatch):
     seen = []
     real = registry.lookup
 
-    def counting(name, params):
+    def counting(name, params, body_fingerprint=None):
         seen.append(name)
-        return real(name, params)
+        return real(name, params, body_fingerprint)
 
     monkeypatch.setattr(registry, "lookup", counting)
     return seen
@@ -274,10 +273,11 @@ def test_cache_key_components():
     assert JITFunction.arg_kind(True) == "plain:int8"
 
 
-def test_string_annotations_with_local_import(recorded):
+def test_string_annotations_with_local_import(recorded, tmp_path):
     # `from __future__ import annotations` with asc imported inside a function: the
     # annotation strings cannot be evaluated in the module globals, ConstExpr is
     # still recognised by its text
+    import importlib.util
     src = (
         "from __future__ import annotations\n"
         "def make():\n"
@@ -287,9 +287,12 @@ def test_string_annotations_with_local_import(recorded):
         "                    size: int, tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):\n"
         "        pass\n"
         "    return vadd_kernel\n")
-    ns = {"__name__": "local_import_kernels"}
-    exec(compile(src, "local_import_kernels", "exec"), ns)
-    k = ns["make"]()
+    path = tmp_path / "local_import_kernels.py"
+    path.write_text(src)  # a real file, so the body's source can be read for its fingerprint
+    spec = importlib.util.spec_from_file_location("local_import_kernels", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    k = mod.make()
     x = torch.zeros(64)
     k[2](x, x, x, 64, 8, 4)
     k[2](x, x, x, 64, 8, 4, always_compile=True)
@@ -424,3 +427,183 @@ def test_invalid_compile_option(recorded):
 
     copy_kernel[1](np.zeros(8, np.float32), np.zeros(8, np.float32), 8)
     assert recorded[-1][-1]["opt_level"] == 2
+
+
+# ------------------------------------------------------------------------------ body fingerprints
+# Dispatch is by (name, parameter names); the body must also be one the native kernel
+# implements (a reference body of that signature) or a declaration.
+
+def _reference_vadd_body():
+    @asc2.jit
+    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                    tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [size])
+        y_gm = asc2.tensor(y_ptr, [size])
+        out_gm = asc2.tensor(out_ptr, [size])
+        base_offset = asc2.block_idx() * tile_size * tile_per_block
+        for i in range(tile_per_block):
+            tile_offset = base_offset + i * tile_size
+            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
+            y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
+            out = x + y
+            asc2.store(out, out_gm, offsets=[tile_offset])
+
+    return vadd_kernel
+
+
+def _renamed_vadd_body():
+    # the same computation with other local names, an inlined temporary and loop hints
+    @asc2.jit
+    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                    tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+        """Adds two vectors tile by tile."""
+        xs = asc2.tensor(x_ptr, [size])
+        ys = asc2.tensor(y_ptr, [size])
+        zs = asc2.tensor(out_ptr, [size])
+        base = asc2.block_idx() * tile_size * tile_per_block
+        for t in range(tile_per_block, unroll_factor=2, parallel=True):
+            off = base + t * tile_size
+            a = asc2.load(xs, [tile_size], offsets=[off])
+            b = asc2.load(ys, [tile_size], offsets=[off])
+            asc2.store(a + b, zs, offsets=[off])
+
+    return vadd_kernel
+
+
+def _different_vadd_body():
+    # same signature, different computation (x - y)
+    @asc2.jit
+    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                    tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [size])
+        y_gm = asc2.tensor(y_ptr, [size])
+        out_gm = asc2.tensor(out_ptr, [size])
+        base_offset = asc2.block_idx() * tile_size * tile_per_block
+        for i in range(tile_per_block):
+            tile_offset = base_offset + i * tile_size
+            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
+            y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
+            out = x - y
+            asc2.store(out, out_gm, offsets=[tile_offset])
+
+    return vadd_kernel
+
+
+def test_reference_body_and_declaration_dispatch(recorded):
+    x = np.zeros(64, np.float32)
+    for k in (_reference_vadd_body(), _renamed_vadd_body(), _cached_vadd()):
+        k[2](x, x, x, 64, 8, 4)
+    assert len(recorded) == 3 and all(r[0].name == "vadd_kernel" for r in recorded)
+    assert _reference_vadd_body().body_fingerprint == _renamed_vadd_body().body_fingerprint
+    assert _cached_vadd().body_fingerprint == "declaration"
+
+
+def test_different_body_is_refused(recorded, monkeypatch):
+    monkeypatch.delenv(registry.ALLOW_BODY_MISMATCH_ENV, raising=False)
+    x = np.zeros(64, np.float32)
+    for options in ({}, {"always_compile": True}):
+        k = _different_vadd_body()
+        with pytest.raises(registry.KernelBodyMismatch, match="differs from every body"):
+            k[2](x, x, x, 64, 8, 4, **options)
+    assert not recorded
+    # the explicit opt-out runs the registered kernel with a warning
+    monkeypatch.setenv(registry.ALLOW_BODY_MISMATCH_ENV, "1")
+    with pytest.warns(RuntimeWarning, match="differs from every body"):
+        _different_vadd_body()[2](x, x, x, 64, 8, 4)
+    assert len(recorded) == 1
+
+
+def test_build_defined_kernels_accept_declarations_only(recorded, monkeypatch):
+    monkeypatch.delenv(registry.ALLOW_BODY_MISMATCH_ENV, raising=False)
+
+    @asc2.jit
+    def matmul_int8_kernel(a_ptr: asc.GlobalAddress, b_ptr: asc.GlobalAddress, c_ptr: asc.GlobalAddress,
+                           a_shape: asc.ConstExpr, b_shape: asc.ConstExpr, c_shape: asc.ConstExpr):
+        c = asc2.matmul(asc2.load(a_ptr, a_shape, offsets=[0, 0]), asc2.load(b_ptr, b_shape, offsets=[0, 0]))
+        asc2.store(c, c_ptr, offsets=[0, 0])
+
+    a = np.zeros((4, 4), np.int8)
+    with pytest.raises(registry.KernelBodyMismatch):
+        matmul_int8_kernel[1](a, a, np.zeros((4, 4), np.int32), [4, 4], [4, 4], [4, 4])
+
+
+def test_source_unavailable_is_refused(monkeypatch):
+    monkeypatch.delenv(registry.ALLOW_BODY_MISMATCH_ENV, raising=False)
+    ns = {"asc": asc, "asc2": asc2}
+    exec("def vadd_kernel(x_ptr, y_ptr, out_ptr, size, tile_size, tile_per_block):\n    pass\n", ns)
+    k = asc2.jit(ns["vadd_kernel"])
+    assert k.body_fingerprint is None
+    with pytest.raises(registry.KernelBodyMismatch, match="source is not available"):
+        k.resolve(np.zeros(4, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 4, 1)
+
+
+def test_fingerprint_table_covers_the_registry():
+    from pyasc_amd import fingerprint
+    table = fingerprint.known_fingerprints()
+    keys = {fingerprint.signature_key(n, p) for n, p in registry.entries()}
+    assert keys == set(table)
+    build_defined = {k for k, v in table.items() if not v}
+    assert {k.split("(")[0] for k in build_defined} == {
+        "flash_attention_fwd_kernel", "matmul_int8_kernel", "matmul_dequant_kernel", "rms_norm_kernel"}
+
+
+@pytest.mark.skipif(not __import__("os").path.isdir("/root/reference/python/test"),
+                    reason="the reference tree is present only where the table is generated")
+def test_fingerprint_table_matches_the_reference(tmp_path, monkeypatch):
+    # regenerate from the reference's sources (parsed as text) and compare with the committed table
+    import json
+    from pyasc_amd import fingerprint, make_fingerprints
+    out = tmp_path / "fp.json"
+    monkeypatch.setattr(make_fingerprints, "FINGERPRINTS_FILE", str(out))
+    make_fingerprints.main(["x", "/root/reference"])
+    with open(fingerprint.FINGERPRINTS_FILE) as f:
+        committed = json.load(f)["kernels"]
+    assert json.loads(out.read_text())["kernels"] == committed
+
+
+# ------------------------------------------------------------------- host-side layout checks
+# Refused on the host, before the C ABI is reached (no GPU needed).
+
+@pytest.fixture
+def no_native(monkeypatch):
+    """kernels.* with CPU tensors standing in for device tensors; records C-ABI calls."""
+    from pyasc_amd import kernels
+    calls = []
+    monkeypatch.setattr(kernels, "_device_tensor", lambda t, name: t)
+    monkeypatch.setattr(kernels._native, "call", lambda *a: calls.append(a))
+    monkeypatch.setattr(kernels, "_stream", lambda s: 0)
+    return calls
+
+
+@pytest.mark.parametrize("which", ["a", "b", "c"])
+def test_matmul_refuses_overlapping_rows(no_native, which):
+    from pyasc_amd import kernels
+    ops = {"a": torch.zeros(64, 32, dtype=torch.bfloat16), "b": torch.zeros(32, 48, dtype=torch.bfloat16),
+           "c": torch.zeros(64, 48, dtype=torch.bfloat16)}
+    shape = ops[which].shape
+    ops[which] = torch.zeros(1, shape[1], dtype=torch.bfloat16).expand(shape[0], shape[1])  # row stride 0
+    with pytest.raises(ValueError, match="row stride 0 below its row length"):
+        kernels.matmul(ops["a"], ops["b"], ops["c"])
+    assert not no_native
+    # a strided row-major view with room between rows is accepted and passes its leading dimension
+    big = torch.zeros(64, 100, dtype=torch.bfloat16)
+    kernels.matmul(big[:, :32], torch.zeros(32, 48, dtype=torch.bfloat16), torch.zeros(64, 48, dtype=torch.bfloat16))
+    assert no_native[-1][0] == "asc_matmul" and no_native[-1][9] == 100  # lda
+
+
+def test_launcher_refuses_noncontiguous_device_tensors():
+    c = torch.zeros(8, 4).t()  # transposed view: writes through reshape(-1) would land in a copy
+    with pytest.raises(ValueError, match="non-contiguous device tensor"):
+        launcher_mod.require_contiguous("c_ptr", c)
+    t = torch.zeros(4, 8)
+    assert launcher_mod.require_contiguous("c_ptr", t) is t
+
+
+@pytest.mark.parametrize("dtype,bad", [(torch.int32, 32), (torch.int32, -1), (torch.int16, 16)])
+def test_shift_amount_range(no_native, dtype, bad):
+    from pyasc_amd import kernels
+    x = torch.zeros(16, dtype=dtype)
+    with pytest.raises(ValueError, match="outside"):
+        kernels.binary(x, bad, torch.empty_like(x), "left_shift")
+    kernels.binary(x, torch.iinfo(dtype).bits - 1, torch.empty_like(x), "right_shift")
+    assert len(no_native) == 1
