@@ -20,8 +20,9 @@ own event pair instead.  HBM-bound workloads rotate through enough
 input/output sets (> 512 MiB) that the 256 MiB Infinity Cache cannot serve
 them; so do the MFMA workloads.  The CPU baseline of every workload is the
 reference test's torch CPU golden expression (oracle/cpu_golden.py), timed on
-the host cores on a bounded sample; each names the host (thread count,
-os.cpu_count(), CPU model) it ran on.
+the host cores on the full workload (repeated to at least 2 s of CPU work, 10 s
+for the headline); each names the host (thread count, os.cpu_count(), CPU
+model) it ran on.
 
 `roofline.traffic` comes from profiles/traffic.json (rocprofv3 FETCH_SIZE /
 WRITE_SIZE passes summarised by profile_summary.py).  Each entry is stamped with
@@ -37,7 +38,6 @@ import hashlib
 import json
 import math
 import os
-import statistics
 import sys
 import time
 
@@ -53,7 +53,8 @@ METRIC = "HBM GB/s (vadd, softmax); TFLOP/s or TOPS (matmul, FA-fwd); % of MI355
 ROTATE_BYTES = 640 << 20  # > 2x the 256 MiB Infinity Cache
 SMALL_SET_BYTES = 4 << 20  # below this a workload is latency-bound and is not rotated
 CSRC = os.path.join(REPO, "pyasc_amd", "csrc")
-CPU_BUDGET_S = 6.0  # per CPU baseline: warm-up, then up to 5 timed runs within this budget
+CPU_MIN_S = 2.0  # timed CPU work per suite baseline (the full workload, repeated to at least this long)
+CPU_HEADLINE_S = 10.0  # the same for the headline's baseline
 
 
 class Workload:
@@ -132,23 +133,32 @@ def host_info() -> dict:
     return _HOST
 
 
-def _time_cpu(fn, budget_s: float = CPU_BUDGET_S) -> float:
-    fn()  # warm-up
-    times = []
-    start = time.perf_counter()
-    for _ in range(5):
-        t0 = time.perf_counter()
+def _time_cpu(fn, min_total_s: float = CPU_MIN_S):
+    """(seconds per call, calls timed): one warm-up call (kept as the sample when it alone
+    takes over a second), then calls until ``min_total_s`` of timed work; the mean."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    if first > 1.0 and first >= min_total_s:
+        return first, 1
+    calls, start = 0, time.perf_counter()
+    while True:
         fn()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - start > budget_s:
-            break
-    return statistics.median(times)
+        calls += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= min_total_s:
+            return elapsed / calls, calls
 
 
-def _cpu(value: float, unit: str, expression: str, sample: str, secs: float, threads=None) -> dict:
+def _cpu(work: float, scale: float, unit: str, expression: str, sample: str, timing) -> dict:
+    """A cpu_baseline object: ``work`` units per call timed as ``timing`` = (seconds per
+    call, calls); value = work / seconds / scale (or microseconds for unit "us")."""
     import torch
-    return {"value": value, "unit": unit, "cores": threads if threads is not None else torch.get_num_threads(),
-            "kind": "port", "expression": expression, "sample": sample + "; median of up to 5 runs after 1 warm-up",
+    secs, calls = timing
+    value = secs * 1e6 if unit == "us" else work / secs / scale
+    return {"value": round(value, 5), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "expression": expression,
+            "sample": f"{sample}; {calls} timed call(s) after 1 warm-up, mean ({secs * calls:.1f} s of CPU work)",
             "seconds_per_call": secs, "host": host_info()}
 
 
@@ -179,14 +189,13 @@ class Softmax(Workload):
         return {"workload": self.name, "rows": self.rows, "cols": self.cols, "tile_size": self.cols, "grid": 16,
                 "input": "randn*2 (N(0,4)), seed 1", "rotating_sets": len(self.xs)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
         x = torch.randn(self.rows, self.cols, generator=torch.Generator().manual_seed(1)) * 2.0
-        secs = _time_cpu(lambda: cpu_golden.softmax(x))
-        return _cpu(round(self.work() / secs / 1e9, 3), "GB/s",
-                    "torch.softmax(x, dim=1) (python/test/asc2/kernels/test_softmax.py:43)",
-                    f"the full {self.rows}x{self.cols} fp32 input", secs)
+        return _cpu(self.work(), 1e9, "GB/s", "torch.softmax(x, dim=1) (python/test/asc2/kernels/test_softmax.py:43)",
+                    f"the full {self.rows}x{self.cols} fp32 workload",
+                    _time_cpu(lambda: cpu_golden.softmax(x), min_total_s))
 
 
 class Copy(Workload):
@@ -223,13 +232,12 @@ class Copy(Workload):
                 "kernel": "asc_copy_bytes (non-temporal 16-byte vectors, 4 per thread)",
                 "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
-        n = min(self.n, 256 << 20)
-        src = torch.randint(0, 256, (n,), dtype=torch.uint8, generator=torch.Generator().manual_seed(0))
+        src = torch.randint(0, 256, (self.n,), dtype=torch.uint8, generator=torch.Generator().manual_seed(0))
         dst = torch.empty_like(src)
-        secs = _time_cpu(lambda: dst.copy_(src))
-        return _cpu(round(2.0 * n / secs / 1e9, 3), "GB/s", "dst.copy_(src) (torch host copy)", f"{n} bytes", secs)
+        return _cpu(self.work(), 1e9, "GB/s", "dst.copy_(src) (torch host copy)", f"the full {self.n}-byte copy",
+                    _time_cpu(lambda: dst.copy_(src), min_total_s))
 
 
 class Vadd(Workload):
@@ -263,15 +271,13 @@ class Vadd(Workload):
         return {"workload": self.name, "size": self.n, "tile_size": 128, "tile_per_block": self.tpb, "grid": 16,
                 "input": "torch.rand (uniform [0,1)), seed 0", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
-        n = min(self.n, 1 << 26)
         g = torch.Generator().manual_seed(0)
-        x, y = torch.rand(n, generator=g), torch.rand(n, generator=g)
-        secs = _time_cpu(lambda: cpu_golden.vadd(x, y))
-        return _cpu(round(12.0 * n / secs / 1e9, 3), "GB/s", "x + y (README.md:53; test_vadd.py:48)",
-                    f"{n} fp32 elements", secs)
+        x, y = torch.rand(self.n, generator=g), torch.rand(self.n, generator=g)
+        return _cpu(self.work(), 1e9, "GB/s", "x + y (README.md:53; test_vadd.py:48)",
+                    f"the full workload, {self.n} fp32 elements", _time_cpu(lambda: cpu_golden.vadd(x, y), min_total_s))
 
 
 class Asc2VaddPlumbing(Workload):
@@ -313,20 +319,14 @@ class Asc2VaddPlumbing(Workload):
                 "note": "latency-bound (96 KiB per launch): value is device microseconds per launch, "
                         "not rotated (the inputs stay in L2 as in the reference test)"}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
         g = torch.Generator().manual_seed(0)
         x, y = torch.rand(8192, generator=g), torch.rand(8192, generator=g)
-        reps = 2000
-
-        def run():
-            for _ in range(reps):
-                cpu_golden.vadd(x, y)
-
-        secs = _time_cpu(run) / reps
-        return _cpu(round(secs * 1e6, 3), "us", "x + y (README.md:53; test_vadd.py:48)",
-                    f"8192 fp32 elements, {reps} calls per timed run", secs)
+        return _cpu(self.work(), 1e9, "us", "x + y (README.md:53; test_vadd.py:48)",
+                    "the full workload, 8192 fp32 elements (microseconds per call)",
+                    _time_cpu(lambda: cpu_golden.vadd(x, y), min_total_s))
 
 
 class LeakyRelu(Workload):
@@ -358,15 +358,14 @@ class LeakyRelu(Workload):
         return {"workload": self.name, "size": self.n, "tile_size": 128, "tile_per_block": self.tpb, "grid": 16,
                 "alpha": "bf16 0.1", "input": "rand*10-5 bf16", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
-        n = min(self.n, 1 << 26)
-        x = torch.rand(n, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16) * 10.0 - 5.0
+        x = torch.rand(self.n, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16) * 10.0 - 5.0
         alpha = torch.tensor(0.1, dtype=torch.bfloat16)
-        secs = _time_cpu(lambda: cpu_golden.leaky_relu(x, alpha))
-        return _cpu(round(4.0 * n / secs / 1e9, 3), "GB/s",
-                    "torch.where(x >= 0, x, x * alpha) (test_leaky_relu.py:47)", f"{n} bf16 elements", secs)
+        return _cpu(self.work(), 1e9, "GB/s", "torch.where(x >= 0, x, x * alpha) (test_leaky_relu.py:47)",
+                    f"the full workload, {self.n} bf16 elements",
+                    _time_cpu(lambda: cpu_golden.leaky_relu(x, alpha), min_total_s))
 
 
 class VMulAdd(Workload):
@@ -397,16 +396,15 @@ class VMulAdd(Workload):
         return {"workload": self.name, "size": self.n, "tile_size": 32, "tile_per_block": self.tpb, "grid": 16,
                 "input": "rand*10 fp32, seed 0", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
-        n = min(self.n, 1 << 26)
         g = torch.Generator().manual_seed(0)
-        x, y, z = (torch.rand(n, generator=g) * 10 for _ in range(3))
-        secs = _time_cpu(lambda: cpu_golden.vmuladd(x, y, z))
-        return _cpu(round(16.0 * n / secs / 1e9, 3), "GB/s",
+        x, y, z = (torch.rand(self.n, generator=g) * 10 for _ in range(3))
+        return _cpu(self.work(), 1e9, "GB/s",
                     "x * y + z, unfused (test_vmuladd.py:52's numpy golden, evaluated with torch)",
-                    f"{n} fp32 elements", secs)
+                    f"the full workload, {self.n} fp32 elements",
+                    _time_cpu(lambda: cpu_golden.vmuladd(x, y, z), min_total_s))
 
 
 class Gelu(Workload):
@@ -437,13 +435,13 @@ class Gelu(Workload):
         return {"workload": self.name, "rows": self.rows, "cols": self.cols, "tile_size": self.cols, "grid": 16,
                 "approximate": self.approximate, "input": "randn*2 fp32", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
         x = torch.randn(self.rows, self.cols, generator=torch.Generator().manual_seed(1)) * 2.0
-        secs = _time_cpu(lambda: cpu_golden.gelu(x, self.approximate))
-        return _cpu(round(self.work() / secs / 1e9, 3), "GB/s", "test_gelu.py:44-48 golden",
-                    f"the full {self.rows}x{self.cols} input", secs)
+        return _cpu(self.work(), 1e9, "GB/s", "test_gelu.py:44-48 golden",
+                    f"the full {self.rows}x{self.cols} workload",
+                    _time_cpu(lambda: cpu_golden.gelu(x, self.approximate), min_total_s))
 
 
 class RmsNorm(Workload):
@@ -475,14 +473,14 @@ class RmsNorm(Workload):
         return {"workload": self.name, "rows": self.rows, "cols": self.cols, "epsilon": 1e-6,
                 "input": "randn*2 fp32, gamma rand+0.5", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         g = torch.Generator().manual_seed(1)
         x = torch.randn(self.rows, self.cols, generator=g) * 2.0
         gamma = torch.rand(self.cols, generator=g) + 0.5
-        secs = _time_cpu(lambda: torch.nn.functional.rms_norm(x, [self.cols], gamma, eps=1e-6))
-        return _cpu(round(self.work() / secs / 1e9, 3), "GB/s", "torch.nn.functional.rms_norm(x, [C], gamma, 1e-6)",
-                    f"the full {self.rows}x{self.cols} input", secs)
+        return _cpu(self.work(), 1e9, "GB/s", "torch.nn.functional.rms_norm(x, [C], gamma, 1e-6)",
+                    f"the full {self.rows}x{self.cols} workload",
+                    _time_cpu(lambda: torch.nn.functional.rms_norm(x, [self.cols], gamma, eps=1e-6), min_total_s))
 
 
 class ReduceRows(Workload):
@@ -512,12 +510,11 @@ class ReduceRows(Workload):
         return {"workload": self.name, "rows": self.rows, "cols": self.cols, "op": "sum", "dim": 1,
                 "input": "randn*2 fp32", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         x = torch.randn(self.rows, self.cols, generator=torch.Generator().manual_seed(1)) * 2.0
-        secs = _time_cpu(lambda: torch.sum(x, 1))
-        return _cpu(round(self.work() / secs / 1e9, 3), "GB/s", "torch.sum(x, 1) (test_reduce_ops.py golden)",
-                    f"the full {self.rows}x{self.cols} input (256 MiB; the host caches may hold part of it)", secs)
+        return _cpu(self.work(), 1e9, "GB/s", "torch.sum(x, 1) (test_reduce_ops.py golden)",
+                    f"the full {self.rows}x{self.cols} workload", _time_cpu(lambda: torch.sum(x, 1), min_total_s))
 
 
 class Matmul(Workload):
@@ -563,13 +560,12 @@ class Matmul(Workload):
             cfg.update({"out": "f32", "epilogue": "leaky_relu(acc + bias[n], 0.001)"})
         return cfg
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
-        rows = 512  # a row band of A against all of B: 1/16 of the FLOPs of the full product
         td = getattr(torch, self.dt)
         g = torch.Generator().manual_seed(2)
-        a = (torch.randn(rows, self.n, generator=g) / math.sqrt(self.n)).to(td)
+        a = (torch.randn(self.n, self.n, generator=g) / math.sqrt(self.n)).to(td)
         b = (torch.randn(self.n, self.n, generator=g) / math.sqrt(self.n)).to(td)
         if self.bias_leaky:
             bias = torch.randn(self.n, generator=g)
@@ -582,9 +578,7 @@ class Matmul(Workload):
             def run():
                 return cpu_golden.matmul(a, b)
             expr = "a.to(float32) @ b.to(float32) (python/test/asc2/kernels/test_matmul_tiled.py:49)"
-        secs = _time_cpu(run)
-        return _cpu(round(2.0 * rows * self.n * self.n / secs / 1e12, 4), "TFLOP/s", expr,
-                    f"rows 0..{rows - 1} of A ({rows}x{self.n}x{self.n})", secs)
+        return _cpu(self.work(), 1e12, "TFLOP/s", expr, f"the full {self.n}^3 workload", _time_cpu(run, min_total_s))
 
 
 class MatmulI8(Workload):
@@ -620,19 +614,18 @@ class MatmulI8(Workload):
                 "epilogue": "fp16(fp32(acc) * scale[n])", "input": "int8 uniform[-127,127], seed 3",
                 "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
-        rows = 64  # a row band: 1/64 of the full product's operations
         g = torch.Generator().manual_seed(3)
-        a = torch.randint(-127, 128, (rows, self.K), dtype=torch.int8, generator=g)
+        a = torch.randint(-127, 128, (self.M, self.K), dtype=torch.int8, generator=g)
         b = torch.randint(-127, 128, (self.K, self.N), dtype=torch.int8, generator=g)
         scale = torch.rand(self.N, generator=g) * 0.009 + 0.001
-        secs = _time_cpu(lambda: cpu_golden.dequant(cpu_golden.matmul_i8(a, b), scale))
-        return _cpu(round(2.0 * rows * self.N * self.K / secs / 1e12, 5), "TOPS",
+        return _cpu(self.work(), 1e12, "TOPS",
                     "(a.to(int32) @ b.to(int32)) then (acc.float() * scale).half() "
                     "(test_matmul_iterate_all.py:116; dequant of test_matmul_quant.py)",
-                    f"rows 0..{rows - 1} of A ({rows}x{self.N}x{self.K})", secs)
+                    f"the full {self.M}x{self.N}x{self.K} workload",
+                    _time_cpu(lambda: cpu_golden.dequant(cpu_golden.matmul_i8(a, b), scale), min_total_s))
 
 
 class FlashAttention(Workload):
@@ -667,23 +660,22 @@ class FlashAttention(Workload):
                 "causal": self.causal, "sm_scale": 1 / math.sqrt(self.D), "input": "bf16 randn, seed 4",
                 "flop_convention": "4*B*H*S^2*D, halved for causal", "rotating_sets": len(self.sets)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, min_total_s: float = CPU_MIN_S):
         import torch
         from oracle import cpu_golden
-        heads = 2  # (batch, head) slices, each the full S x S problem
         g = torch.Generator().manual_seed(4)
-        q, k, v = [torch.randn(heads, self.S, self.D, generator=g).to(torch.bfloat16) for _ in range(3)]
+        shape = (self.B * self.H, self.S, self.D)
+        q, k, v = [torch.randn(*shape, generator=g).to(torch.bfloat16) for _ in range(3)]
         scale = 1 / math.sqrt(self.D)
 
         def run():
-            for i in range(heads):
+            for i in range(shape[0]):
                 cpu_golden.attention(q[i], k[i], v[i], scale, self.causal)
 
-        secs = _time_cpu(run)
-        work = heads * 4.0 * self.S * self.S * self.D * (0.5 if self.causal else 1.0)
-        return _cpu(round(work / secs / 1e12, 4), "TFLOP/s",
+        return _cpu(self.work(), 1e12, "TFLOP/s",
                     "fp32 softmax((q @ k.T) * scale [+ causal mask]) @ v per (batch, head) slice",
-                    f"{heads} slices of S={self.S}, D={self.D}, same FLOP convention", secs)
+                    f"the full workload, {shape[0]} (batch, head) slices of S={self.S}, D={self.D}, "
+                    "same FLOP convention", _time_cpu(run, min_total_s))
 
 
 WORKLOADS = {
@@ -959,7 +951,7 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    cpu = None if args.no_cpu else head.cpu_baseline()
+    cpu = None if args.no_cpu else head.cpu_baseline(CPU_HEADLINE_S)
     line = {
         "metric": METRIC,
         "value": round(res["value"], 3),

@@ -171,7 +171,7 @@ def mfma(folder: str) -> int:
       clock            = cycles per XCD / kernel duration
       MFMA busy        = SQ_VALU_MFMA_BUSY_CYCLES / (cycles per XCD x CUs x 4 SIMDs)
     and the achieved rate at 100 % busy is the MFMA peak scaled by clock / 2.4 GHz."""
-    info = bench_device_info(folder)
+    cus, xcds, info = device_shape(folder)
     lines = [
         "# MFMA utilisation and shader clock (rocprofv3 PMC), one MI355X", "",
         "Generated by `python profile_summary.py mfma DIR` from one counter pass per workload "
@@ -192,7 +192,6 @@ def mfma(folder: str) -> int:
         "peak at this clock | achieved (bench FLOP / duration) | achieved / peak at this clock |",
         "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|",
     ]
-    cus, xcds = info_cus(folder), 8
     for key, make in bench.WORKLOADS.items():
         d = os.path.join(folder, f"{key}_MFMA")
         if not os.path.isdir(d):
@@ -227,31 +226,25 @@ def mfma(folder: str) -> int:
     return 0
 
 
-def _agent_rows(folder: str):
+def _gpu_agent(folder: str) -> dict:
+    """The GPU row of rocprofv3's agent_info.csv under ``folder``."""
     for path in glob.glob(os.path.join(folder, "**", "*agent_info.csv"), recursive=True):
         with open(path, newline="") as f:
             for r in csv.DictReader(f):
-                if r.get("Agent_Type", r.get("Type", "")).upper().endswith("GPU") or "gfx" in json.dumps(r):
+                if r.get("Agent_Type") == "GPU":
                     return r
     return {}
 
 
-def info_cus(folder: str) -> int:
-    for d in glob.glob(os.path.join(folder, "*")):
-        r = _agent_rows(d)
-        for key in ("Cu_Count", "CU_Count", "Compute_Unit_Count", "Cu_Count_Per_Xcc"):
-            if r.get(key):
-                v = int(r[key])
-                return v * 8 if key.endswith("Per_Xcc") else v
-    return 256
-
-
-def bench_device_info(folder: str) -> str:
-    for d in glob.glob(os.path.join(folder, "*")):
-        r = _agent_rows(d)
+def device_shape(folder: str):
+    """(CUs, XCDs, description) of the profiled GPU (256, 8 for MI355X)."""
+    for d in sorted(glob.glob(os.path.join(folder, "*"))):
+        r = _gpu_agent(d)
         if r:
-            return f"{r.get('Name', r.get('Gfx_Target_Version', 'gfx950'))}, {info_cus(folder)} CUs, 8 XCDs"
-    return "gfx950, 256 CUs, 8 XCDs"
+            cus, xcds = int(r.get("Cu_Count") or 256), int(r.get("Num_Xcc") or 8)
+            return cus, xcds, (f"{r.get('Name') or 'gfx950'}, {cus} CUs in {xcds} XCDs, max engine clock "
+                               f"{r.get('Max_Engine_Clk_Fcompute', '?')} MHz")
+    return 256, 8, "gfx950, 256 CUs in 8 XCDs"
 
 
 def main(argv) -> int:
