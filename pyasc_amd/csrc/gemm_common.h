@@ -8,6 +8,7 @@ namespace asc {
 namespace gemm {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // LDS tiles are stored as rows of 8 chunks of 16 bytes (128 bytes per row, K
 // contiguous).  The chunk index is XOR-swizzled with
@@ -70,8 +71,6 @@ __device__ __forceinline__ void transpose4x4_b8(uint32_t x0, uint32_t x1, uint32
   y3 = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);
 }
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
 // 8-bit 16x8 transpose: in[r] (r < 16) holds 8 consecutive columns of row r;
 // out[c] (c < 8) receives the 16 rows of column c.
 __device__ __forceinline__ void transpose16x8_b8(const u32x2 (&in)[16], u32x4 (&out)[8]) {
@@ -85,6 +84,96 @@ __device__ __forceinline__ void transpose16x8_b8(const u32x2 (&in)[16], u32x4 (&
       out[4 * w + 1][q] = y1;
       out[4 * w + 2][q] = y2;
       out[4 * w + 3][q] = y3;
+    }
+  }
+}
+
+// ---- epilogue stores through quad transposes ------------------------------
+// A 32x32 MFMA result block leaves lane l with column l%32 and, in registers
+// 4g..4g+3, rows 8g + 4*(l/32) + 0..3.  Storing straight from that layout
+// writes one element per lane per instruction.  Inside each quad of lanes
+// (4q..4q+3, consecutive columns) the 4 registers of group g form a 4x4 block;
+// transposing it (two lane exchanges, xor 2 then xor 1) leaves lane 4q+t with
+// row 8g + 4*(l/32) + t, columns 4q..4q+3: one 8-byte (16-bit output) or
+// 16-byte (32-bit output) store per lane and group, a quarter of the
+// instructions.
+__device__ __forceinline__ uint32_t quad_xor1(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ uint32_t quad_xor2(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, true));
+}
+
+// 16-bit values: on entry d0 = (v0 | v1 << 16), d1 = (v2 | v3 << 16) with v_k the
+// element of row k, column t (t = lane % 4); on exit the same packing holds the
+// elements of row t, columns 0..3.
+__device__ __forceinline__ void quad_transpose_b16(uint32_t& d0, uint32_t& d1, int t) {
+  const bool hi2 = (t & 2) != 0;
+  const uint32_t recv = quad_xor2(hi2 ? d0 : d1);
+  if (hi2) {
+    d0 = recv;  // rows 2,3 of column t-2
+  } else {
+    d1 = recv;  // rows 0,1 of column t+2
+  }
+  const bool odd = (t & 1) != 0;
+  // even lanes send the high halves (the odd partner's row), odd lanes the low halves
+  const uint32_t r = quad_xor1(odd ? __builtin_amdgcn_perm(d1, d0, 0x05040100u)
+                                   : __builtin_amdgcn_perm(d1, d0, 0x07060302u));
+  const uint32_t e0 = __builtin_amdgcn_perm(r, d0, 0x05040100u), e1 = __builtin_amdgcn_perm(r, d1, 0x07060100u);
+  const uint32_t o0 = __builtin_amdgcn_perm(d0, r, 0x07060100u), o1 = __builtin_amdgcn_perm(d1, r, 0x07060302u);
+  d0 = odd ? o0 : e0;
+  d1 = odd ? o1 : e1;
+}
+
+// 32-bit values: v[k] = element (row k, column t) on entry, (row t, column k) on exit.
+__device__ __forceinline__ void quad_transpose_b32(uint32_t (&v)[4], int t) {
+  const bool hi2 = (t & 2) != 0;
+  const uint32_t s0 = quad_xor2(hi2 ? v[0] : v[2]);
+  const uint32_t s1 = quad_xor2(hi2 ? v[1] : v[3]);
+  const uint32_t a0 = hi2 ? s0 : v[0], a1 = hi2 ? s1 : v[1], a2 = hi2 ? v[2] : s0, a3 = hi2 ? v[3] : s1;
+  const bool odd = (t & 1) != 0;
+  const uint32_t r0 = quad_xor1(odd ? a0 : a1);
+  const uint32_t r1 = quad_xor1(odd ? a2 : a3);
+  v[0] = odd ? r0 : a0;
+  v[1] = odd ? a1 : r0;
+  v[2] = odd ? r1 : a2;
+  v[3] = odd ? a3 : r1;
+}
+
+// Stores a wave's 128 x (32 kJ) block of results (4 x kJ MFMA blocks, `acc`) at
+// c + (m_base, n_base) (row stride ldc elements) through the quad transposes,
+// with non-temporal stores (the results are not read again by this kernel).
+// conv(j, x) turns accumulator value x of block column j into the output bits
+// (the low 16 bits for 16-bit outputs).  Blocks of one row band go out
+// column-block after column-block, so each row's outputs leave in consecutive
+// instructions.  Every element must be in bounds.
+template <int kOutBytes, int kJ, class AccT, class Conv>
+__device__ __forceinline__ void store_wave_tile(const AccT (&acc)[4][kJ], Conv conv, void* c, int64_t ldc, int m_base,
+                                                int n_base, int lane) {
+  static_assert(kOutBytes == 2 || kOutBytes == 4, "16- or 32-bit outputs");
+  const int t = lane & 3, q = (lane & 31) >> 2, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t row = m_base + i * 32 + g * 8 + h * 4 + t;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int64_t off = row * ldc + n_base + j * 32 + 4 * q;
+        if constexpr (kOutBytes == 2) {
+          uint32_t d0 = (conv(j, acc[i][j][4 * g + 0]) & 0xFFFFu) | (conv(j, acc[i][j][4 * g + 1]) << 16);
+          uint32_t d1 = (conv(j, acc[i][j][4 * g + 2]) & 0xFFFFu) | (conv(j, acc[i][j][4 * g + 3]) << 16);
+          quad_transpose_b16(d0, d1, t);
+          __builtin_nontemporal_store(u32x2{d0, d1}, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(c) + off));
+        } else {
+          uint32_t v[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = conv(j, acc[i][j][4 * g + k]);
+          quad_transpose_b32(v, t);
+          __builtin_nontemporal_store(u32x4{v[0], v[1], v[2], v[3]},
+                                      reinterpret_cast<u32x4*>(static_cast<uint32_t*>(c) + off));
+        }
+      }
     }
   }
 }

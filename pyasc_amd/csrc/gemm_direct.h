@@ -1,8 +1,10 @@
 // Direct-to-LDS MFMA GEMM main loop for tile-aligned shapes (the fast path of
 // matmul.hip and matmul_i8.hip; ragged shapes use gemm_core.h).
 //
-//   - 256x256 output tile per 256-thread workgroup; 4 waves in 2x2, each wave
-//     128x128 = 4x4 blocks of 32x32 MFMA accumulators (256 AGPRs).
+//   - 256x256 output tile per workgroup of 2 x kWavesN waves: with kWavesN = 2
+//     each wave owns 128x128 = 4x4 blocks of 32x32 MFMA accumulators (256
+//     AGPRs, one wave per SIMD); with kWavesN = 4 each owns 128x64 = 4x2 blocks
+//     (128 AGPRs), two waves per SIMD whose stalls the other covers.
 //   - A k-tile is 64 bytes of K (32 fp16/bf16 or 64 int8 elements): 2 MFMA
 //     k-steps.  Operands go from HBM straight into LDS (buffer_load ... lds,
 //     16 bytes per lane, 1 KiB per wave instruction): no staging registers, no
@@ -43,10 +45,8 @@ typedef int i32x2_t __attribute__((vector_size(8)));
 
 constexpr int kDirectStages = 5;
 constexpr int kDirectStageBytes = 32768;
-// loads a wave may leave in flight at a k-tile's barrier: tiles kt+3 .. kt+S-1
-constexpr int kDirectInFlight = 8 * (kDirectStages - 3);
 
-template <class Tr>
+template <class Tr, int kWavesN = 2>
 struct GemmDirectLoop {
   using Elem = typename Tr::Elem;
   using Acc = typename Tr::Acc;
@@ -55,6 +55,15 @@ struct GemmDirectLoop {
   static constexpr int kBRowBytes = 256 * kES;  // one B tile row (256 columns)
   static constexpr int kBRowsPerLoad = 1024 / kBRowBytes;
   static constexpr int kBOff = 16384;
+  static constexpr int kWaves = 2 * kWavesN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kJ = 8 / kWavesN;           // 32-column MFMA blocks per wave
+  static constexpr int kLoads = 16 / kWaves;       // 1 KiB load instructions per wave per operand and k-tile
+  // loads a wave may leave in flight at a k-tile's barrier: tiles kt+3 .. kt+S-1
+  static constexpr int kInFlight = 2 * kLoads * (kDirectStages - 3);
+  static constexpr int kMfmaPerStep = 4 * kJ;
+  static constexpr int kDsPerStep = 4 + 2 * kJ;
+  static_assert(kWavesN == 2 || kWavesN == 4, "2x2 or 2x4 waves");
 
   // A chunk swizzle (4 chunks per 64-byte row).  Chosen by measurement
   // (SQ_LDS_BANK_CONFLICT on the operand-read pattern): (row >> 2) & 3 reads
@@ -73,8 +82,8 @@ struct GemmDirectLoop {
   int lda_bytes, ldb_bytes;
   uint8_t* lds[kDirectStages];
   __amdgpu_buffer_rsrc_t rsrc_a, rsrc_b;
-  int voff_a[4];  // per A load instruction (the swizzle depends on the 16-row block)
-  int voff_b[2];  // per parity of the B load instruction
+  int voff_a[4];       // per A load instruction (the first kLoads are used)
+  int voff_b[2];       // per parity of the B load instruction
 
   __device__ __forceinline__ void init(int64_t lda, int64_t ldb) {
     lda_bytes = static_cast<int>(lda) * kES;
@@ -85,11 +94,11 @@ struct GemmDirectLoop {
                                                0x00020000);
     rsrc_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<Elem*>(b_cols), static_cast<short>(0), 0x7fffffff,
                                                0x00020000);
-    // A: instruction i of wave w loads rows 16R .. 16R+15, R = 4w + i; lane l ->
+    // A: instruction i of wave w loads rows 16R .. 16R+15, R = kLoads*w + i; lane l ->
     // row 16R + l/4, LDS position l%4 holding logical chunk (l%4) ^ ga(row).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int R = wave * 4 + i;
+    for (int i = 0; i < kLoads; ++i) {
+      const int R = wave * kLoads + i;
       const int row = 16 * R + (lane >> 2);
       const int c = (lane & 3) ^ ga(row);
       voff_a[i] = (lane >> 2) * lda_bytes + c * 16;
@@ -111,14 +120,14 @@ struct GemmDirectLoop {
     uint8_t* base = lds[kS];
     const int kb = k0 * kES;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int R = wave * 4 + i;
+    for (int i = 0; i < kLoads; ++i) {
+      const int R = wave * kLoads + i;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) void*)(base + R * 1024),
                                                16, voff_a[i], 16 * R * lda_bytes + kb, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int R = wave * 4 + i;
+    for (int i = 0; i < kLoads; ++i) {
+      const int R = wave * kLoads + i;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b,
                                                (__attribute__((address_space(3))) void*)(base + kBOff + R * 1024), 16,
                                                voff_b[i & 1], (k0 + kBRowsPerLoad * R) * ldb_bytes, 0, 0);
@@ -132,7 +141,7 @@ struct GemmDirectLoop {
   }
 
   template <int kS>
-  __device__ __forceinline__ void read_frags(int step, u32x4 (&fa)[4], u32x4 (&fbv)[4]) const {
+  __device__ __forceinline__ void read_frags(int step, u32x4 (&fa)[4], u32x4 (&fbv)[kJ]) const {
     const uint8_t* as = lds[kS];
     const uint8_t* bs = as + kBOff;
     const int h = lane >> 5;
@@ -145,8 +154,8 @@ struct GemmDirectLoop {
     }
     const int g = (lane >> 4) & 1, t = lane & 15;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nb = wn * 128 + j * 32 + 16 * g;
+    for (int j = 0; j < kJ; ++j) {
+      const int nb = wn * (32 * kJ) + j * 32 + 16 * g;
       if constexpr (kES == 2) {
         // k = 16*step + 8h + e; read e = 0..3 then 4..7; lane 4jj+q -> row +jj, col +4q
         const int row = step * 16 + 8 * h + (t >> 2);
@@ -171,11 +180,11 @@ struct GemmDirectLoop {
     }
   }
 
-  __device__ __forceinline__ static void mma(Acc (&acc)[4][4], const u32x4 (&fa)[4], const u32x4 (&fbv)[4]) {
+  __device__ __forceinline__ static void mma(Acc (&acc)[4][kJ], const u32x4 (&fa)[4], const u32x4 (&fbv)[kJ]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = Tr::mfma(fa[i], fbv[j], acc[i][j]);
+      for (int j = 0; j < kJ; ++j) acc[i][j] = Tr::mfma(fa[i], fbv[j], acc[i][j]);
   }
 
   // Workgroup barrier that does not wait for outstanding loads (unlike
@@ -185,54 +194,55 @@ struct GemmDirectLoop {
   // k-tile kt, held in stage kS.  On entry the k-step-0 fragments of tile kt
   // are in fa0/fb0, and tiles kt and kt+1 are visible in LDS.
   template <int kS>
-  __device__ __forceinline__ void iteration(int kt, int k_tiles, Acc (&acc)[4][4], u32x4 (&fa0)[4],
-                                            u32x4 (&fb0)[4], u32x4 (&fa1)[4], u32x4 (&fb1)[4]) {
+  __device__ __forceinline__ void iteration(int kt, int k_tiles, Acc (&acc)[4][kJ], u32x4 (&fa0)[4],
+                                            u32x4 (&fb0)[kJ], u32x4 (&fa1)[4], u32x4 (&fb1)[kJ]) {
     constexpr int kAheadTiles = kDirectStages - 1;
     constexpr int kNext = (kS + 1) % kDirectStages;
     constexpr int kAhead = (kS + kAheadTiles) % kDirectStages;  // the stage tile kt-1 has left
+    constexpr int kVmem = 2 * kLoads;
     // k-step 0: tile kt+4's loads (clamped: the tail re-loads the last tile
     // into a free stage) and k-step 1's operand reads, one per MFMA.
     issue_loads<kAhead>((kt + kAheadTiles < k_tiles ? kt + kAheadTiles : k_tiles - 1) * kBK);
     read_frags<kS>(1, fa1, fb1);
     mma(acc, fa0, fb0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kVmem; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (LDS DMA)
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kDsPerStep - kVmem; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    if constexpr (kMfmaPerStep > kDsPerStep) __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerStep - kDsPerStep, 0);
     // k-step 1: the next tile's k-step-0 operands, one read per MFMA
     read_frags<kNext>(0, fa0, fb0);
     mma(acc, fa1, fb1);
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
+    for (int i = 0; i < kDsPerStep; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+    if constexpr (kMfmaPerStep > kDsPerStep) __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerStep - kDsPerStep, 1);
     // own loads of tile kt+2 done (only the newer tiles' may still run), and
     // this wave's reads of stage kS complete before anyone reloads it
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"i"(kDirectInFlight) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"i"(kInFlight) : "memory");
     barrier();
   }
 
   // One pass over the ring: k-tiles kt .. kt+kDirectStages-1 in stages 0 ..
   template <int... kS>
-  __device__ __forceinline__ void ring(std::integer_sequence<int, kS...>, int kt, int k_tiles, Acc (&acc)[4][4],
-                                       u32x4 (&fa0)[4], u32x4 (&fb0)[4], u32x4 (&fa1)[4], u32x4 (&fb1)[4]) {
+  __device__ __forceinline__ void ring(std::integer_sequence<int, kS...>, int kt, int k_tiles, Acc (&acc)[4][kJ],
+                                       u32x4 (&fa0)[4], u32x4 (&fb0)[kJ], u32x4 (&fa1)[4], u32x4 (&fb1)[kJ]) {
     (iteration<kS>(kt + kS, k_tiles, acc, fa0, fb0, fa1, fb1), ...);
   }
   // The last k_tiles - kt (< kDirectStages) tiles, from stage 0.
   template <int... kS>
   __device__ __forceinline__ void ring_tail(std::integer_sequence<int, kS...>, int kt, int k_tiles,
-                                            Acc (&acc)[4][4], u32x4 (&fa0)[4], u32x4 (&fb0)[4], u32x4 (&fa1)[4],
-                                            u32x4 (&fb1)[4]) {
+                                            Acc (&acc)[4][kJ], u32x4 (&fa0)[4], u32x4 (&fb0)[kJ], u32x4 (&fa1)[4],
+                                            u32x4 (&fb1)[kJ]) {
     ((kt + kS < k_tiles ? iteration<kS>(kt + kS, k_tiles, acc, fa0, fb0, fa1, fb1) : void()), ...);
   }
 
@@ -241,17 +251,17 @@ struct GemmDirectLoop {
     (issue_loads<kS>((kS < k_tiles ? kS : k_tiles - 1) * kBK), ...);
   }
 
-  __device__ __forceinline__ void run(int K, Acc (&acc)[4][4]) {
+  __device__ __forceinline__ void run(int K, Acc (&acc)[4][kJ]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
+      for (int j = 0; j < kJ; ++j) acc[i][j] = Acc{};
     const int k_tiles = K / kBK;
     // tiles 0 .. kDirectStages-2 (clamped like the loop's), then wait for 0 and 1
     prologue(std::make_integer_sequence<int, kDirectStages - 1>(), k_tiles);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"i"(kDirectInFlight) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"(kInFlight) : "memory");
     barrier();
-    u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
+    u32x4 fa0[4], fb0[kJ], fa1[4], fb1[kJ];
     read_frags<0>(0, fa0, fb0);
     int kt = 0;
     for (; kt + kDirectStages <= k_tiles; kt += kDirectStages)

@@ -116,15 +116,62 @@ struct Tr16 {
   }
 };
 
+// Waves across the 256 columns of the fast path's tile: 2 (one wave per SIMD,
+// 128x128 accumulators each) or 4 (two waves per SIMD, 128x64 each).
+constexpr int kFastWavesN = 4;
+using FastLoopBf16 = asc::gemm::GemmDirectLoop<Tr16<true>, kFastWavesN>;
+constexpr int kFastThreads = FastLoopBf16::kThreads;
+
 template <bool kBf16, bool kChecked, int kOut>
-__global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(kChecked ? kThreads : kFastThreads, 1) gemm_mfma_kernel(GemmArgs p) {
   int tm, tn;
   asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, asc::gemm::kGroupM, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
-  const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
-  f32x16 acc[4][4];
-  if constexpr (kChecked) {
+  if constexpr (!kChecked) {
+    // the LDS stages as distinct objects (see gemm_direct.h)
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
+    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
+    using Loop = asc::gemm::GemmDirectLoop<Tr16<kBf16>, kFastWavesN>;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
+    Loop L;
+    L.a = p.a;
+    L.b = p.b;
+    L.m0 = m0;
+    L.n0 = n0;
+    L.lane = lane;
+    L.wave = wave;
+    L.wm = wave / kFastWavesN;
+    L.wn = wave % kFastWavesN;
+    L.lds[0] = lds0;
+    L.lds[1] = lds1;
+    L.lds[2] = lds2;
+    L.lds[3] = lds3;
+    L.lds[4] = lds4;
+    L.init(p.lda, p.ldb);
+    f32x16 acc[4][Loop::kJ];
+    L.run(p.K, acc);
+    // Epilogue: the whole tile is in bounds and C's rows are 16-byte aligned, so the
+    // results leave through quad-transposed wide stores.
+    const int n_base = n0 + L.wn * 32 * Loop::kJ;
+    float bias_n[Loop::kJ];
+#pragma unroll
+    for (int j = 0; j < Loop::kJ; ++j) bias_n[j] = p.epi.bias_at(n_base + j * 32 + (lane & 31));
+    const auto conv = [&](int j, float x) -> uint32_t {
+      const float v = p.epi(x, bias_n[j]);
+      if constexpr (kOut == kOutF32) return __float_as_uint(v);
+      else if constexpr (kOut == kOutF16) return asc::f32_to_f16_rne(v);
+      else return asc::f32_to_bf16_rne(v);
+    };
+    asc::gemm::store_wave_tile<kOut == kOutF32 ? 4 : 2, Loop::kJ>(acc, conv, p.c, p.ldc, m0 + L.wm * 128, n_base,
+                                                                   lane);
+  } else {
+    const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
+    f32x16 acc[4][4];
     __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kStageBytes];
     asc::gemm::GemmMainLoop<Tr16<kBf16>, true> L;
@@ -143,59 +190,29 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_mfma_kernel(GemmArgs p) {
     L.lds[0] = lds0;
     L.lds[1] = lds1;
     L.run(acc);
-  } else {
-    // the LDS stages as distinct objects (see gemm_direct.h)
-    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
-    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
-    asc::gemm::GemmDirectLoop<Tr16<kBf16>> L;
-    L.a = p.a;
-    L.b = p.b;
-    L.m0 = m0;
-    L.n0 = n0;
-    L.lane = lane;
-    L.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
-    L.wm = wm;
-    L.wn = wn;
-    L.lds[0] = lds0;
-    L.lds[1] = lds1;
-    L.lds[2] = lds2;
-    L.lds[3] = lds3;
-    L.lds[4] = lds4;
-    L.init(p.lda, p.ldb);
-    L.run(p.K, acc);
-  }
-
-  // Epilogue.  MFMA 32x32 result layout: lane holds column lane%32 of the block,
-  // register r holds row 8*(r/4) + 4*(lane/32) + r%4.
-  const int col_in = lane & 31;
-  const int row_q = (lane >> 5) * 4;
-  float bias_n[4];
+    // Epilogue.  MFMA 32x32 result layout: lane holds column lane%32 of the block,
+    // register r holds row 8*(r/4) + 4*(lane/32) + r%4.
+    const int col_in = lane & 31;
+    const int row_q = (lane >> 5) * 4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 128 + j * 32 + col_in;
-    bias_n[j] = (!kChecked || n < p.N) ? p.epi.bias_at(n) : 0.0f;
-  }
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 128 + j * 32 + col_in;
+        const float bias_n = n < p.N ? p.epi.bias_at(n) : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 128 + j * 32 + col_in;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
-        if (kChecked && (m >= p.M || n >= p.N)) continue;
-        const float v = p.epi(acc[i][j][r], bias_n[j]);
-        const int64_t off = static_cast<int64_t>(m) * p.ldc + n;
-        if constexpr (kOut == kOutF32) {
-          static_cast<float*>(p.c)[off] = v;
-        } else if constexpr (kOut == kOutF16) {
-          static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
-        } else {
-          static_cast<uint16_t*>(p.c)[off] = asc::f32_to_bf16_rne(v);
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
+          if (m >= p.M || n >= p.N) continue;
+          const float v = p.epi(acc[i][j][r], bias_n);
+          const int64_t off = static_cast<int64_t>(m) * p.ldc + n;
+          if constexpr (kOut == kOutF32) {
+            static_cast<float*>(p.c)[off] = v;
+          } else if constexpr (kOut == kOutF16) {
+            static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
+          } else {
+            static_cast<uint16_t*>(p.c)[off] = asc::f32_to_bf16_rne(v);
+          }
         }
       }
     }
@@ -307,7 +324,8 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__
 template <bool kBf16, bool kChecked, int kOut>
 int32_t launch_mfma(const GemmArgs& p, hipStream_t stream) {
   const int blocks = p.tiles_m * p.tiles_n;
-  hipLaunchKernelGGL((gemm_mfma_kernel<kBf16, kChecked, kOut>), dim3(blocks), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((gemm_mfma_kernel<kBf16, kChecked, kOut>), dim3(blocks), dim3(kChecked ? kThreads : kFastThreads),
+                     0, stream, p);
   return asc::check_launch("asc_matmul");
 }
 
@@ -401,7 +419,11 @@ int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const vo
                        (lda % 8) == 0 && (ldb % 8) == 0;
   // the direct-to-LDS path addresses each operand with 31-bit buffer offsets
   const bool offsets_fit = (BM * lda + K) * 2 < (int64_t{1} << 31) && (K + 64) * ldb * 2 < (int64_t{1} << 31);
-  const bool fast = aligned && offsets_fit && (M % BM) == 0 && (N % BN) == 0 && (K % 32) == 0 && K > 0;
+  // the fast path's epilogue stores 8 (16-bit C) or 16 (fp32 C) bytes per lane at 4-column steps
+  const int64_t out_bytes = out_dtype == ASC_DT_FLOAT32 ? 4 : 2;
+  const bool c_rows_aligned = (reinterpret_cast<uintptr_t>(c) & 15) == 0 && (ldc * out_bytes) % 16 == 0;
+  const bool fast = aligned && c_rows_aligned && offsets_fit && (M % BM) == 0 && (N % BN) == 0 && (K % 32) == 0 &&
+                    K > 0;
   // K == 0 takes the checked kernel: no k-tile runs and C receives cast(0).
   return in_dtype == ASC_DT_BFLOAT16 ? dispatch_out<true>(p, out_dtype, fast, s)
                                      : dispatch_out<false>(p, out_dtype, fast, s);

@@ -93,16 +93,66 @@ struct TrI8 {
   }
 };
 
+// Waves across the 256 columns of the fast path's tile: 2 (one wave per SIMD,
+// 128x128 accumulators each) or 4 (two waves per SIMD, 128x64 each).
+constexpr int kFastWavesN = 4;
+using FastLoop = asc::gemm::GemmDirectLoop<TrI8, kFastWavesN>;
+constexpr int kFastThreads = FastLoop::kThreads;
+
+// fp32 scale of column n (optionally with its low 13 mantissa bits cleared)
+__device__ __forceinline__ float load_scale(const I8Args& p, int n) {
+  float s = p.scale[n];
+  if (p.trunc19) s = __uint_as_float(__float_as_uint(s) & 0xFFFFE000u);
+  return s;
+}
+
 // kMode: 0 = int32 accumulators, 1 = fp16 dequant
 template <bool kChecked, int kMode>
-__global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
+__global__ void __launch_bounds__(kChecked ? kThreads : kFastThreads, 1) gemm_i8_kernel(I8Args p) {
   int tm, tn;
   asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, asc::gemm::kGroupM, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
-  const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
-  i32x16 acc[4][4];
-  if constexpr (kChecked) {
+  if constexpr (!kChecked) {
+    // the LDS stages as distinct objects (see gemm_direct.h)
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
+    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
+    FastLoop L;
+    L.a = p.a;
+    L.b = p.b;
+    L.m0 = m0;
+    L.n0 = n0;
+    L.lane = lane;
+    L.wave = wave;
+    L.wm = wave / kFastWavesN;
+    L.wn = wave % kFastWavesN;
+    L.lds[0] = lds0;
+    L.lds[1] = lds1;
+    L.lds[2] = lds2;
+    L.lds[3] = lds3;
+    L.lds[4] = lds4;
+    L.init(p.K, p.N);
+    i32x16 acc[4][FastLoop::kJ];
+    L.run(p.K, acc);
+    // Epilogue: the whole tile is in bounds and C's rows are 16-byte aligned, so the
+    // results leave through quad-transposed wide stores.
+    const int n_base = n0 + L.wn * 32 * FastLoop::kJ;
+    float scale_n[FastLoop::kJ];
+#pragma unroll
+    for (int j = 0; j < FastLoop::kJ; ++j) scale_n[j] = kMode == 1 ? load_scale(p, n_base + j * 32 + (lane & 31)) : 0.f;
+    const auto conv = [&](int j, int32_t x) -> uint32_t {
+      if constexpr (kMode == 0) return static_cast<uint32_t>(x);
+      else return asc::f32_to_f16_rne(asc::materialize(static_cast<float>(x) * scale_n[j]));
+    };
+    asc::gemm::store_wave_tile<kMode == 0 ? 4 : 2, FastLoop::kJ>(acc, conv, p.c, p.N, m0 + L.wm * 128, n_base, lane);
+  } else {
+    const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
+    i32x16 acc[4][4];
     __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kStageBytes];
     asc::gemm::GemmMainLoop<TrI8, true> L;
@@ -120,58 +170,27 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
     L.lds[0] = lds0;
     L.lds[1] = lds1;
     L.run(acc);
-  } else {
-    // the LDS stages as distinct objects (see gemm_direct.h)
-    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
-    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
-    asc::gemm::GemmDirectLoop<TrI8> L;
-    L.a = p.a;
-    L.b = p.b;
-    L.m0 = m0;
-    L.n0 = n0;
-    L.lane = lane;
-    L.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
-    L.wm = wm;
-    L.wn = wn;
-    L.lds[0] = lds0;
-    L.lds[1] = lds1;
-    L.lds[2] = lds2;
-    L.lds[3] = lds3;
-    L.lds[4] = lds4;
-    L.init(p.K, p.N);
-    L.run(p.K, acc);
-  }
-
-  // Epilogue: lane holds column lane%32 of each 32x32 block, register r row
-  // 8*(r/4) + 4*(lane/32) + r%4.
-  const int col_in = lane & 31;
-  const int row_q = (lane >> 5) * 4;
+    // Epilogue: lane holds column lane%32 of each 32x32 block, register r row
+    // 8*(r/4) + 4*(lane/32) + r%4.
+    const int col_in = lane & 31;
+    const int row_q = (lane >> 5) * 4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 128 + j * 32 + col_in;
-    float s = 0.f;
-    if constexpr (kMode == 1) {
-      if (!kChecked || n < p.N) {
-        s = p.scale[n];
-        if (p.trunc19) s = __uint_as_float(__float_as_uint(s) & 0xFFFFE000u);
-      }
-    }
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 128 + j * 32 + col_in;
+      const float s = (kMode == 1 && n < p.N) ? load_scale(p, n) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
-        if (kChecked && (m >= p.M || n >= p.N)) continue;
-        const int64_t off = static_cast<int64_t>(m) * p.N + n;
-        if constexpr (kMode == 0) {
-          static_cast<int32_t*>(p.c)[off] = acc[i][j][r];
-        } else {
-          const float v = asc::materialize(static_cast<float>(acc[i][j][r]) * s);
-          static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
+          if (m >= p.M || n >= p.N) continue;
+          const int64_t off = static_cast<int64_t>(m) * p.N + n;
+          if constexpr (kMode == 0) {
+            static_cast<int32_t*>(p.c)[off] = acc[i][j][r];
+          } else {
+            const float v = asc::materialize(static_cast<float>(acc[i][j][r]) * s);
+            static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
+          }
         }
       }
     }
@@ -180,7 +199,8 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_i8_kernel(I8Args p) {
 
 template <bool kChecked, int kMode>
 int32_t launch(const I8Args& p, hipStream_t stream, const char* who) {
-  hipLaunchKernelGGL((gemm_i8_kernel<kChecked, kMode>), dim3(p.tiles_m * p.tiles_n), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((gemm_i8_kernel<kChecked, kMode>), dim3(p.tiles_m * p.tiles_n),
+                     dim3(kChecked ? kThreads : kFastThreads), 0, stream, p);
   return asc::check_launch(who);
 }
 
@@ -206,7 +226,9 @@ int32_t run(const int8_t* a, const int8_t* b, const float* scale, void* c, int64
   p.tiles_n = static_cast<int>((N + BN - 1) / BN);
   // the direct-to-LDS path addresses each operand with 31-bit buffer offsets
   const bool offsets_fit = (BM * K + K) < (int64_t{1} << 31) && (K + 128) * N < (int64_t{1} << 31);
-  const bool fast = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 && offsets_fit &&
+  // (the fast path's epilogue also stores 8 or 16 bytes per lane: C must be 16-byte aligned)
+  const bool fast = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                      reinterpret_cast<uintptr_t>(c)) & 15) == 0 && offsets_fit &&
                     (M % BM) == 0 && (N % BN) == 0 && (K % 64) == 0 && K > 0;
   if (mode == 0) return fast ? launch<false, 0>(p, stream, who) : launch<true, 0>(p, stream, who);
   return fast ? launch<false, 1>(p, stream, who) : launch<true, 1>(p, stream, who);
