@@ -135,9 +135,15 @@ int32_t asc_gelu_rows_f32(const float* x, float* out, int64_t num_rows,
  * columns are replaced by exp(x - max) / sum(exp(x - max)) (the reference
  * divides, lib/Conversion/LowerToAsc/LowerArithBinary.cpp:116; here one
  * correctly rounded reciprocal per row and a multiply, within 2 ulp of the
- * quotient); columns >= tile_size are untouched.  tile_size must be <= num_cols: with tile_size > num_cols the
- * reference's reduction counts the zero padding and its store spills into the
- * next row, which is rejected here (ASC_ERR_UNSUPPORTED). */
+ * quotient); columns >= tile_size are untouched.
+ * tile_size > num_cols: the reference's load right-pads the tile with zeros
+ * (lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:181-222) and its
+ * reductions count the whole tile (lib/Conversion/LowerToAsc/LowerAscTile.cpp:
+ * 428-459), so row i gets exp(x - m) / s with m = max(max x, 0) and
+ * s = sum exp(x - m) + (tile_size - num_cols) * exp(-m).  The reference's store
+ * also spills the padded values into the next row, racing with that row's own
+ * store across blocks; here each row writes its own num_cols values (the result
+ * of the rows running in order on one block). */
 int32_t asc_softmax_rows_f32(const float* x, float* out, int64_t num_rows,
                              int64_t num_cols, int32_t tile_size, int32_t grid,
                              asc_stream_t stream);

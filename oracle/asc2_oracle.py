@@ -10,7 +10,9 @@ How each function is pinned (tests/test_oracle.py):
                   kernel body, IEEE/two's-complement known answers, torch's own
                   float16/bfloat16 add.
   softmax_*       closed forms (constant row -> 1/n, two-point rows), shift
-                  invariance, row sums, torch.softmax (the reference's golden).
+                  invariance, row sums, torch.softmax (the reference's golden);
+                  tiles wider than the row: torch.softmax of the explicitly
+                  zero-padded row, a zero row -> 1/tile, tile == cols unchanged.
   matmul          identity / permutation products, a pure-Python fp64 loop on
                   tiny shapes, torch fp32 matmul (the reference's golden).
   mnblock cover   hand-derived rectangles, full coverage of the reference test's
@@ -264,16 +266,23 @@ def softmax_row_f16(row: np.ndarray) -> np.ndarray:
 def softmax_rows(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, tile_size: int,
                  grid: int) -> np.ndarray:
     """test_softmax.py:16-27: rows i = b, b+grid, ... for b < grid; the first ``tile_size``
-    columns of each row are replaced; ``tile_size > num_cols`` is rejected (the reference
-    would count the zero padding, LowerAscTile.cpp:428-459, and spill its store)."""
-    if tile_size > num_cols:
-        raise ValueError("tile_size > num_cols is not supported")
+    columns of each row are replaced.  With ``tile_size > num_cols`` the [1, tile] load
+    right-pads the row with the pad value 0 (LowerAscTileDataTransfer.cpp:181-222) and the
+    reductions run over the whole tile (LowerAscTile.cpp:428-459): the softmax of the
+    padded row, whose first num_cols values are the row's result.  (The reference's store
+    also spills the padded values into the next row, where they race with that row's own
+    store across blocks; the row's own values are what an in-order run leaves, and what
+    is written here.)"""
     x2 = x.reshape(-1)[:num_rows * num_cols].reshape(num_rows, num_cols)
     res = out.copy().reshape(-1)
     res2 = res[:num_rows * num_cols].reshape(num_rows, num_cols)
+    pad = max(0, tile_size - num_cols)
     for b in range(grid):
         for i in range(b, num_rows, grid):
-            res2[i, :tile_size] = softmax_row(x2[i, :tile_size])
+            tile = x2[i, :tile_size]
+            if pad:
+                tile = np.concatenate([tile, np.zeros(pad, dtype=tile.dtype)])
+            res2[i, :min(tile_size, num_cols)] = softmax_row(tile)[:min(tile_size, num_cols)]
     return res.reshape(out.shape)
 
 

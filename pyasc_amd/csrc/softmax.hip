@@ -345,6 +345,65 @@ bool rows_aligned16(const void* x, const void* out, int64_t stride, int64_t len)
   return asc::aligned16(x) && asc::aligned16(out) && (stride % 8) == 0 && (len % 8) == 0;
 }
 
+// ---- tiles wider than the row (test_softmax.py's softmax_kernel with tile_size >
+// num_cols).  The reference's load right-pads the [1, tile] tile with the pad value 0
+// (lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:181-222) and its reductions
+// count the whole tile (lib/Conversion/LowerToAsc/LowerAscTile.cpp:428-459), so each
+// row's statistics include pad = tile - num_cols zeros:
+//   m = max(max_j x_j, 0),  s = sum_j exp(x_j - m) + pad * exp(-m),  out_j = exp(x_j - m) / s.
+// Its store then writes the whole tile from the row's start, spilling pad values
+// into the next row, where they race with that row's own store whenever the two rows
+// run on different blocks; here every row writes its own num_cols values only (what
+// running the rows in order on one block leaves).  One 256-thread workgroup per row
+// (grid-stride), three passes; not a tuned path.
+template <bool kHalf>
+__device__ __forceinline__ float padded_at(const void* row, int64_t c) {
+  if constexpr (kHalf) return half_at(static_cast<const uint16_t*>(row), static_cast<int>(c));
+  else return static_cast<const float*>(row)[c];
+}
+
+template <bool kHalf>
+__global__ void __launch_bounds__(256) softmax_padded_kernel(const void* x, void* out, int64_t rows, int64_t cols,
+                                                             int32_t pad) {
+  __shared__ float red[2][4];
+  const int t = threadIdx.x;
+  constexpr int64_t kES = kHalf ? 2 : 4;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const void* row = static_cast<const uint8_t*>(x) + r * cols * kES;
+    float m = pad > 0 ? 0.0f : -INFINITY;  // the padding zeros take part in the maximum
+    for (int64_t c = t; c < cols; c += 256) m = fmaxf(m, padded_at<kHalf>(row, c));
+    m = asc::wave_max(m);
+    __syncthreads();
+    if ((t & 63) == 0) red[0][t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float s = 0.f;
+    for (int64_t c = t; c < cols; c += 256) s += exp_nonpos(padded_at<kHalf>(row, c) - m);
+    s = asc::wave_sum(s);
+    if ((t & 63) == 0) red[1][t >> 6] = s;
+    __syncthreads();
+    s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    s += static_cast<float>(pad) * exp_nonpos(0.0f - m);
+    const float rs = 1.0f / s;
+    for (int64_t c = t; c < cols; c += 256) {
+      const float v = exp_nonpos(padded_at<kHalf>(row, c) - m) * rs;
+      if constexpr (kHalf) static_cast<uint16_t*>(out)[r * cols + c] = to_half(v);
+      else static_cast<float*>(out)[r * cols + c] = v;
+    }
+  }
+}
+
+template <bool kHalf>
+int32_t launch_padded(const void* x, void* out, int64_t rows, int64_t cols, int32_t tile, hipStream_t stream,
+                      const char* who) {
+  if (rows == 0) return ASC_OK;
+  ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "%s: null buffer", who);
+  const int64_t blocks = rows < 65536 ? rows : 65536;
+  hipLaunchKernelGGL((softmax_padded_kernel<kHalf>), dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, x,
+                     out, rows, cols, static_cast<int32_t>(tile - cols));
+  return asc::check_launch(who);
+}
+
 }  // namespace
 
 extern "C" int32_t asc_softmax_rows_f32(const float* x, float* out, int64_t num_rows, int64_t num_cols,
@@ -353,10 +412,10 @@ extern "C" int32_t asc_softmax_rows_f32(const float* x, float* out, int64_t num_
               "asc_softmax_rows_f32: negative shape (%lld, %lld)", (long long)num_rows, (long long)num_cols);
   ASC_REQUIRE(tile_size > 0 && grid > 0, ASC_ERR_INVALID_ARG,
               "asc_softmax_rows_f32: need tile_size > 0 and grid > 0 (got %d, %d)", tile_size, grid);
-  ASC_REQUIRE(tile_size <= num_cols, ASC_ERR_UNSUPPORTED,
-              "asc_softmax_rows_f32: tile_size %d > num_cols %lld (the reference's padded reduction and "
-              "row-spilling store are not reproduced)",
-              tile_size, (long long)num_cols);
+  if (tile_size > num_cols) {
+    return launch_padded<false>(x, out, num_rows, num_cols, tile_size, static_cast<hipStream_t>(stream),
+                                "asc_softmax_rows_f32");
+  }
   if (num_rows == 0) return ASC_OK;
   ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_softmax_rows_f32: null buffer");
   // Rows b, b+grid, ... for b < grid cover every row exactly once.
@@ -385,10 +444,10 @@ extern "C" int32_t asc_softmax_rows_f16(const void* x, void* out, int64_t num_ro
               "asc_softmax_rows_f16: negative shape (%lld, %lld)", (long long)num_rows, (long long)num_cols);
   ASC_REQUIRE(tile_size > 0 && grid > 0, ASC_ERR_INVALID_ARG,
               "asc_softmax_rows_f16: need tile_size > 0 and grid > 0 (got %d, %d)", tile_size, grid);
-  ASC_REQUIRE(tile_size <= num_cols, ASC_ERR_UNSUPPORTED,
-              "asc_softmax_rows_f16: tile_size %d > num_cols %lld (the reference's padded reduction and "
-              "row-spilling store are not reproduced)",
-              tile_size, (long long)num_cols);
+  if (tile_size > num_cols) {
+    return launch_padded<true>(x, out, num_rows, num_cols, tile_size, static_cast<hipStream_t>(stream),
+                               "asc_softmax_rows_f16");
+  }
   if (num_rows == 0) return ASC_OK;
   ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_softmax_rows_f16: null buffer");
   RowView16 p{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), num_rows, num_cols, tile_size,

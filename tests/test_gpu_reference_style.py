@@ -76,6 +76,15 @@ def test_softmax(device):
     torch.testing.assert_close(out, torch.softmax(x, dim=1))
 
 
+def test_softmax_tile_wider_than_row(device):
+    # softmax_kernel with tile_size > num_cols: the padded tile's zeros enter max and sum
+    x = torch.rand((64, 1000), dtype=torch.float32)
+    out = torch.zeros_like(x)
+    softmax_kernel[16](x, out, 64, 1000, tile_size=1024)
+    padded = torch.nn.functional.pad(x.double(), (0, 24))
+    torch.testing.assert_close(out, torch.softmax(padded, dim=1)[:, :1000].float(), rtol=1e-6, atol=0)
+
+
 def test_softmax_fused(device):
     @asc2.jit(always_compile=True)
     def softmax_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: int,

@@ -64,6 +64,24 @@ def test_partial_tile_leaves_columns(device):
     np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=RTOL, atol=0)
 
 
+@pytest.mark.parametrize("rows,cols,tile", [(64, 1024, 2048), (37, 1000, 1024), (5, 3, 64), (300, 1, 2),
+                                            (9, 4096, 5000)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_tile_wider_than_row_vs_oracle(device, rows, cols, tile, dtype):
+    # the reference's padded load and whole-tile reductions: each row's max and sum include
+    # tile - cols zeros; the row's own cols outputs are written
+    x = (_rand(rows, cols, cols, scale=0.5)).to(dtype)
+    out = torch.full((rows, cols), 7.0, dtype=dtype, device=device)
+    kernels.softmax_rows(x.to(device), out, rows, cols, tile, 16)
+    torch.cuda.synchronize()
+    expected = O.softmax_rows(x.numpy(), np.zeros((rows, cols), x.numpy().dtype), rows, cols, tile, 16)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=RTOL, atol=0)
+    else:  # within one float16 ulp of the exact padded softmax
+        np.testing.assert_allclose(out.cpu().float().numpy(), expected.astype(np.float32), rtol=2 ** -10, atol=0)
+    assert (out.double().sum(1).cpu() < 1).all()
+
+
 @pytest.mark.parametrize("rows,cols,block,grid", [(64, 1024, 4, 16), (100, 333, 7, 10), (10, 4096, 3, 2),
                                                   (16384, 1024, 1024, 16)])
 def test_fused_blocks_coverage(device, rows, cols, block, grid):

@@ -131,8 +131,33 @@ def test_softmax_fixture_and_partial_columns():
     np.testing.assert_array_equal(got[:, 512:], 5.0)
     np.testing.assert_allclose(got[:, :512], torch.softmax(torch.from_numpy(f["x"][:, :512]), 1).numpy(),
                                rtol=1e-6, atol=0)
-    with pytest.raises(ValueError):
-        O.softmax_rows(f["x"], out, 64, 1024, 2048, 16)
+
+
+@pytest.mark.parametrize("rows,cols,tile", [(64, 1024, 2048), (7, 1000, 1024), (3, 5, 64), (5, 1, 2)])
+def test_softmax_tile_wider_than_row(rows, cols, tile):
+    # the padded load + whole-tile reductions: torch.softmax of the explicitly zero-padded row
+    # (a library routine on the tile the reference's load builds), first num_cols values kept
+    x = (torch.randn(rows, cols, generator=torch.Generator().manual_seed(cols)) * 0.5).numpy()
+    got = O.softmax_rows(x, np.zeros_like(x), rows, cols, tile, 16)
+    padded = torch.nn.functional.pad(torch.from_numpy(x), (0, tile - cols))
+    np.testing.assert_allclose(got, torch.softmax(padded, dim=1)[:, :cols].numpy(), rtol=3e-6, atol=1e-30)
+    np.testing.assert_allclose(got, torch.softmax(padded.double(), dim=1)[:, :cols].numpy(), rtol=1e-6, atol=0)
+    # the padding takes part in the sum: the row's own outputs sum to less than 1
+    assert (got.astype(np.float64).sum(1) < 1 - 1e-3).all()
+
+
+def test_softmax_tile_wider_than_row_closed_forms():
+    # a zero row padded to the tile: every element of the tile is 0, each output 1/tile
+    got = O.softmax_rows(np.zeros((2, 6), np.float32), np.zeros((2, 6), np.float32), 2, 6, 8, 1)
+    np.testing.assert_array_equal(got, np.full((2, 6), 1 / 8, np.float32))
+    # a row far below zero: the padding zeros hold the maximum, exp(x - 0) underflows to 0
+    got = O.softmax_rows(np.full((1, 3), -200.0, np.float32), np.zeros((1, 3), np.float32), 1, 3, 5, 1)
+    np.testing.assert_array_equal(got, np.zeros((1, 3), np.float32))
+    # float16 rows take the same padded path
+    x = np.array([[0.5, -1.0, 2.0]], np.float16)
+    got = O.softmax_rows(x, np.zeros_like(x), 1, 3, 4, 1)
+    e = np.exp(np.array([0.5, -1.0, 2.0, 0.0]) - 2.0)
+    np.testing.assert_array_equal(got, (e / e.sum())[:3].astype(np.float16)[None])
 
 
 def test_softmax_blocks_coverage():
