@@ -35,7 +35,7 @@ def test_version_string():
     ("asc_vadd", (0, 0, 0, 0, 16, 0, 4, 16, None), _native.ERR_INVALID_ARG),
     ("asc_vadd", (0, 0, 0, 0, 16, 4, 4, 16, None), _native.ERR_INVALID_ARG),  # null buffers
     ("asc_vadd", (9, 1, 1, 1, 16, 4, 4, 16, None), _native.ERR_UNSUPPORTED),
-    ("asc_softmax_rows_f32", (0, 0, 4, 8, 16, 1, None), _native.ERR_UNSUPPORTED),
+    ("asc_softmax_rows_f32", (0, 0, 4, 8, 16, 1, None), _native.ERR_INVALID_ARG),  # padded tile, null buffer
     ("asc_softmax_rows_f32", (0, 0, 4, 8, 0, 1, None), _native.ERR_INVALID_ARG),
     ("asc_softmax_blocks_f32", (0, 0, 4, 8, 1, 0, None), _native.ERR_INVALID_ARG),
     ("asc_unary", (18, 0, 1, 1, 8, None), _native.ERR_INVALID_ARG),           # unknown op
