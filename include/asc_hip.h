@@ -68,6 +68,31 @@ int32_t asc_device_info(int32_t device, int32_t* cu_count, int32_t* lds_bytes,
  * python/asc/runtime/launcher.py:187). */
 int32_t asc_stream_synchronize(asc_stream_t stream);
 
+/* ---- code objects --------------------------------------------------------
+ * The reference registers the binary its compiler produced and launches the
+ * registered function with a packed argument blob
+ * (python/asc/runtime/launcher.py:156-195, 226-238).  Here the binaries are
+ * gfx950 code objects built ahead of time (pyasc_amd/lib/co/*.hsaco) and
+ * cached per specialisation by the asc2 launch path.
+ * asc_module_load       replaces DevBinaryRegisterWrapper
+ *                       (python/asc/lib/runtime/rt_wrapper.cpp:115-118):
+ *                       hipModuleLoad of the code object at `path` on the
+ *                       current device.
+ * asc_module_unload     replaces DevBinaryUnRegisterWrapper (rt_wrapper.cpp:127).
+ * asc_module_get_function replaces FunctionRegisterWrapper (rt_wrapper.cpp:140-144):
+ *                       the kernel named `name` (its C symbol).
+ * asc_module_launch     replaces KernelLaunchWrapper (rt_wrapper.cpp:189-193):
+ *                       `grid` workgroups of `block` threads on `stream`, the
+ *                       kernel's arguments as one blob of `args_size` bytes laid
+ *                       out as the kernel declares them (natural alignment,
+ *                       8-byte pointers). */
+int32_t asc_module_load(const char* path, void** module);
+int32_t asc_module_unload(void* module);
+int32_t asc_module_get_function(void* module, const char* name, void** function);
+int32_t asc_module_launch(void* function, uint32_t grid, uint32_t block,
+                          const void* args, uint64_t args_size,
+                          asc_stream_t stream);
+
 /* ---- vadd ----------------------------------------------------------------
  * asc2 vadd_kernel(x_ptr, y_ptr, out_ptr, size: int, tile_size: ConstExpr[int],
  *                  tile_per_block: ConstExpr[int])

@@ -38,6 +38,10 @@ SIGNATURES = {
     "asc_device_info": [_c_i32, ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32),
                         ctypes.c_char_p],
     "asc_stream_synchronize": [_c_p],
+    "asc_module_load": [ctypes.c_char_p, ctypes.POINTER(_c_p)],
+    "asc_module_unload": [_c_p],
+    "asc_module_get_function": [_c_p, ctypes.c_char_p, ctypes.POINTER(_c_p)],
+    "asc_module_launch": [_c_p, ctypes.c_uint32, ctypes.c_uint32, _c_p, ctypes.c_uint64, _c_p],
     "asc_vadd": [_c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
     "asc_copy_bytes": [_c_p, _c_p, _c_i64, _c_p],
     "asc_leaky_relu": [_c_i32, _c_p, _c_f32, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],

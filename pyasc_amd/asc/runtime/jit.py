@@ -30,7 +30,7 @@ import numpy as np
 
 from ... import fingerprint, registry
 from ..core import ConstExpr, DataType, require_constexpr
-from .cache import get_mem_cache_key
+from .cache import get_file_cache_key, get_mem_cache_key
 from .launcher import LaunchOptions, Launcher
 
 CODEGEN_OPTIONS = ("capture_exceptions", "ir_multithreading", "custom_builtins")
@@ -75,12 +75,16 @@ def _is_constexpr_annotation(ann_type: Any) -> bool:
     return inspect.isclass(origin) and issubclass(origin, ConstExpr)
 
 
-@dataclass(frozen=True)
+@dataclass
 class ResolvedKernel:
     """One cached specialisation: the native kernel a call resolves to (the
-    counterpart of the reference's CompiledKernel / LaunchedKernel cache entry)."""
+    counterpart of the reference's CompiledKernel / LaunchedKernel cache entry).
+    For a kernel with a code object, ``file_cache_key`` names its binary in the file
+    cache and ``launched`` holds the loaded module after the first launch."""
     entry: registry.KernelEntry
     cache_key: str
+    file_cache_key: str = ""
+    launched: Any = None
 
 
 class JITFunction:
@@ -314,7 +318,8 @@ class JITFunction:
             if hit is not None:
                 return hit, runtime_args, constexprs
         arg_kinds = {name: self.arg_kind(value) for name, value in runtime_args.items()}
-        key = get_mem_cache_key(self._gen_cache_factors(arg_kinds, constexprs, options))
+        factors = self._gen_cache_factors(arg_kinds, constexprs, options)
+        key = get_mem_cache_key(factors)
         hit = self.kernel_cache.get(key)
         if hit is not None:
             if quick is not None:
@@ -322,7 +327,9 @@ class JITFunction:
             return hit, runtime_args, constexprs
         # miss: full validation (ConstExpr types, argument types), then the registry
         runtime_args, constexprs, _ = self.bind(*args, **kwargs)
-        resolved = ResolvedKernel(registry.lookup(self.fn_name, self.params, self.body_fingerprint), key)
+        entry = registry.lookup(self.fn_name, self.params, self.body_fingerprint)
+        file_key = get_file_cache_key(self.cache_key, factors) if entry.code_object is not None else ""
+        resolved = ResolvedKernel(entry, key, file_key)
         self.kernel_cache[key] = resolved
         if quick is not None:
             self._quick_cache[quick] = resolved
@@ -331,7 +338,8 @@ class JITFunction:
     def _run(self, *args, **kwargs) -> None:
         resolved, runtime_args, constexprs = self.resolve(*args, **kwargs)
         options = {**self.default_options, **{k: v for k, v in kwargs.items() if k in COMPILE_OPTIONS}}
-        Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs, options)
+        Launcher(self.launch_options).run(resolved.entry, self.fn_name, runtime_args, constexprs, options,
+                                          resolved=resolved if resolved.cache_key else None)
 
 
 def _check_compile_options(options: Dict[str, Any]) -> None:

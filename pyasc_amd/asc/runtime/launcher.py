@@ -118,7 +118,11 @@ class Launcher:
         return device_args, copy_back
 
     def run(self, entry: KernelEntry, function_name: str, runtime_args: Dict[str, Any],
-            constexprs: Dict[str, Any], options: Optional[Dict[str, Any]] = None) -> None:
+            constexprs: Dict[str, Any], options: Optional[Dict[str, Any]] = None, resolved: Any = None) -> None:
+        """Launches one call.  For an entry with a code object (module.py), ``resolved``
+        (the JIT's cached specialisation) holds the loaded code object after the first
+        launch; without it, or with ``always_compile``, the code object is loaded for
+        this launch and unloaded after it (launcher.py:226-238)."""
         if os.environ.get("DRY_RUN"):
             return
         if self.options.core_num <= 0:
@@ -128,7 +132,10 @@ class Launcher:
         stream = stream_handle(self.options.stream)
         call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream,
                           {"options": dict(options or {})})
-        entry.launch(call)
+        if entry.code_object is None:
+            entry.launch(call)
+        else:
+            self._launch_code_object(entry, call, resolved)
         if copy_back:
             from ... import _native
             _native.call("asc_stream_synchronize", stream)
@@ -137,3 +144,24 @@ class Launcher:
                     np.copyto(host, dev.cpu().numpy())
                 else:
                     host.copy_(dev.cpu())
+
+    @staticmethod
+    def _launch_code_object(entry: KernelEntry, call: KernelCall, resolved: Any) -> None:
+        from . import module
+        co = entry.code_object
+        cached = resolved is not None and getattr(resolved, "file_cache_key", None)
+        if cached and resolved.launched is not None:
+            co.launch(call, resolved.launched.functions)  # memory-cache hit: nothing to load
+            return
+        path = module.compiled_path(co, resolved.file_cache_key if cached else None, call.name)
+        launched = module.load(co, path)
+        if cached:
+            resolved.launched = launched
+            co.launch(call, launched.functions)
+            return
+        try:  # caches bypassed: the module lives for this launch only
+            co.launch(call, launched.functions)
+            from ... import _native
+            _native.call("asc_stream_synchronize", call.stream)
+        finally:
+            module.unload(launched)

@@ -1,91 +1,29 @@
-// Elementwise vadd for asc2 vadd_kernel (python/test/asc2/kernels/test_vadd.py:16-28).
-//
-// HBM-bound: 3 x 4 bytes per fp32 element.  Each thread moves 4 independent
-// 16-byte vectors per operand (global_load_dwordx4) so a wave keeps 8 loads in
-// flight; the physical grid is sized by the covered length, not by the
-// Ascend-style logical grid, which only decides how far the writes reach.
-#include "common.h"
-#include "numeric.h"
+// Elementwise vadd for asc2 vadd_kernel (python/test/asc2/kernels/test_vadd.py:16-28),
+// launched through asc_vadd; the device bodies are in vadd_kernels.h.
+#include "vadd_kernels.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+using asc::vadd::AddBF16;
+using asc::vadd::AddF16;
+using asc::vadd::AddF32;
+using asc::vadd::AddI32;
+using asc::vadd::kThreads;
+using asc::vadd::kUnroll;
+using asc::vadd::u32x4;
 
-// 16-byte vector as a clang ext-vector so the nontemporal builtins accept it.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-struct AddF32 {
-  using T = float;
-  __device__ static float op(float a, float b) { return a + b; }
-};
-struct AddI32 {
-  using T = int32_t;
-  // two's-complement wraparound without signed-overflow UB
-  __device__ static int32_t op(int32_t a, int32_t b) {
-    return static_cast<int32_t>(static_cast<uint32_t>(a) + static_cast<uint32_t>(b));
-  }
-};
-struct AddF16 {
-  using T = uint16_t;
-  // fp32 add then RNE to fp16 equals the correctly rounded fp16 add (24 >= 2*11+2 bits)
-  __device__ static uint16_t op(uint16_t a, uint16_t b) {
-    return asc::f32_to_f16_rne(asc::f16_to_f32(a) + asc::f16_to_f32(b));
-  }
-};
-struct AddBF16 {
-  using T = uint16_t;
-  __device__ static uint16_t op(uint16_t a, uint16_t b) {
-    return asc::f32_to_bf16_rne(asc::bf16_to_f32(a) + asc::bf16_to_f32(b));
-  }
-};
-
-template <typename Op>
-__device__ __forceinline__ u32x4 add_vec(u32x4 a, u32x4 b) {
-  using T = typename Op::T;
-  constexpr int kN = 16 / sizeof(T);
-  T ea[kN], eb[kN], ec[kN];
-  __builtin_memcpy(ea, &a, 16);
-  __builtin_memcpy(eb, &b, 16);
-#pragma unroll
-  for (int i = 0; i < kN; ++i) ec[i] = Op::op(ea[i], eb[i]);
-  u32x4 c;
-  __builtin_memcpy(&c, ec, 16);
-  return c;
-}
-
-// out[v] = x[v] + y[v] for 16-byte vectors v < n_vec.
 template <typename Op>
 __global__ void __launch_bounds__(kThreads) vadd_vec_kernel(const u32x4* __restrict__ x, const u32x4* __restrict__ y,
                                                             u32x4* __restrict__ out, int64_t n_vec) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
-  u32x4 a[kUnroll], b[kUnroll];
-  if (base + (kUnroll - 1) * kThreads < n_vec) {
-#pragma unroll
-    for (int j = 0; j < kUnroll; ++j) a[j] = __builtin_nontemporal_load(x + base + j * kThreads);
-#pragma unroll
-    for (int j = 0; j < kUnroll; ++j) b[j] = __builtin_nontemporal_load(y + base + j * kThreads);
-#pragma unroll
-    for (int j = 0; j < kUnroll; ++j) __builtin_nontemporal_store(add_vec<Op>(a[j], b[j]), out + base + j * kThreads);
-  } else {
-#pragma unroll
-    for (int j = 0; j < kUnroll; ++j) {
-      const int64_t v = base + j * kThreads;
-      if (v < n_vec) out[v] = add_vec<Op>(x[v], y[v]);
-    }
-  }
+  asc::vadd::vec_body<Op>(x, y, out, n_vec);
 }
 
-// Element-wise path for [begin, end): unaligned buffers and the sub-vector tail.
 template <typename Op>
 __global__ void __launch_bounds__(kThreads) vadd_scalar_kernel(const typename Op::T* __restrict__ x,
                                                                const typename Op::T* __restrict__ y,
                                                                typename Op::T* __restrict__ out, int64_t begin,
                                                                int64_t end) {
-  for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < end;
-       i += static_cast<int64_t>(gridDim.x) * kThreads) {
-    out[i] = Op::op(x[i], y[i]);
-  }
+  asc::vadd::scalar_body<Op>(x, y, out, begin, end);
 }
 
 template <typename Op>
@@ -99,20 +37,17 @@ int32_t launch(const void* xv, const void* yv, void* outv, int64_t covered, hipS
   if (asc::aligned16(x) && asc::aligned16(y) && asc::aligned16(out)) {
     const int64_t n_vec = covered / kPerVec;
     if (n_vec > 0) {
-      const int64_t blocks = asc::ceil_div(n_vec, kThreads * kUnroll);
-      hipLaunchKernelGGL(vadd_vec_kernel<Op>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
-                         reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(y),
-                         reinterpret_cast<u32x4*>(out), n_vec);
+      hipLaunchKernelGGL(vadd_vec_kernel<Op>, dim3(static_cast<uint32_t>(asc::vadd::vec_blocks(n_vec))),
+                         dim3(kThreads), 0, stream, reinterpret_cast<const u32x4*>(x),
+                         reinterpret_cast<const u32x4*>(y), reinterpret_cast<u32x4*>(out), n_vec);
       int32_t rc = asc::check_launch("asc_vadd");
       if (rc != ASC_OK) return rc;
     }
     done = n_vec * kPerVec;
   }
   if (done < covered) {
-    const int64_t rest = covered - done;
-    const int64_t blocks = asc::ceil_div(rest, kThreads) < 4096 ? asc::ceil_div(rest, kThreads) : 4096;
-    hipLaunchKernelGGL(vadd_scalar_kernel<Op>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, x, y,
-                       out, done, covered);
+    hipLaunchKernelGGL(vadd_scalar_kernel<Op>, dim3(static_cast<uint32_t>(asc::vadd::scalar_blocks(covered - done))),
+                       dim3(kThreads), 0, stream, x, y, out, done, covered);
     return asc::check_launch("asc_vadd");
   }
   return ASC_OK;

@@ -59,12 +59,13 @@ def vadd_covered(size: int, tile_size: int, tile_per_block: int, grid: int) -> i
     return max(0, min(size, grid * tile_per_block * tile_size))
 
 
-def vadd(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
-         grid: int, stream: Any = None) -> None:
+def vadd_check(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
+               grid: int) -> int:
+    """Host checks of a vadd launch; returns the covered element count."""
     for t, n in ((x, "x"), (y, "y"), (out, "out")):
         _contiguous(_device_tensor(t, n), n)
     allowed = (torch.float32, torch.float16, torch.bfloat16, torch.int32)
-    code = _code(x, "x", allowed)
+    _code(x, "x", allowed)
     if y.dtype != x.dtype or out.dtype != x.dtype:
         raise TypeError(f"vadd operands must share one dtype, got {x.dtype}, {y.dtype}, {out.dtype}")
     if tile_size <= 0 or tile_per_block < 0 or grid <= 0 or size < 0:
@@ -74,6 +75,13 @@ def vadd(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, size: int, tile_si
     for t, n in ((x, "x"), (y, "y"), (out, "out")):
         if t.numel() < covered:
             raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {covered}")
+    return covered
+
+
+def vadd(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
+         grid: int, stream: Any = None) -> None:
+    vadd_check(x, y, out, size, tile_size, tile_per_block, grid)
+    code = _DTYPE_CODES[x.dtype]
     _native.call("asc_vadd", code, x.data_ptr(), y.data_ptr(), out.data_ptr(), size, tile_size, tile_per_block,
                  grid, _stream(stream))
 

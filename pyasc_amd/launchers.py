@@ -12,6 +12,7 @@ import torch
 
 from . import kernels
 from .asc.core import as_torch_dtype, ceildiv
+from .asc.runtime import module
 from .registry import KernelCall, register
 
 
@@ -48,8 +49,42 @@ def _asc2_matmul_dtype(t: torch.Tensor) -> None:
 
 # ---------------------------------------------------------------------------------------------- vadd
 
+_VADD_CO_SUFFIX = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16", torch.int32: "i32"}
+
+
+def _vadd_code_object_launch(call: KernelCall, functions) -> None:
+    """vadd_kernel through the asc2_vadd code object: the same device bodies and launch
+    geometry as asc_vadd (csrc/vadd.hip, vadd_kernels.h) -- 16-byte vectors of the
+    covered range when all three buffers are 16-byte aligned, one thread per element for
+    the rest -- with the kernels' arguments packed into one blob."""
+    x, y, out = call.args["x_ptr"], call.args["y_ptr"], call.args["out_ptr"]
+    covered = kernels.vadd_check(x, y, out, int(call.args["size"]), int(call.consts["tile_size"]),
+                                 int(call.consts["tile_per_block"]), call.grid)
+    if covered == 0:
+        return
+    sfx = _VADD_CO_SUFFIX[x.dtype]
+    ptrs = [("ptr", x.data_ptr()), ("ptr", y.data_ptr()), ("ptr", out.data_ptr())]
+    per_vec = 16 // x.element_size()
+    done = 0
+    if all(t.data_ptr() % 16 == 0 for t in (x, y, out)):
+        n_vec = covered // per_vec
+        if n_vec:
+            module.launch(functions[f"asc2_vadd_vec_{sfx}"], ceildiv(n_vec, VADD_THREADS * VADD_UNROLL),
+                          VADD_THREADS, ptrs + [("i64", n_vec)], call.stream)
+        done = n_vec * per_vec
+    if done < covered:
+        module.launch(functions[f"asc2_vadd_elem_{sfx}"], ceildiv(covered - done, VADD_THREADS), VADD_THREADS,
+                      ptrs + [("i64", done), ("i64", covered)], call.stream)
+
+
+VADD_THREADS, VADD_UNROLL = 256, 4  # vadd_kernels.h: kThreads, kUnroll
+VADD_CODE_OBJECT = module.CodeObject(
+    "asc2_vadd", tuple(f"asc2_vadd_{kind}_{sfx}" for sfx in ("f32", "f16", "bf16", "i32") for kind in ("vec", "elem")),
+    _vadd_code_object_launch, "pyasc_amd/csrc/co/asc2_vadd.hip")
+
+
 @register("vadd_kernel", ("x_ptr", "y_ptr", "out_ptr", "size", "tile_size", "tile_per_block"),
-          "python/test/asc2/kernels/test_vadd.py:16-28")
+          "python/test/asc2/kernels/test_vadd.py:16-28", code_object=VADD_CODE_OBJECT)
 def _vadd(call: KernelCall) -> None:
     kernels.vadd(call.args["x_ptr"], call.args["y_ptr"], call.args["out_ptr"], int(call.args["size"]),
                  int(call.consts["tile_size"]), int(call.consts["tile_per_block"]), call.grid, call.stream)

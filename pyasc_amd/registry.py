@@ -39,19 +39,24 @@ class KernelEntry:
     params: Tuple[str, ...]
     launch: Callable[[KernelCall], None]
     reference: str  # file:line of the reference kernel this entry stands for
+    # the prebuilt code object the asc2 launch path loads for this kernel (module.py);
+    # None: the kernel launches through the library's C ABI
+    code_object: Any = None
 
 
 _REGISTRY: Dict[Tuple[str, Tuple[str, ...]], KernelEntry] = {}
 
 
-def register(name: str, params: Tuple[str, ...], reference: str):
-    """Decorator registering ``launch`` for kernels named ``name`` with ``params``."""
+def register(name: str, params: Tuple[str, ...], reference: str, code_object: Any = None):
+    """Decorator registering ``launch`` for kernels named ``name`` with ``params``;
+    ``code_object`` (a module.CodeObject) makes the asc2 launch path load and launch
+    that prebuilt code object instead of calling ``launch``."""
 
     def deco(launch: Callable[[KernelCall], None]) -> Callable[[KernelCall], None]:
         key = (name, tuple(params))
         if key in _REGISTRY:
             raise RuntimeError(f"kernel signature registered twice: {name}{tuple(params)}")
-        _REGISTRY[key] = KernelEntry(name, tuple(params), launch, reference)
+        _REGISTRY[key] = KernelEntry(name, tuple(params), launch, reference, code_object)
         return launch
 
     return deco

@@ -53,6 +53,13 @@ def test_version_string():
     ("asc_fill", (0, 0, 8, 1.0, 0, None), _native.ERR_INVALID_ARG),
     ("asc_rect_binary", (0, 0, 1, 1, 1, 8, 8, -1, 0, 2, 2, None), _native.ERR_INVALID_ARG),
     ("asc_broadcast_rows", (3, 1, 1, 2, 2, None), _native.ERR_UNSUPPORTED),
+    ("asc_module_load", (None, None), _native.ERR_INVALID_ARG),
+    ("asc_module_unload", (None,), _native.ERR_INVALID_ARG),
+    ("asc_module_get_function", (None, b"k", None), _native.ERR_INVALID_ARG),
+    ("asc_module_launch", (None, 1, 64, None, 0, None), _native.ERR_INVALID_ARG),  # null function
+    ("asc_module_launch", (1, 0, 64, None, 0, None), _native.ERR_INVALID_ARG),  # empty grid
+    ("asc_module_launch", (1, 1, 2048, None, 0, None), _native.ERR_INVALID_ARG),  # block too large
+    ("asc_module_launch", (1, 1, 64, None, 8, None), _native.ERR_INVALID_ARG),  # null argument blob
     ("asc_copy_bytes", (16, 32, -16, None), _native.ERR_INVALID_ARG),
     ("asc_copy_bytes", (0, 32, 16, None), _native.ERR_INVALID_ARG),  # null src
     ("asc_copy_bytes", (16, 32, 24, None), _native.ERR_ALIGNMENT),  # size not a multiple of 16

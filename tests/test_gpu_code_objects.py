@@ -1,0 +1,123 @@
+"""The asc2 launch path through prebuilt gfx950 code objects (pyasc_amd/asc/runtime/module.py):
+vadd_kernel[grid](...) loads pyasc_amd/lib/co/asc2_vadd.hsaco with hipModuleLoad, keeps it per
+specialisation in the memory cache and the file cache, and bypasses both under always_compile,
+as the reference's launch path does with the binaries its compiler produces
+(python/asc/runtime/jit.py:158-223, launcher.py:204-238).  Results are bit-identical to the
+library path (asc_vadd), whose kernels share the device bodies."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import asc
+import asc2
+from pyasc_amd import kernels
+from pyasc_amd.asc.runtime import module
+from pyasc_amd.launchers import VADD_CODE_OBJECT
+
+pytestmark = pytest.mark.gpu
+
+
+def _vadd(**options):
+    @asc2.jit(**options)
+    def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
+                    tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [size])
+        y_gm = asc2.tensor(y_ptr, [size])
+        out_gm = asc2.tensor(out_ptr, [size])
+        base_offset = asc2.block_idx() * tile_size * tile_per_block
+        for i in range(tile_per_block):
+            tile_offset = base_offset + i * tile_size
+            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
+            y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
+            out = x + y
+            asc2.store(out, out_gm, offsets=[tile_offset])
+
+    return vadd_kernel
+
+
+@pytest.fixture
+def cache_dir(tmp_path, monkeypatch):
+    monkeypatch.setenv("PYASC_AMD_CACHE_DIR", str(tmp_path))
+    return tmp_path
+
+
+def _inputs(dtype, n, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.int32:
+        x, y = (torch.randint(-2 ** 31, 2 ** 31 - 1, (n,), generator=g, dtype=torch.int32) for _ in range(2))
+    else:
+        x, y = ((torch.rand(n, generator=g) * 10).to(dtype) for _ in range(2))
+    return x.to(device), y.to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.int32])
+@pytest.mark.parametrize("n,tile,tpb,grid,offset", [(8192, 128, 4, 16, 0), (100003, 128, 49, 16, 0),
+                                                   (1000, 128, 2, 3, 0), (5000, 64, 5, 16, 1)])
+def test_code_object_path_matches_library_path(device, cache_dir, dtype, n, tile, tpb, grid, offset):
+    x, y = _inputs(dtype, n + offset, n + tile, device)
+    x, y = x[offset:], y[offset:]  # offset 1: unaligned views take the element kernel only
+    out_co = torch.full((n + offset,), 3, dtype=dtype, device=device)[offset:]
+    out_lib = out_co.clone()
+    _vadd()[grid](x, y, out_co, n, tile, tpb)
+    kernels.vadd(x, y, out_lib, n, tile, tpb, grid)
+    torch.cuda.synchronize()
+    assert torch.equal(out_co, out_lib)
+    covered = min(n, grid * tpb * tile)
+    exp = (x.cpu().to(torch.int64) + y.cpu().to(torch.int64)).to(torch.int32) if dtype == torch.int32 else \
+        x.cpu() + y.cpu()
+    assert torch.equal(out_co.cpu()[:covered], exp[:covered])
+    assert (out_co.cpu()[covered:] == 3).all()
+
+
+def test_memory_and_file_cache_hits(device, cache_dir):
+    x, y = _inputs(torch.float32, 8192, 1, device)
+    out = torch.empty_like(x)
+    k = _vadd()
+    loads = module.stats["module_loads"]
+    k[16](x, y, out, 8192, 128, 4)  # miss: the code object goes into the file cache and is loaded
+    assert module.stats["module_loads"] == loads + 1
+    files = list(cache_dir.rglob("vadd_kernel.hsaco"))
+    assert len(files) == 1 and files[0].read_bytes() == VADD_CODE_OBJECT.path.read_bytes()
+    mtime = files[0].stat().st_mtime_ns
+    for _ in range(5):  # memory-cache hits: no load
+        k[16](x, y, out, 8192, 128, 4)
+    assert module.stats["module_loads"] == loads + 1
+    torch.cuda.synchronize()
+    assert torch.equal(out, x + y)
+    # a new function object with the same source: memory miss, file-cache hit (the cached file is loaded)
+    k2 = _vadd()
+    k2[16](x, y, out, 8192, 128, 4)
+    assert module.stats["module_loads"] == loads + 2
+    assert list(cache_dir.rglob("vadd_kernel.hsaco")) == files and files[0].stat().st_mtime_ns == mtime
+    # another specialisation (dtype) gets its own file-cache entry
+    xh, yh = x.half(), y.half()
+    outh = torch.empty_like(xh)
+    k[16](xh, yh, outh, 8192, 128, 4)
+    torch.cuda.synchronize()
+    assert len(list(cache_dir.rglob("vadd_kernel.hsaco"))) == 2 and torch.equal(outh, xh + yh)
+
+
+def test_always_compile_bypasses_both_caches(device, cache_dir):
+    x, y = _inputs(torch.float32, 8192, 2, device)
+    out = torch.empty_like(x)
+    k = _vadd(always_compile=True)
+    loads, unloads = module.stats["module_loads"], module.stats["module_unloads"]
+    for _ in range(3):
+        k[16](x, y, out, 8192, 128, 4)
+    assert module.stats["module_loads"] == loads + 3 and module.stats["module_unloads"] == unloads + 3
+    assert not list(cache_dir.rglob("*.hsaco")) and k.kernel_cache == {}
+    torch.cuda.synchronize()
+    assert torch.equal(out, x + y)
+
+
+def test_reference_test_through_code_object(device, cache_dir):
+    # python/test/asc2/kernels/test_vadd.py:41-48 on numpy inputs (host buffers copied in and back)
+    rng = np.random.default_rng(seed=2026)
+    x = rng.random(8192, dtype=np.float32) * 10
+    y = rng.random(8192, dtype=np.float32) * 10
+    out = np.empty_like(x)
+    _vadd()[16](x, y, out, 8192, 128, asc.ceildiv(asc.ceildiv(8192, 128), 16))
+    np.testing.assert_array_equal(out, x + y)
+    assert os.path.isdir(cache_dir)

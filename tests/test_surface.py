@@ -25,7 +25,7 @@ def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc
 def recorded(monkeypatch):
     calls = []
 
-    def fake_run(self, entry, function_name, runtime_args, constexprs, options=None):
+    def fake_run(self, entry, function_name, runtime_args, constexprs, options=None, resolved=None):
         calls.append((entry, function_name, runtime_args, constexprs, self.options, options))
 
     monkeypatch.setattr(launcher_mod.Launcher, "run", fake_run)
@@ -607,3 +607,60 @@ def test_shift_amount_range(no_native, dtype, bad):
         kernels.binary(x, bad, torch.empty_like(x), "left_shift")
     kernels.binary(x, torch.iinfo(dtype).bits - 1, torch.empty_like(x), "right_shift")
     assert len(no_native) == 1
+
+
+# ------------------------------------------------------------------- code objects and the file cache
+# The asc2 vadd_kernel launches through a prebuilt gfx950 code object kept per specialisation in
+# the file cache (pyasc_amd/asc/runtime/{cache,module}.py); these parts need no GPU.
+
+def test_file_cache_manager(tmp_path, monkeypatch):
+    from pyasc_amd.asc.runtime import cache
+    monkeypatch.setenv("PYASC_AMD_CACHE_DIR", str(tmp_path))
+    key = cache.hexdigest(b"factors")
+    m = cache.get_cache_manager(key)
+    assert m.cache_dir.startswith(str(tmp_path)) and not m.has_file("k.hsaco") and m.get_file("k.hsaco") is None
+    path = m.put(b"\x7fELF-bytes", "k.hsaco")
+    assert m.get_file("k.hsaco") == path and open(path, "rb").read() == b"\x7fELF-bytes"
+    assert sorted(p.name for p in tmp_path.rglob("*")) == [m.key, "k.hsaco"]  # no temporary left behind
+    # the file key separates functions and factors and follows the prebuilt binaries' identity
+    k1 = cache.get_file_cache_key("fnA", "f=1")
+    assert k1 != cache.get_file_cache_key("fnB", "f=1") and k1 != cache.get_file_cache_key("fnA", "f=2")
+
+
+def test_code_object_compiled_path(tmp_path, monkeypatch):
+    from pyasc_amd.asc.runtime import cache, module
+    from pyasc_amd.launchers import VADD_CODE_OBJECT
+    monkeypatch.setenv("PYASC_AMD_CACHE_DIR", str(tmp_path))
+    assert VADD_CODE_OBJECT.path.exists(), "build() produces pyasc_amd/lib/co/asc2_vadd.hsaco"
+    key = cache.get_file_cache_key("fn", "factors")
+    p1 = module.compiled_path(VADD_CODE_OBJECT, key, "vadd_kernel")
+    assert p1.startswith(str(tmp_path)) and open(p1, "rb").read() == VADD_CODE_OBJECT.path.read_bytes()
+    assert module.compiled_path(VADD_CODE_OBJECT, key, "vadd_kernel") == p1  # a file-cache hit
+    assert module.compiled_path(VADD_CODE_OBJECT, None, "vadd_kernel") == str(VADD_CODE_OBJECT.path)  # bypassed
+    # the code object is a gfx950 ELF holding every kernel the launcher names
+    data = VADD_CODE_OBJECT.path.read_bytes()
+    assert data[:4] == b"\x7fELF"
+    for name in VADD_CODE_OBJECT.functions:
+        assert name.encode() + b".kd" in data
+
+
+def test_pack_args_layout():
+    from pyasc_amd.asc.runtime import module
+    blob = module.pack_args([("ptr", 0x1000), ("i32", 7), ("i64", -2), ("f32", 1.5), ("ptr", 0x2000)])
+    import struct
+    # natural alignment: ptr @0, i32 @8, (pad) i64 @16, f32 @24, (pad) ptr @32
+    assert len(blob) == 40
+    assert struct.unpack_from("<Q", blob, 0)[0] == 0x1000 and struct.unpack_from("<i", blob, 8)[0] == 7
+    assert struct.unpack_from("<q", blob, 16)[0] == -2 and struct.unpack_from("<f", blob, 24)[0] == 1.5
+    assert struct.unpack_from("<Q", blob, 32)[0] == 0x2000 and blob[12:16] == b"\0" * 4
+
+
+def test_vadd_entry_has_code_object_and_resolution_records_file_key(tmp_path, monkeypatch):
+    monkeypatch.setenv("PYASC_AMD_CACHE_DIR", str(tmp_path))
+    k = _cached_vadd()
+    x = np.zeros(64, np.float32)
+    resolved, _, _ = k.resolve(x, x, x, 64, 8, 4)
+    assert resolved.entry.code_object is not None and resolved.entry.code_object.name == "asc2_vadd"
+    assert len(resolved.file_cache_key) == 32 and resolved.launched is None
+    fresh, _, _ = _cached_vadd(always_compile=True).resolve(x, x, x, 64, 8, 4)
+    assert fresh.cache_key == "" and fresh.file_cache_key == ""
