@@ -72,7 +72,7 @@ int32_t asc_stream_synchronize(asc_stream_t stream);
  * The reference registers the binary its compiler produced and launches the
  * registered function with a packed argument blob
  * (python/asc/runtime/launcher.py:156-195, 226-238).  Here the binaries are
- * gfx950 code objects built ahead of time (pyasc_amd/lib/co/*.hsaco) and
+ * gfx950 code objects built ahead of time (pyasc_amd/lib/co/<name>.hsaco) and
  * cached per specialisation by the asc2 launch path.
  * asc_module_load       replaces DevBinaryRegisterWrapper
  *                       (python/asc/lib/runtime/rt_wrapper.cpp:115-118):

@@ -128,14 +128,17 @@ __device__ __forceinline__ float other_half(float v) {
   return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-// Largest exponent (log2 domain) an unnormalised probability may reach before
-// the running max is moved; bounds exp2 values by 2^8.
-constexpr float kRescaleSlack = 8.0f;
+// Largest sum of one lane's unnormalised probabilities over a key tile (32
+// values) before the reference point is moved: bounds every exp2 value by 2^16.
+constexpr float kTileSumLimit = 65536.0f;
 
-// Per-wave state of the attention kernel (a wave owns 32 queries; a workgroup
-// of kWaves waves owns 32*kWaves).
-template <int D, int kWaves>
+// Per-wave state of the attention kernel.  A wave owns QB blocks of 32 queries
+// (32*QB queries); a workgroup of kWaves waves owns 32*QB*kWaves.  Every K or V
+// operand a wave reads from LDS feeds QB MFMAs, one per query block, so LDS
+// read traffic per MFMA falls as 1/QB.
+template <int D, int kWaves, int QB>
 struct FaState {
+  static constexpr int kQ = 32 * QB;              // queries per wave
   static constexpr int kChunks = D / 8;           // 16-byte chunks per row
   static constexpr int kTileBytes = BKV * D * 2;  // one K or V tile
   static constexpr int kKSteps = D / 16;          // MFMA k-steps over head_dim
@@ -144,7 +147,8 @@ struct FaState {
   static constexpr int kLoadsPerWave = BKV / kRowsPerLoad / kWaves;  // per tile
 
   int lane, wave, col, h;
-  int q0, S, my_q, wave_qmax, causal;
+  int q0, S, causal;
+  int qw0;  // first query of this wave: q0 + wave * kQ
   float scale_log2;
   __amdgpu_buffer_rsrc_t rsrc_k, rsrc_v;
   int voff_k[4], voff_v;  // voff_k[i]: this wave's i-th K load (kLoadsPerWave <= 4)
@@ -153,10 +157,13 @@ struct FaState {
   // that of row j, so every other term of a read address is an immediate.
   uint32_t kaddr[kKSteps];   // K row col, chunk 2*kk+h
   uint32_t vaddr[kDBlocks];  // V transpose read of d block db, rows 4h+j
-  u32x4 qreg[kKSteps];
-  f32x16 acc_o[kDBlocks];
-  float m_run;   // reference point of the scaled scores (log2 domain), <= running max
-  float l_part;  // this lane half's share of the running sum of exp2(s*scale_log2 - m_run)
+  u32x4 qreg[QB][kKSteps];
+  f32x16 acc_o[QB][kDBlocks];
+  float m_run[QB];   // reference point of the scaled scores (log2 domain), <= running max
+  float l_part[QB];  // this lane half's share of the running sum of exp2(s*scale_log2 - m_run)
+
+  // query of this lane in query block qb
+  __device__ __forceinline__ int my_q(int qb) const { return qw0 + qb * 32 + col; }
 
   // K/V tile rows go straight from HBM into LDS (buffer_load ... lds, 1 KiB per
   // wave instruction, lane l -> row kRowsPerLoad*R + l/(64/kRowsPerLoad)).  The
@@ -192,6 +199,11 @@ struct FaState {
   // Keys k0 .. k0+63 of K (kIsV false) or V into one LDS stage.
   template <bool kIsV>
   __device__ __forceinline__ void load_tile(uint8_t* dst, int k0) const {
+    // The LDS destination (M0) of each load is formed here, from an opaque copy
+    // of the wave's offset: left to itself the compiler keeps one SGPR per stage
+    // and load for the whole kernel and spills them.
+    int wave_lds = wave * (kLoadsPerWave * 1024);
+    asm volatile("" : "+s"(wave_lds));
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i) {
       const int R = wave * kLoadsPerWave + i;
@@ -199,51 +211,65 @@ struct FaState {
       // buffer range check (keys >= S read as zero) only covers the former
       const int roff = (k0 + kRowsPerLoad * R) * (D * 2);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(kIsV ? rsrc_v : rsrc_k,
-                                               (__attribute__((address_space(3))) void*)(dst + R * 1024), 16,
-                                               (kIsV ? voff_v : voff_k[i]) + roff, 0, 0, 0);
+                                               (__attribute__((address_space(3))) void*)(dst + wave_lds + i * 1024),
+                                               16, (kIsV ? voff_v : voff_k[i]) + roff, 0, 0, 0);
     }
   }
 
   // causal: a wave whose queries all precede the tile skips it
-  __device__ __forceinline__ bool active(int k0) const { return !(causal && k0 > wave_qmax); }
+  __device__ __forceinline__ bool active(int k0) const { return !(causal && k0 > qw0 + kQ - 1); }
 
-  // S^T = K Q^T for keys k0 .. k0+63 (two 32-key blocks).  Register r of block
-  // kb then holds key k0 + 32*kb + 8*(r/4) + 4*h + r%4 for query my_q.
-  // The kKSteps operand reads of a block go out together; each MFMA waits only
-  // for its own.
-  __device__ __forceinline__ void scores(const uint8_t* ks_, f32x16 (&s)[2]) const {
+  // S^T = K Q^T for keys k0 .. k0+63 (two 32-key blocks) and each query block.
+  // Register r of s[qb][kb] then holds key k0 + 32*kb + 8*(r/4) + 4*h + r%4 for
+  // query my_q(qb).  A window of kWin K operand reads is in flight: read r+kWin
+  // goes out once the MFMAs of read r have been issued (they have read their
+  // operands by then).
+  __device__ __forceinline__ void scores(const uint8_t* ks_, f32x16 (&s)[QB][2]) const {
     const uint32_t base = lds_addr(ks_);
+    constexpr int kWin = 4;
+    constexpr int kReads = 2 * kKSteps;
+    u32x4 a[kReads];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x16{};
-      u32x4 a[kKSteps];
+    for (int r = 0; r < kWin; ++r) a[r] = lds_read_b128(base + kaddr[r % kKSteps], (r / kKSteps) * 32 * (D * 2));
 #pragma unroll
-      for (int kk = 0; kk < kKSteps; ++kk) a[kk] = lds_read_b128(base + kaddr[kk], kb * 32 * (D * 2));
+    for (int qb = 0; qb < QB; ++qb) {
+      s[qb][0] = f32x16{};
+      s[qb][1] = f32x16{};
+    }
 #pragma unroll
-      for (int kk = 0; kk < kKSteps; ++kk) {
-        lds_wait(a[kk], kKSteps - 1 - kk);
-        s[kb] = mfma_bf16(a[kk], qreg[kk], s[kb]);
+    for (int r = 0; r < kReads; ++r) {
+      lds_wait(a[r], r + kWin <= kReads ? kWin - 1 : kReads - 1 - r);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        s[qb][r / kKSteps] = mfma_bf16(a[r], qreg[qb][r % kKSteps], s[qb][r / kKSteps]);
+      }
+      if (r + kWin < kReads) {
+        a[r + kWin] = lds_read_b128(base + kaddr[(r + kWin) % kKSteps], ((r + kWin) / kKSteps) * 32 * (D * 2));
       }
     }
   }
 
   // Keys >= S and (causal) keys after the query score -inf.
-  __device__ __forceinline__ void mask(f32x16 (&s)[2], int k0) const {
-    const bool need_mask = (k0 + BKV > S) || (causal && k0 + BKV - 1 > q0 + wave * 32);
-    if (need_mask) {
+  __device__ __forceinline__ void mask(f32x16 (&s)[QB][2], int k0) const {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+    for (int qb = 0; qb < QB; ++qb) {
+      const bool need_mask = (k0 + BKV > S) || (causal && k0 + BKV - 1 > qw0 + qb * 32);
+      if (need_mask) {
+        const int q = my_q(qb);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + kb * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-          if (key >= S || (causal && key > my_q)) s[kb][r] = -INFINITY;
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + kb * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+            if (key >= S || (causal && key > q)) s[qb][kb][r] = -INFINITY;
+          }
         }
       }
     }
   }
 
-  // Tile max of the raw scores over both lane halves, times scale_log2
-  // (sm_scale > 0, so the max of the scaled scores is the scaled max).
+  // Tile max of the raw scores of one query block over both lane halves, times
+  // scale_log2 (sm_scale > 0, so the max of the scaled scores is the scaled max).
   __device__ __forceinline__ float tile_max(const f32x16 (&s)[2]) const {
     float mt = -INFINITY;
 #pragma unroll
@@ -253,26 +279,25 @@ struct FaState {
     return fmaxf(mt, other_half(mt)) * scale_log2;
   }
 
-  // Lazy rescale: the reference point m_run only moves when the tile max
-  // exceeds it by more than kRescaleSlack (log2 units), so exp2 values stay
-  // below 2^kRescaleSlack and O / l are rescaled rarely.  The branch is
-  // wave-uniform (any lane that needs it).
-  __device__ __forceinline__ void rebase(float mt) {
-    const bool upd = mt > m_run + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(upd) != 0) {
-      const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
-      if (upd) m_run = mt;
-      l_part *= alpha;
+  // The reference point of query block qb moves up to the tile max mt wherever
+  // that exceeds it: on the first tile, and on the rare tile whose
+  // probabilities relative to the current reference point come out too large
+  // (see fa_step).  O and l are rescaled by the same factor.
+  __device__ __forceinline__ void raise(int qb, float mt) {
+    const bool upd = mt > m_run[qb];
+    const float alpha = upd ? __builtin_amdgcn_exp2f(m_run[qb] - mt) : 1.0f;
+    if (upd) m_run[qb] = mt;
+    l_part[qb] *= alpha;
 #pragma unroll
-      for (int db = 0; db < kDBlocks; ++db) acc_o[db] *= alpha;
-    }
+    for (int db = 0; db < kDBlocks; ++db) acc_o[qb][db] *= alpha;
   }
 
-  // P^T operands: exp2(s * scale_log2 - m_run) rounded to bf16.  Block kb, step
-  // u uses registers 8u..8u+7, i.e. keys 32kb + 16u + 4h + {0..3} and
-  // 32kb + 16u + 8 + 4h + {0..3}.
-  __device__ __forceinline__ void probs(const f32x16 (&s)[2], u32x4 (&pb)[2][2]) {
-    const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+  // P^T operands of query block qb: exp2(s * scale_log2 - m_run) rounded to
+  // bf16.  Block kb, step u uses registers 8u..8u+7, i.e. keys 32kb + 16u + 4h +
+  // {0..3} and 32kb + 16u + 8 + 4h + {0..3}.  Returns this lane's sum of the
+  // tile's probabilities (fp32, before rounding).
+  __device__ __forceinline__ float probs(int qb, const f32x16 (&s)[2], u32x4 (&pb)[2][2]) const {
+    const float neg_m = m_run[qb] == -INFINITY ? 0.f : -m_run[qb];
     float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -286,96 +311,136 @@ struct FaState {
           rs += e1;
           pb[kb][u][w] = pack_bf16(e0, e1);
         }
-    l_part += rs;
+    return rs;
   }
 
-  // V^T operands of d block db: for (kb, u) the rows kb*32 + u*16 + {0, 8}
-  // of the tile, four MFMA A operands of two transpose reads each.
-  __device__ __forceinline__ void vt_reads(uint32_t base, int db, u32x4 (&a)[4]) const {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const u32x2 lo = lds_read_tr16_b64(base + vaddr[db], (kb * 32 + u * 16) * (D * 2));
-        const u32x2 hi = lds_read_tr16_b64(base + vaddr[db], (kb * 32 + u * 16 + 8) * (D * 2));
-        a[kb * 2 + u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
+  // V^T operand r of the tile (d block r / 4, keys 16 * (r % 4) .. +15): the
+  // tile rows 16 * (r % 4) + {0, 8}, two transpose reads.
+  __device__ __forceinline__ u32x4 vt_read(uint32_t base, int r) const {
+    const int db = r / 4, row = (r % 4) * 16;
+    const u32x2 lo = lds_read_tr16_b64(base + vaddr[db], row * (D * 2));
+    const u32x2 hi = lds_read_tr16_b64(base + vaddr[db], (row + 8) * (D * 2));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 
-  // O^T += V^T P^T; V^T comes from transpose reads of the row-major V tile.
-  // The reads of d block db+1 are in flight while block db multiplies.
-  __device__ __forceinline__ void pv(const uint8_t* vs_, const u32x4 (&pb)[2][2]) {
+  // O^T += V^T P^T for every query block; V^T comes from transpose reads of the
+  // row-major V tile, a window of kWin operands in flight: operand r+kWin is
+  // read once the MFMAs of operand r have been issued.
+  __device__ __forceinline__ void pv(const uint8_t* vs_, const u32x4 (&pb)[QB][2][2]) {
     const uint32_t base = lds_addr(vs_);
-    u32x4 a[2][4];
-    vt_reads(base, 0, a[0]);
+    constexpr int kWin = 4;
+    constexpr int kOps = 4 * kDBlocks;
+    u32x4 a[kOps];
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) {
-      u32x4(&cur)[4] = a[db & 1];
-      if (db + 1 < kDBlocks) {
-        vt_reads(base, db + 1, a[(db + 1) & 1]);
-        lds_wait(cur, 8);  // the newest 8 reads belong to block db+1
-      } else {
-        lds_wait(cur, 0);
+    for (int r = 0; r < kWin; ++r) a[r] = vt_read(base, r);
+#pragma unroll
+    for (int r = 0; r < kOps; ++r) {
+      lds_wait(a[r], 2 * (r + kWin <= kOps ? kWin - 1 : kOps - 1 - r));
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        acc_o[qb][r / 4] = mfma_bf16(a[r], pb[qb][(r % 4) >> 1][r & 1], acc_o[qb][r / 4]);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc_o[db] = mfma_bf16(cur[i], pb[i >> 1][i & 1], acc_o[db]);
+      if (r + kWin < kOps) a[r + kWin] = vt_read(base, r + kWin);
     }
   }
 };
 
-// One pipeline step for key tile j.  On entry LDS holds K_{j+1} (k_next) and
-// V_j (v_cur), and sc holds the masked scores of tile j with m_run already
-// rebased for them.  The step streams V_{j+1} and K_{j+2} into the stages freed
-// by the previous step, then overlaps the exp2 of tile j with the S^T MFMAs of
-// tile j+1, and the P.V MFMAs of tile j with the max of tile j+1.  kGuard
-// false (a clean step): tile j+1 exists, every wave is active for tiles j and
-// j+1, and tile j+1 needs no mask -- the caller guarantees it.
-template <int D, int kWaves, bool kGuard>
-__device__ __forceinline__ void fa_step(FaState<D, kWaves>& st, int j, int n_tiles, uint8_t* k_load, uint8_t* v_load,
-                                        const uint8_t* k_next, const uint8_t* v_cur, f32x16 (&sc)[2],
-                                        f32x16 (&sn)[2]) {
+// One pipeline step for key tile j.  K and V each stream through a ring of
+// three LDS stages, tile t in stage t % 3.  On entry LDS holds K_{j+1} and V_j,
+// and sc holds the masked scores of tile j; K_{j+2} and V_{j+1} may still be in
+// flight.  The step requests V_{j+2} and K_{j+3} into the stages read in the
+// previous step, overlaps the exp2 of tile j with the S^T MFMAs of tile j+1
+// (into sn), and multiplies P_j V_j.  At its end every wave waits for its loads
+// of the previous step (those of this step stay in flight for a whole step
+// more) and its LDS reads, and the workgroup meets.
+// The reference point m_run is not moved per tile: the probabilities of tile j
+// are taken against the current one, and only when a lane's sum over the tile
+// exceeds kTileSumLimit (a score above the reference point by more than about
+// 11 in log2 units) does the wave take the tile max, move the reference point
+// and take them again.  kGuard false (a clean step): tiles j+1 .. j+3 exist,
+// every wave is active for tiles j and j+1, and tile j+1 needs no mask -- the
+// caller guarantees it.  `ring` is the LDS ring base (K stages 0-2, V stages
+// 3-5), `c` = j % 3.
+template <int D, int kWaves, int QB, bool kGuard>
+__device__ __forceinline__ void fa_step(FaState<D, kWaves, QB>& st, int j, int n_tiles, uint8_t* ring, int c,
+                                        f32x16 (&sc)[QB][2], f32x16 (&sn)[QB][2]) {
+  using St = FaState<D, kWaves, QB>;
+  constexpr int T = St::kTileBytes;
+  constexpr int L = St::kLoadsPerWave;
+  const int c1 = c == 2 ? 0 : c + 1;  // (j + 1) % 3
+  const int c2 = c == 0 ? 2 : c - 1;  // (j + 2) % 3
   const int k1 = (j + 1) * BKV;
   const bool has_next = !kGuard || j + 1 < n_tiles;
   const bool act = !kGuard || st.active(j * BKV);
   const bool act_next = !kGuard || (has_next && st.active(k1));
-  if (has_next) st.template load_tile<true>(v_load, k1);
-  if (j + 2 < n_tiles) st.template load_tile<false>(k_load, k1 + BKV);
-  u32x4 pb[2][2];
-  if (act) st.probs(sc, pb);
-  if (act_next) st.scores(k_next, sn);
+  const bool load_v = !kGuard || j + 2 < n_tiles;
+  const bool load_k = !kGuard || j + 3 < n_tiles;
+  if (load_v) st.template load_tile<true>(ring + (3 + c2) * T, k1 + BKV);
+  if (load_k) st.template load_tile<false>(ring + c * T, k1 + 2 * BKV);
+  u32x4 pb[QB][2][2];
+  float rs[QB];
+  if (act) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = st.probs(qb, sc[qb], pb[qb]);
+  }
+  if (act_next) st.scores(ring + c1 * T, sn);
   if (kGuard && act_next) st.mask(sn, k1);
-  if (act) st.pv(v_cur, pb);
-  const float mt = act_next ? st.tile_max(sn) : -INFINITY;
-  // a wave waits for its own loads and LDS reads only, then the workgroup
-  // meets (a plain s_barrier: __syncthreads' fence would drain more)
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  if (act) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (__builtin_amdgcn_ballot_w64(rs[qb] > kTileSumLimit) != 0) {
+        st.raise(qb, st.tile_max(sc[qb]));
+        rs[qb] = st.probs(qb, sc[qb], pb[qb]);
+      }
+      st.l_part[qb] += rs[qb];
+    }
+    st.pv(ring + (3 + c) * T, pb);
+  }
+  if (load_v && load_k) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * L) : "memory");
+  } else if (load_v || load_k) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(L) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  }
   asm volatile("s_barrier" ::: "memory");
-  if (act_next) st.rebase(mt);
 }
 
-// kWaves = 4: two workgroups per CU, the two waves of a SIMD come from different
-// workgroups and drift apart.  kWaves = 8: one workgroup of 256 queries per CU,
-// each K/V tile streamed once for twice the queries (half the DMA per query);
-// the two waves of a SIMD belong to one workgroup and would run their exp2 and
-// MFMA phases in lockstep, so waves 0-3 run at raised priority and their SIMD
-// partners fill in behind them (non-causal +3.6% over kWaves = 4; causal with
-// the grouped block order 1.5-2% faster than with 128-query blocks).
-template <int D, int kWaves>
-__global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs p) {
-  using St = FaState<D, kWaves>;
+// Configurations.  head_dim 128: one workgroup of 8 waves (256 queries) per CU,
+// each K/V tile streamed once for 256 queries; the two waves of a SIMD belong
+// to one workgroup and would run their exp2 and MFMA phases in lockstep, so
+// waves 0-3 run at raised priority and their SIMD partners fill in behind them.
+// (4 waves of 64 queries each, QB = 2, halve the LDS reads per MFMA but leave
+// one wave per SIMD with nothing to overlap its MFMAs with: 1025 against 950 us
+// at the bench shape, measured with the rare rescale path left out -- with it
+// the kernel does not fit the register file.)  head_dim 64: 4 waves of 32 queries, two workgroups per
+// CU, whose waves share each SIMD and drift apart.
+template <int D>
+struct FaConfig;
+template <>
+struct FaConfig<128> {
+  static constexpr int kWaves = 8, QB = 1, kWgPerCu = 1;
+};
+template <>
+struct FaConfig<64> {
+  static constexpr int kWaves = 4, QB = 1, kWgPerCu = 2;
+};
+
+template <int D>
+__global__ void __launch_bounds__(FaConfig<D>::kWaves * 64, FaConfig<D>::kWgPerCu) fa_fwd_kernel(FaArgs p) {
+  constexpr int kWaves = FaConfig<D>::kWaves;
+  constexpr int QB = FaConfig<D>::QB;
+  using St = FaState<D, kWaves, QB>;
   constexpr int kTileBytes = St::kTileBytes;
   constexpr int kChunks = St::kChunks;
   constexpr int kKSteps = St::kKSteps;
   constexpr int kDBlocks = St::kDBlocks;
   constexpr int kThreads = kWaves * 64;
-  constexpr int BQ = 32 * kWaves;  // queries per workgroup
-  // K and V rings of two stages each, as distinct objects, so the compiler can
-  // tell that loads into one stage do not alias reads of another.  K runs one
-  // tile ahead of V.
-  __shared__ __attribute__((aligned(16))) uint8_t kst0[kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t kst1[kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t vst0[kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t vst1[kTileBytes];
+  constexpr int BQ = St::kQ * kWaves;  // queries per workgroup
+  // K ring (stages 0-2) and V ring (stages 3-5).  LDS reads of the rings are
+  // inline asm with explicit waits, so no compiler alias analysis between DMA
+  // and reads is involved.
+  __shared__ __attribute__((aligned(16))) uint8_t ring[6 * kTileBytes];
 
   St st;
   const int tid = threadIdx.x;
@@ -383,7 +448,7 @@ __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs 
   if (kWaves == 8 && (tid >> 6) < 4) __builtin_amdgcn_s_setprio(1);
   st.lane = lane;
   st.wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  st.col = lane & 31;  // query column within the wave's 32
+  st.col = lane & 31;  // query column within a query block
   st.h = lane >> 5;    // lane half
   const int wave = st.wave, col = st.col, h = st.h;
 
@@ -402,7 +467,7 @@ __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs 
   // Otherwise: query-block major (heavy first over all heads when causal).
   const int64_t bid = blockIdx.x;
   int64_t bh;
-  int qb;
+  int qblk;
   if (p.heads_total % 8 == 0) {
     const int64_t slot = bid >> 3;  // < heads_total / 8 * n_qblocks
     const int64_t per_group = static_cast<int64_t>(p.head_group) * p.n_qblocks;
@@ -412,13 +477,13 @@ __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs 
     const int64_t heads_left = (p.heads_total >> 3) - g0;  // >= 1; the last group may be partial
     const int64_t gsz = heads_left < p.head_group ? heads_left : p.head_group;
     bh = (bid & 7) + 8 * (g0 + r % gsz);
-    qb = static_cast<int>(r / gsz);
+    qblk = static_cast<int>(r / gsz);
   } else {
     bh = bid % p.heads_total;
-    qb = static_cast<int>(bid / p.heads_total);
+    qblk = static_cast<int>(bid / p.heads_total);
   }
-  if (p.causal) qb = p.n_qblocks - 1 - qb;
-  const int q0 = qb * BQ;
+  if (p.causal) qblk = p.n_qblocks - 1 - qblk;
+  const int q0 = qblk * BQ;
   const int S = p.seq;
   const int64_t head_off = bh * static_cast<int64_t>(S) * D;
   const uint16_t* Qh = p.q + head_off;
@@ -426,91 +491,113 @@ __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs 
   st.S = S;
   st.causal = p.causal;
   st.scale_log2 = p.scale_log2;
-  st.my_q = q0 + wave * 32 + col;
-  st.wave_qmax = q0 + wave * 32 + 31;
-  const int my_q = st.my_q;
+  st.qw0 = q0 + wave * St::kQ;
 
-  // Q^T operand: lane (query col, half h) holds Q[my_q][16*ks + 8h .. +8]
+  // Q^T operand of query block qb: lane (query col, half h) holds
+  // Q[my_q(qb)][16*ks + 8h .. +8]
 #pragma unroll
-  for (int ks = 0; ks < kKSteps; ++ks) {
-    if (my_q < S) {
-      st.qreg[ks] = *reinterpret_cast<const u32x4*>(Qh + static_cast<int64_t>(my_q) * D + ks * 16 + h * 8);
-    } else {
-      st.qreg[ks] = u32x4{0, 0, 0, 0};
+  for (int qb = 0; qb < QB; ++qb) {
+    const int q = st.my_q(qb);
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) {
+      if (q < S) {
+        st.qreg[qb][ks] = *reinterpret_cast<const u32x4*>(Qh + static_cast<int64_t>(q) * D + ks * 16 + h * 8);
+      } else {
+        st.qreg[qb][ks] = u32x4{0, 0, 0, 0};
+      }
     }
-  }
 #pragma unroll
-  for (int i = 0; i < kDBlocks; ++i) st.acc_o[i] = f32x16{};
-  st.m_run = -INFINITY;
-  st.l_part = 0.f;
+    for (int i = 0; i < kDBlocks; ++i) st.acc_o[qb][i] = f32x16{};
+    st.m_run[qb] = -INFINITY;
+    st.l_part[qb] = 0.f;
+  }
 
   int kv_end = S;
   if (p.causal) kv_end = min(S, q0 + BQ);
   const int n_tiles = (kv_end + BKV - 1) / BKV;
 
+  // K_0, V_0 and K_1 are needed first; V_1 and K_2 (step 1) may land later
   st.init_loads(p.k + head_off, p.v + head_off);
-  st.template load_tile<false>(kst0, 0);
-  st.template load_tile<true>(vst0, 0);
-  if (n_tiles > 1) st.template load_tile<false>(kst1, BKV);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  constexpr int L = St::kLoadsPerWave;
+  st.template load_tile<false>(ring, 0);
+  st.template load_tile<true>(ring + 3 * kTileBytes, 0);
+  if (n_tiles > 1) {
+    st.template load_tile<false>(ring + kTileBytes, BKV);
+    st.template load_tile<true>(ring + 4 * kTileBytes, BKV);
+  }
+  if (n_tiles > 2) {
+    st.template load_tile<false>(ring + 2 * kTileBytes, 2 * BKV);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L) : "memory");
+  } else if (n_tiles > 1) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
   asm volatile("s_barrier" ::: "memory");
-  f32x16 sa[2], sb[2];
-  st.scores(kst0, sa);  // tile 0 is active for every wave
-  // step 0 refills kst0 with tile 2: every wave must be done reading tile 0
+  f32x16 sa[QB][2], sb[QB][2];
+  st.scores(ring, sa);  // tile 0 is active for every wave
+  // step 0 refills stage 0 with K_3: every wave must be done reading K_0
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   asm volatile("s_barrier" ::: "memory");
   st.mask(sa, 0);
-  st.rebase(st.tile_max(sa));
+  // Key 0 is never masked, so the reference points are finite from here on.
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) st.raise(qb, st.tile_max(sa[qb]));
   // Clean tiles need no mask and are active for every wave: all their keys are
   // < S and, for causal, precede the block's first query q0.  Step j is clean
-  // when tile j+1 is; the clean steps run as pairs, the rest (at most four:
-  // n_tiles - n_clean <= 2) guarded.  Tile j lives in stage j % 2 of each ring.
+  // when tile j+1 is and tiles up to j+3 exist; the clean steps run as pairs,
+  // the rest (at most seven: n_tiles - n_clean <= 4 for BQ = 256) guarded.
+  // c = j % 3 is the ring stage of tile j.
   const int n_clean = p.causal ? min(q0 / BKV, S / BKV) : S / BKV;
-  int j = 0;
-  for (; j + 2 < n_clean; j += 2) {
-    fa_step<D, kWaves, false>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
-    fa_step<D, kWaves, false>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
+  int j = 0, c = 0;
+  for (; j + 4 < n_clean; j += 2) {
+    fa_step<D, kWaves, QB, false>(st, j, n_tiles, ring, c, sa, sb);
+    c = c == 2 ? 0 : c + 1;
+    fa_step<D, kWaves, QB, false>(st, j + 1, n_tiles, ring, c, sb, sa);
+    c = c == 2 ? 0 : c + 1;
   }
   for (; j < n_tiles; j += 2) {
-    fa_step<D, kWaves, true>(st, j, n_tiles, kst0, vst1, kst1, vst0, sa, sb);
-    if (j + 1 < n_tiles) fa_step<D, kWaves, true>(st, j + 1, n_tiles, kst1, vst0, kst0, vst1, sb, sa);
+    fa_step<D, kWaves, QB, true>(st, j, n_tiles, ring, c, sa, sb);
+    c = c == 2 ? 0 : c + 1;
+    if (j + 1 < n_tiles) fa_step<D, kWaves, QB, true>(st, j + 1, n_tiles, ring, c, sb, sa);
+    c = c == 2 ? 0 : c + 1;
   }
 
-  // ---- epilogue: O = O^T / l, transposed through LDS (the K ring, free after
-  //      the last step's barrier) into row-major bf16.  Lane holds query my_q
-  //      and, for d block db and register r, d = 32*db + 8*(r/4) + 4*h + r%4.
-  //      Block rows 0..63 go to kst0, 64..127 to kst1, 128..191 to vst0,
-  //      192..255 to vst1 (all four stages are free after the last barrier).
-  const float l_run = st.l_part + other_half(st.l_part);
-  const float m_run = st.m_run;
-  const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
-  {
-    const int sg = wave >> 1;
-    uint8_t* os_ = sg == 0 ? kst0 : sg == 1 ? kst1 : sg == 2 ? vst0 : vst1;
-    const int row = (wave & 1) * 32 + col;
+  // ---- epilogue: O = O^T / l, transposed through LDS (the rings, free after
+  //      the last step's barrier: no load is in flight then) into row-major
+  //      bf16.  Lane holds query my_q(qb) and, for d block db and register r,
+  //      d = 32*db + 8*(r/4) + 4*h + r%4.  Block rows 64*g .. 64*g+63 go to
+  //      ring stage g.
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l_run = st.l_part[qb] + other_half(st.l_part[qb]);
+    const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+    const int brow = wave * St::kQ + qb * 32 + col;  // row within the workgroup's block
+    uint8_t* os_ = ring + (brow >> 6) * kTileBytes;
+    const int row = brow & 63;
 #pragma unroll
     for (int db = 0; db < kDBlocks; ++db) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int d = db * 32 + rq * 8 + h * 4;
         u32x2 w;
-        w[0] = pack_bf16(st.acc_o[db][rq * 4 + 0] * inv_l, st.acc_o[db][rq * 4 + 1] * inv_l);
-        w[1] = pack_bf16(st.acc_o[db][rq * 4 + 2] * inv_l, st.acc_o[db][rq * 4 + 3] * inv_l);
+        w[0] = pack_bf16(st.acc_o[qb][db][rq * 4 + 0] * inv_l, st.acc_o[qb][db][rq * 4 + 1] * inv_l);
+        w[1] = pack_bf16(st.acc_o[qb][db][rq * 4 + 2] * inv_l, st.acc_o[qb][db][rq * 4 + 3] * inv_l);
         *reinterpret_cast<u32x2*>(os_ + k_off<D>(row, d >> 3) + (d & 7) * 2) = w;
       }
     }
-  }
-  if (p.lse != nullptr && h == 0 && my_q < S) {
-    p.lse[bh * S + my_q] = (m_run + __log2f(l_run)) * 0.69314718055994530942f;
+    const int q = st.my_q(qb);
+    if (p.lse != nullptr && h == 0 && q < S) {
+      p.lse[bh * S + q] = (st.m_run[qb] + __log2f(l_run)) * 0.69314718055994530942f;
+    }
   }
   __syncthreads();
   uint16_t* Oh = p.o + head_off;
 #pragma unroll
   for (int i = 0; i < BQ * kChunks / kThreads; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / kChunks, ch = c % kChunks;
-    const int sg = row >> 6;
-    const uint8_t* os_ = sg == 0 ? kst0 : sg == 1 ? kst1 : sg == 2 ? vst0 : vst1;
+    const int cc = tid + kThreads * i;
+    const int row = cc / kChunks, ch = cc % kChunks;
+    const uint8_t* os_ = ring + (row >> 6) * kTileBytes;
     const int q = q0 + row;
     if (q < S) {
       *reinterpret_cast<u32x4*>(Oh + static_cast<int64_t>(q) * D + ch * 8) =
@@ -519,9 +606,10 @@ __global__ void __launch_bounds__(kWaves * 64, 8 / kWaves) fa_fwd_kernel(FaArgs 
   }
 }
 
-template <int D, int kWaves>
+template <int D>
 int32_t launch(FaArgs p, hipStream_t stream) {
-  constexpr int BQ = 32 * kWaves;
+  using Cfg = FaConfig<D>;
+  constexpr int BQ = 32 * Cfg::QB * Cfg::kWaves;
   p.n_qblocks = static_cast<int>((p.seq + BQ - 1) / BQ);
   p.head_group = 1;
   if (p.causal) {
@@ -536,7 +624,7 @@ int32_t launch(FaArgs p, hipStream_t stream) {
     // Twice the smallest group that fills them: at the bench shape (64 slots, 32
     // blocks per head) groups of 1, 2, 4, 8, 16 heads measured 582-621, 569-591,
     // 564-575, 572-578 and 581-586 us.
-    const int64_t slots = static_cast<int64_t>(cus) / 8 * (8 / kWaves);
+    const int64_t slots = static_cast<int64_t>(cus) / 8 * Cfg::kWgPerCu;
     const int64_t g = 2 * ((slots + p.n_qblocks - 1) / p.n_qblocks);
     const int64_t heads_xcd = p.heads_total / 8;
     p.head_group = static_cast<int>(g < 1 ? 1 : (g > heads_xcd && heads_xcd > 0 ? heads_xcd : g));
@@ -544,11 +632,10 @@ int32_t launch(FaArgs p, hipStream_t stream) {
   const int64_t blocks = p.heads_total * p.n_qblocks;
   // one workgroup per (head, query block): the grid's x dimension and its thread count
   // (blocks x kWaves x 64) must fit 32 bits
-  ASC_REQUIRE(blocks <= (int64_t{1} << 31) - 1 && blocks * kWaves * 64 < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED,
+  ASC_REQUIRE(blocks <= (int64_t{1} << 31) - 1 && blocks * Cfg::kWaves * 64 < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED,
               "asc_flash_attention_fwd_bf16: %lld heads x %d query blocks exceed the launch grid limit",
               static_cast<long long>(p.heads_total), p.n_qblocks);
-  hipLaunchKernelGGL((fa_fwd_kernel<D, kWaves>), dim3(static_cast<uint32_t>(blocks)), dim3(kWaves * 64), 0, stream,
-                     p);
+  hipLaunchKernelGGL(fa_fwd_kernel<D>, dim3(static_cast<uint32_t>(blocks)), dim3(Cfg::kWaves * 64), 0, stream, p);
   return asc::check_launch("asc_flash_attention_fwd_bf16");
 }
 
@@ -582,6 +669,6 @@ extern "C" int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k, co
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.causal = causal ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (head_dim == 64) return launch<64, 4>(p, s);
-  return launch<128, 8>(p, s);
+  if (head_dim == 64) return launch<64>(p, s);
+  return launch<128>(p, s);
 }

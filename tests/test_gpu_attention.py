@@ -87,6 +87,40 @@ def test_config_shape_all_heads(device, causal):
                 torch.testing.assert_close(out[b, hh][rows].float(), ref, atol=TOL, rtol=TOL)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("profile", ["ramp", "outlier"])
+def test_rescale_when_scores_grow(device, D, causal, profile):
+    """Scores that grow along the keys: the kernel keeps the first tile's max as its
+    reference point until a tile's probabilities against it sum past 2^16 per lane,
+    then moves it.  "ramp" (every query row sees scores 0.25 * key, natural log units)
+    moves it on every tile; "outlier" (one key far above the rest, late in the
+    sequence) once.  Both against the fp32 CPU reference and the log-sum-exp."""
+    S = 1000
+    g = torch.Generator().manual_seed(11 + D)
+    u = torch.full((D,), 1 / math.sqrt(D))
+    q = u.expand(1, 2, S, D).clone()
+    if profile == "ramp":
+        t = 0.25 * torch.arange(S, dtype=torch.float32)
+    else:
+        t = 0.1 * torch.randn(S, generator=g)
+        t[700] = 60.0
+    k = (t[:, None] * u).expand(1, 2, S, D).clone()
+    k[0, 1] += 0.05 * torch.randn(S, D, generator=g)
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    v = torch.randn(1, 2, S, D, generator=g).to(torch.bfloat16)
+    out, lse = _run(q, k, v, 1.0, causal, device, lse=True)
+    assert torch.isfinite(out.float()).all()
+    for hh in range(2):
+        qf, kf, vf = q[0, hh].float(), k[0, hh].float(), v[0, hh].float()
+        ref = cpu_golden.attention(qf, kf, vf, 1.0, causal)
+        torch.testing.assert_close(out[0, hh].float(), ref, atol=TOL, rtol=TOL)
+        sc = qf.double() @ kf.double().T
+        if causal:
+            sc = sc.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+        torch.testing.assert_close(lse[0, hh].double(), torch.logsumexp(sc, dim=1), atol=1e-3, rtol=1e-4)
+
+
 @asc2.jit
 def flash_attention_fwd_kernel(q_ptr: asc.GlobalAddress, k_ptr: asc.GlobalAddress, v_ptr: asc.GlobalAddress,
                                o_ptr: asc.GlobalAddress, batch: int, heads: int, seq_len: int,
