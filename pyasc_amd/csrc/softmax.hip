@@ -5,9 +5,8 @@
 // over the row's first L columns (row stride S).
 //
 // HBM-bound (one read + one write of every element).  Rows up to 8192 columns
-// stay in registers: a wave per row (two rows per wave) up to 1024 columns, a
-// 128-thread block per row up to 4096 (measured faster there than one wave or
-// four waves per row), 256 threads above.  Max, min and sum reduce in-thread,
+// stay in registers: a wave per row (two rows per wave) up to 512 columns, a
+// 128- or 256-thread block per row above (see launch_rows).  Max, min and sum reduce in-thread,
 // then across the wave with DPP and permlane swaps (no LDS round trips), then
 // across waves through LDS.  x - max is rounded to fp32 as in the reference
 // (test_softmax.py:22-24); exp of it is accurate to ~2 ulp (the row's min picks
@@ -240,13 +239,17 @@ int32_t launch_rows(const RowView& p, hipStream_t stream, const char* who) {
   } else if (L <= 512) {
     hipLaunchKernelGGL((softmax_wave_kernel<2, 2>), wave_grid, block, 0, stream, p);
   } else if (L <= 1024) {
-    hipLaunchKernelGGL((softmax_wave_kernel<4, 2>), wave_grid, block, 0, stream, p);
+    // Above 512 columns a row takes several waves with 2-4 vectors per lane:
+    // more, shorter waves than one wave per row, and each wave's loads, cross-wave
+    // reductions and stores finish sooner (fp32 rows, 64 MiB in and out, same
+    // box: 1024 columns 5500-5560 GB/s with one wave per two rows, 5950 here;
+    // 2048: 5680 with two waves per row, 5870 with four; 4096: 5560-5590 with
+    // two waves per row, 5740-5780 with four, beside a 5840-5850 GB/s copy).
+    hipLaunchKernelGGL((softmax_block_kernel<2, 128>), dim3(static_cast<uint32_t>(p.rows)), dim3(128), 0, stream, p);
   } else if (L <= 2048) {
-    hipLaunchKernelGGL((softmax_block_kernel<4, 128>), dim3(static_cast<uint32_t>(p.rows)), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL((softmax_block_kernel<2, 256>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else if (L <= 4096) {
-    // two waves per row: 32 values per lane keep 8 waves per SIMD resident, so
-    // a 4096-row launch is in flight at once
-    hipLaunchKernelGGL((softmax_block_kernel<8, 128>), dim3(static_cast<uint32_t>(p.rows)), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL((softmax_block_kernel<4, 256>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else if (L <= 8192) {
     hipLaunchKernelGGL((softmax_block_kernel<8, 256>), dim3(static_cast<uint32_t>(p.rows)), block, 0, stream, p);
   } else {
