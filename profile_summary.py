@@ -2,6 +2,7 @@
 
     python profile_summary.py traffic DIR   # FETCH_SIZE / WRITE_SIZE passes -> profiles/traffic.json + hbm_traffic.md
     python profile_summary.py mfma DIR      # MFMA-busy / clock passes -> profiles/mfma_counters.md
+    python profile_summary.py trace DIR     # kernel traces -> profiles/kernel_trace_suite.md
 
 DIR holds one rocprofv3 output folder per pass, written with ``-f csv -o run`` by
 the commands the summaries print:
@@ -9,6 +10,9 @@ the commands the summaries print:
   traffic: DIR/<workload>_FETCH_SIZE and DIR/<workload>_WRITE_SIZE, from
       rocprofv3 --pmc FETCH_SIZE -f csv -d DIR/<workload>_FETCH_SIZE -o run -- \
           python3 bench.py --workload <workload> --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration
+  trace: DIR/<workload>_TRACE and the bench's output in DIR/<workload>_TRACE.log, from
+      rocprofv3 --kernel-trace --stats -f csv -d DIR/<workload>_TRACE -o run -- \
+          python3 bench.py --workload <workload> --no-suite --no-cpu --steps 20 --warmup 3 > DIR/<workload>_TRACE.log
   mfma: DIR/<workload>_MFMA, from
       rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv \
           -d DIR/<workload>_MFMA -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --steps 5 \
@@ -226,6 +230,61 @@ def mfma(folder: str) -> int:
     return 0
 
 
+def trace(folder: str) -> int:
+    """Traced kernel durations of each workload's timed replay beside the bench's own
+    HIP-event figure for the same replay (the last ``steps`` dispatches of the
+    workload's kernel are the timed replay: warm-up launches and the untimed first
+    replay come before it)."""
+    lines = [
+        "# Kernel trace: the bench workloads on one MI355X", "",
+        "Generated by `python profile_summary.py trace DIR` from one traced bench run per workload "
+        "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
+        "```",
+        "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof/${W}_TRACE -o run -- python3 bench.py "
+        "--workload $W --no-suite --no-cpu --steps 20 --warmup 3 > gpurun_out/prof/${W}_TRACE.log",
+        "```", "",
+        "Durations in microseconds: average, minimum and maximum of the timed replay's dispatches "
+        "(Start/End timestamps), the bench's figure for the same replay (HIP events around the graph "
+        "replay on the launch stream, divided by the launches) and the bench's value computed from it.", "",
+        "| Workload | Kernel | timed dispatches | avg us | min | max | bench events us | trace / events | "
+        "bench value |",
+        "|---|---|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for key, make in bench.WORKLOADS.items():
+        d = os.path.join(folder, f"{key}_TRACE")
+        log = d + ".log"
+        if not (os.path.isdir(d) and os.path.exists(log)):
+            continue
+        w = make()
+        with open(log) as f:
+            res = json.loads([ln for ln in f if ln.startswith("{")][-1])
+        files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+        if not files:
+            raise FileNotFoundError(f"no kernel_trace.csv under {d}")
+        rows = []
+        for path in files:
+            with open(path, newline="") as f:
+                rows += [r for r in csv.DictReader(f)
+                         if _is_library_kernel(r["Kernel_Name"]) and w.kernel_hint in r["Kernel_Name"]]
+        rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+        steps = int(res["steps"])
+        launches = getattr(w, "launches_per_step", 1)
+        timed = rows[-steps * launches:]
+        if len(timed) < steps * launches:
+            raise RuntimeError(f"{d}: {len(timed)} dispatches of {w.kernel_hint!r}, expected {steps * launches}")
+        durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in timed]
+        names = sorted({_short(r["Kernel_Name"]) for r in timed})
+        per_step = sum(durs) / steps
+        ev = res["kernel_ms"] * 1e3
+        lines.append(f"| `{w.name}` | {', '.join(f'`{n}`' for n in names)} | {len(durs)} | {per_step:.2f} | "
+                     f"{min(durs):.2f} | {max(durs):.2f} | {ev:.2f} | {per_step / ev:.3f} | "
+                     f"{res['value']:.4g} {res['unit']} |")
+        print(lines[-1])
+    with open(os.path.join(PROFILES, "kernel_trace_suite.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    return 0
+
+
 def _gpu_agent(folder: str) -> dict:
     """The GPU row of rocprofv3's agent_info.csv under ``folder``."""
     for path in glob.glob(os.path.join(folder, "**", "*agent_info.csv"), recursive=True):
@@ -248,10 +307,11 @@ def device_shape(folder: str):
 
 
 def main(argv) -> int:
-    if len(argv) != 3 or argv[1] not in ("traffic", "mfma"):
+    modes = {"traffic": traffic, "mfma": mfma, "trace": trace}
+    if len(argv) != 3 or argv[1] not in modes:
         print(__doc__, file=sys.stderr)
         return 2
-    return {"traffic": traffic, "mfma": mfma}[argv[1]](argv[2])
+    return modes[argv[1]](argv[2])
 
 
 if __name__ == "__main__":

@@ -3,14 +3,15 @@
 // python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py).
 //
 // fp16/bf16 inputs run on MFMA (v_mfma_f32_32x32x16_{bf16,f16}) with fp32
-// accumulation, 256x256 output tile per 256-thread workgroup, 4 waves in 2x2,
-// each wave 128x128 = 4x4 MFMA blocks (256 fp32 accumulators per lane):
+// accumulation and a 256x256 output tile per workgroup:
 //   - tile-aligned shapes (M, N multiples of 256, K of 32, offsets within
-//     32 bits): the direct-to-LDS loop of gemm_direct.h -- operands go from HBM
+//     32 bits): the direct-to-LDS loop of gemm_direct.h with 8 waves in 2x4,
+//     each 128x64 = 4x2 MFMA blocks, two waves per SIMD -- operands go from HBM
 //     straight into five 32 KiB LDS stages, B stays row-major and its
 //     K-contiguous MFMA operand comes from LDS transpose reads;
-//   - other shapes: the register-staged loop of gemm_core.h with bounds-checked
-//     loads (zero fill), B transposed in registers, masked stores;
+//   - other shapes: the register-staged loop of gemm_core.h (4 waves in 2x2,
+//     each 128x128) with bounds-checked loads (zero fill), B transposed in
+//     registers, masked stores;
 //   - XCD-aware, grouped tile order (gemm_common.h).
 // The epilogue applies the fixpipe relu and the RNE cast to fp16/bf16, or
 // stores fp32 as is.

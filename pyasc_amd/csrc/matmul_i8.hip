@@ -4,10 +4,10 @@
 //  lib/Conversion/LowerToAsc/LowerAscTileDataTransfer.cpp:116-117).
 //
 // Same structure as the fp16/bf16 kernel on v_mfma_i32_32x32x32_i8: 256x256
-// output tile, 4 waves of 128x128; tile-aligned shapes take the direct-to-LDS
-// loop of gemm_direct.h (64-byte k-tiles, B read with ds_read_b64_tr_b8),
-// others the register-staged loop of gemm_core.h (B transposed in registers as
-// 16(k) x 8(n) byte blocks).  The epilogue either stores the int32
+// output tile; tile-aligned shapes take the direct-to-LDS loop of
+// gemm_direct.h (8 waves of 128x64, 64-byte k-tiles, B read with
+// ds_read_b64_tr_b8), others the register-staged loop of gemm_core.h (4 waves
+// of 128x128, B transposed in registers as 16(k) x 8(n) byte blocks).  The epilogue either stores the int32
 // accumulators or out = fp16_rne(fp32_rne(acc) * s[n]) with s[n] the fp32
 // scale (optionally with its low 13 mantissa bits cleared, the reference
 // golden's trunc-19 form).
