@@ -145,8 +145,9 @@ int32_t asc_vmuladd(int32_t dtype, const void* x, const void* y, const void* z,
  *   approximate != 0: x - x / (exp(x * (x*x*k2 + k1)) + 1),
  *                     k1 = 2*sqrt(2/pi), k2 = k1 * 0.044715
  *   approximate == 0: x * (erf(x * sqrt(0.5)) + 1) * 0.5
- * (the reference body's expressions and order).  tile_size must be <=
- * num_cols (ASC_ERR_UNSUPPORTED otherwise, as for the row softmax). */
+ * (the reference body's expressions and order).  tile_size > num_cols: the
+ * reference's load pads the row with zeros and gelu is element-wise, so every
+ * column of the row is computed; nothing past the row is written. */
 int32_t asc_gelu_rows_f32(const float* x, float* out, int64_t num_rows,
                           int64_t num_cols, int32_t tile_size,
                           int32_t approximate, int32_t grid,

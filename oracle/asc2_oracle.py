@@ -192,9 +192,12 @@ def gelu_values(x: np.ndarray, approximate: bool) -> np.ndarray:
 def gelu_rows(x: np.ndarray, out: np.ndarray, num_rows: int, num_cols: int, tile_size: int,
               approximate: bool) -> np.ndarray:
     """test_gelu.py:19-33: every row's first ``tile_size`` columns (grid-stride rows cover all
-    rows); ``tile_size > num_cols`` is rejected like the row softmax."""
-    if tile_size > num_cols:
-        raise ValueError("tile_size > num_cols is not supported")
+    rows).  With ``tile_size > num_cols`` the [1, tile] load pads the row with zeros
+    (LowerAscTileDataTransfer.cpp:181-222); gelu is element-wise, so the row's own columns
+    are gelu(x) whatever the padding, and only the row's own columns are written (the
+    reference's tile store would also write the padding's gelu(0) = 0 into the next row,
+    racing with that row's own store)."""
+    tile_size = min(tile_size, num_cols)
     x2 = np.asarray(x, dtype=np.float32).reshape(num_rows, num_cols)
     res = np.array(out, dtype=np.float64).reshape(num_rows, num_cols)
     res[:, :tile_size] = gelu_values(x2[:, :tile_size], approximate)

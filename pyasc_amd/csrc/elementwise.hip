@@ -265,10 +265,10 @@ extern "C" int32_t asc_gelu_rows_f32(const float* x, float* out, int64_t num_row
   ASC_REQUIRE(num_rows >= 0 && num_cols >= 0, ASC_ERR_INVALID_ARG, "asc_gelu_rows_f32: negative shape");
   ASC_REQUIRE(tile_size > 0 && grid > 0, ASC_ERR_INVALID_ARG,
               "asc_gelu_rows_f32: need tile_size > 0 and grid > 0 (got %d, %d)", tile_size, grid);
-  ASC_REQUIRE(tile_size <= num_cols, ASC_ERR_UNSUPPORTED,
-              "asc_gelu_rows_f32: tile_size %d > num_cols %lld (the reference's row store would spill into the "
-              "next row)",
-              tile_size, (long long)num_cols);
+  // A tile wider than the row: the load pads with zeros and gelu is element-wise, so the
+  // row's own columns are all that is computed and written (the reference's tile store
+  // would also spill the padding's gelu(0) = 0 into the next row).
+  if (tile_size > num_cols) tile_size = static_cast<int32_t>(num_cols);
   if (num_rows == 0) return ASC_OK;
   ASC_REQUIRE(x && out, ASC_ERR_INVALID_ARG, "asc_gelu_rows_f32: null buffer");
   GeluArgs p{x, out, num_rows, num_cols, tile_size, approximate ? 1 : 0,

@@ -134,12 +134,11 @@ def vmuladd(x: torch.Tensor, y: torch.Tensor, z: torch.Tensor, out: torch.Tensor
 
 def gelu_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, approximate: bool,
               grid: int, stream: Any = None) -> None:
-    """asc2 gelu_kernel (python/test/asc2/kernels/test_gelu.py:19-33) on fp32 rows."""
+    """asc2 gelu_kernel (python/test/asc2/kernels/test_gelu.py:19-33) on fp32 rows.  A tile
+    wider than the row computes the row's own columns (the padding is zeros and gelu is
+    element-wise) and writes nothing past them."""
     if tile_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
         raise ValueError(f"invalid gelu launch: rows={num_rows}, cols={num_cols}, tile={tile_size}, grid={grid}")
-    if tile_size > num_cols:
-        raise ValueError(f"tile_size {tile_size} > num_cols {num_cols}: the reference kernel's row store would "
-                         "spill into the next row")
     for t, n in ((x, "x"), (out, "out")):
         _contiguous(_device_tensor(t, n), n)
         if t.dtype != torch.float32:

@@ -198,7 +198,8 @@ def test_elementwise_unaligned_views(device):
 
 
 @pytest.mark.parametrize("approximate", [True, False])
-@pytest.mark.parametrize("rows,cols,tile", [(37, 1000, 1000), (64, 4096, 3000), (5, 7, 7), (16384, 1024, 1024)])
+@pytest.mark.parametrize("rows,cols,tile", [(37, 1000, 1000), (64, 4096, 3000), (5, 7, 7), (16384, 1024, 1024),
+                                           (9, 100, 128), (3, 5, 64)])
 def test_gelu_vs_oracle(device, approximate, rows, cols, tile):
     g = torch.Generator().manual_seed(rows * cols)
     x = torch.randn(rows, cols, generator=g) * 3
@@ -215,5 +216,7 @@ def test_elementwise_argument_errors(device):
         kernels.leaky_relu(x, 0.1, torch.empty(50, device=device), 100, 32, 4, 1)
     with pytest.raises(TypeError):
         kernels.vmuladd(x, x.half(), x, x, 100, 32, 4, 1)
+    with pytest.raises(ValueError):  # the launch touches 20 x 10 elements of a 100-element tensor
+        kernels.gelu_rows(x, torch.empty_like(x), 20, 10, 11, True, 1)
     with pytest.raises(ValueError):
-        kernels.gelu_rows(x, torch.empty_like(x), 10, 10, 11, True, 1)
+        kernels.gelu_rows(x, torch.empty_like(x), 10, 10, 0, True, 1)

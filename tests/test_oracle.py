@@ -362,6 +362,14 @@ def test_gelu_matches_torch_and_identities(approximate):
     np.testing.assert_allclose(ours - O.gelu_values(-x, approximate), x.astype(np.float64), rtol=0, atol=1e-12)
     out = O.gelu_rows(np.tile(x[:64], 3), np.full(192, 5.0), 3, 64, 40, approximate)
     assert (out[:, 40:] == 5.0).all()
+    # a tile wider than the row: the row zero-padded to the tile, gelu over the padded row,
+    # the row's own columns kept (the padding's values are gelu(0) = 0, written nowhere)
+    rows = np.tile(x[:50], 3).reshape(3, 50)
+    padded = np.concatenate([rows, np.zeros((3, 14), np.float32)], axis=1)
+    wide = O.gelu_rows(rows, np.full((3, 50), 5.0), 3, 50, 64, approximate)
+    full = O.gelu_rows(padded, np.full((3, 64), 5.0), 3, 64, 64, approximate)
+    np.testing.assert_array_equal(wide, full[:, :50])
+    assert (full[:, 50:] == 0.0).all()
 
 
 def test_matmul_bias_leaky_relu_known_answer_and_tutorial_golden():
