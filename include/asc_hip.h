@@ -196,6 +196,30 @@ int32_t asc_softmax_blocks_f16(const void* x, void* out, int64_t num_rows,
                                int64_t num_cols, int32_t block_size,
                                int32_t grid, asc_stream_t stream);
 
+/* The launch the four softmax entries above make, for a launcher that runs the
+ * same kernels from the code object pyasc_amd/lib/co/asc2_softmax.hsaco instead
+ * (the asc2 launch path does, through asc_module_launch).  No counterpart in the
+ * reference, whose compiler fixes the launch inside the kernel binary.
+ * dtype ASC_DT_FLOAT32 / FLOAT16; fused 0 for asc_softmax_rows_* (size is
+ * tile_size), 1 for asc_softmax_blocks_* (size is block_size); the other
+ * arguments and the errors are the entry's.  On success `plan` names the
+ * kernel, its grid and block, and its arguments after x and out:
+ *   kernel(const void* x, void* out, int64_t rows, int64_t stride,
+ *          int32_t len, int32_t flag)
+ * grid 0 means there is nothing to launch. */
+typedef struct asc_softmax_plan {
+  char kernel[32]; /* NUL-terminated symbol in asc2_softmax.hsaco */
+  uint32_t grid;   /* workgroups */
+  uint32_t block;  /* threads per workgroup */
+  int64_t rows;
+  int64_t stride;
+  int32_t len;
+  int32_t flag;
+} asc_softmax_plan_t;
+int32_t asc_softmax_plan(int32_t dtype, int32_t fused, const void* x,
+                         const void* out, int64_t num_rows, int64_t num_cols,
+                         int32_t size, int32_t grid, asc_softmax_plan_t* plan);
+
 /* ---- reductions ---------------------------------------------------------------
  * asc2.reduce_sum / reduce_max / reduce_min / reduce_prod
  *   (python/asc/language/tile/reduction_ops.py:61-126) as the reference's

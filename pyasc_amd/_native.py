@@ -33,6 +33,14 @@ ERR_ALIGNMENT = -3
 
 _c_i32, _c_i64, _c_p, _c_f32, _c_f64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_double
 
+
+
+class SoftmaxPlan(ctypes.Structure):
+    """asc_softmax_plan_t: a softmax launch as kernel name, grid, block and arguments."""
+    _fields_ = [("kernel", ctypes.c_char * 32), ("grid", ctypes.c_uint32), ("block", ctypes.c_uint32),
+                ("rows", _c_i64), ("stride", _c_i64), ("len", _c_i32), ("flag", _c_i32)]
+
+
 # name -> argtypes; every entry point returns int32_t.
 SIGNATURES = {
     "asc_device_info": [_c_i32, ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32),
@@ -53,6 +61,7 @@ SIGNATURES = {
     "asc_softmax_blocks_f32": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
     "asc_softmax_rows_f16": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
     "asc_softmax_blocks_f16": [_c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p],
+    "asc_softmax_plan": [_c_i32, _c_i32, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, ctypes.POINTER(SoftmaxPlan)],
     "asc_matmul": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
     "asc_matmul_bias_act": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                             _c_i32, _c_f32, _c_p],

@@ -46,6 +46,7 @@ PER_FILE_FLAGS = {
     "vadd.hip": ["-ffp-contract=off"],
     "asc2_vadd.hip": ["-ffp-contract=off"],
     "softmax.hip": ["-ffp-contract=off"],
+    "asc2_softmax.hip": ["-ffp-contract=off"],
     "matmul_i8.hip": ["-ffp-contract=off"],
     "elementwise.hip": ["-ffp-contract=off"],
     "tile_ops.hip": ["-ffp-contract=off"],

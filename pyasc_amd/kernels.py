@@ -7,6 +7,7 @@ GPU.  Launches are asynchronous on ``stream`` (default: torch's current stream).
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Any, Optional
 
 import torch
@@ -164,15 +165,24 @@ def _check_softmax(x: torch.Tensor, out: torch.Tensor, rows: int, num_cols: int)
     return "f32" if x.dtype == torch.float32 else "f16"
 
 
+def _softmax_launch(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, size: int, grid: int,
+                    fused: bool) -> str:
+    """Checks a softmax launch (size is tile_size, or block_size when fused); returns the
+    dtype suffix ("f32" / "f16")."""
+    if size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
+        raise ValueError(f"invalid softmax launch: rows={num_rows}, cols={num_cols}, "
+                         f"{'block' if fused else 'tile'}={size}, grid={grid}")
+    rows = softmax_blocks_covered(num_rows, size, grid) if fused else num_rows
+    return _check_softmax(x, out, rows, num_cols)
+
+
 def softmax_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, grid: int,
                  stream: Any = None) -> None:
     """asc2 softmax_kernel(x, out, num_rows, num_cols, tile_size) of
     python/test/asc2/kernels/test_softmax.py:16-27.  With tile_size > num_cols each row's
     statistics include the tile's tile_size - num_cols zero padding (the reference's padded
     load and whole-tile reductions) and each row writes its own num_cols outputs."""
-    if tile_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
-        raise ValueError(f"invalid softmax launch: rows={num_rows}, cols={num_cols}, tile={tile_size}, grid={grid}")
-    suffix = _check_softmax(x, out, num_rows, num_cols)
+    suffix = _softmax_launch(x, out, num_rows, num_cols, tile_size, grid, False)
     _native.call(f"asc_softmax_rows_{suffix}", x.data_ptr(), out.data_ptr(), num_rows, num_cols, tile_size, grid,
                  _stream(stream))
 
@@ -186,12 +196,22 @@ def softmax_blocks(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: 
                    stream: Any = None) -> None:
     """asc2 softmax_kernel(x, out, num_rows, num_cols, block_size) of
     python/test/asc2/kernels/test_softmax_fused.py:16-24."""
-    if block_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
-        raise ValueError(f"invalid softmax launch: rows={num_rows}, cols={num_cols}, block={block_size}, "
-                         f"grid={grid}")
-    suffix = _check_softmax(x, out, softmax_blocks_covered(num_rows, block_size, grid), num_cols)
+    suffix = _softmax_launch(x, out, num_rows, num_cols, block_size, grid, True)
     _native.call(f"asc_softmax_blocks_{suffix}", x.data_ptr(), out.data_ptr(), num_rows, num_cols, block_size,
                  grid, _stream(stream))
+
+
+def softmax_plan(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, size: int, grid: int,
+                 fused: bool) -> "_native.SoftmaxPlan":
+    """The launch softmax_rows (fused False, size = tile_size) or softmax_blocks (fused True,
+    size = block_size) makes for these buffers, as a kernel of the asc2_softmax code object
+    with its grid, block and arguments (asc_softmax_plan); plan.grid == 0 when there is
+    nothing to launch.  Same checks and errors as those two calls."""
+    suffix = _softmax_launch(x, out, num_rows, num_cols, size, grid, fused)
+    plan = _native.SoftmaxPlan()
+    _native.call("asc_softmax_plan", _native.DT_FLOAT32 if suffix == "f32" else _native.DT_FLOAT16, int(fused),
+                 x.data_ptr(), out.data_ptr(), num_rows, num_cols, size, grid, ctypes.byref(plan))
+    return plan
 
 
 # ---------------------------------------------------------------------------------- reductions, rms_norm

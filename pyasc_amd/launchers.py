@@ -129,15 +129,46 @@ def _gelu(call: KernelCall) -> None:
 
 # ------------------------------------------------------------------------------------------- softmax
 
+# The kernels of the asc2_softmax code object (csrc/co/asc2_softmax.hip), one per row body.
+SOFTMAX_CO_FUNCTIONS = tuple(f"asc2_softmax_{body}" for body in (
+    "wave_1x2", "wave_2x2", "block_2x128", "block_2x256", "block_4x256", "block_8x256", "long", "f16", "padded_f32",
+    "padded_f16"))
+
+
+def _softmax_code_object_launch(fused: bool):
+    """softmax_kernel through the asc2_softmax code object: asc_softmax_plan picks the
+    kernel, grid, block and arguments the library entry (asc_softmax_rows_* /
+    asc_softmax_blocks_*) would launch, and the code object's kernel of that name runs
+    them (the same device body)."""
+    size_name = "block_size" if fused else "tile_size"
+
+    def launch(call: KernelCall, functions) -> None:
+        x, out = call.args["x_ptr"], call.args["out_ptr"]
+        plan = kernels.softmax_plan(x, out, int(call.get("num_rows")), int(call.get("num_cols")),
+                                    int(call.get(size_name)), call.grid, fused)
+        if plan.grid:
+            module.launch(functions[plan.kernel.decode()], plan.grid, plan.block,
+                          [("ptr", x.data_ptr()), ("ptr", out.data_ptr()), ("i64", plan.rows),
+                           ("i64", plan.stride), ("i32", plan.len), ("i32", plan.flag)], call.stream)
+
+    return launch
+
+
+SOFTMAX_ROWS_CODE_OBJECT = module.CodeObject("asc2_softmax", SOFTMAX_CO_FUNCTIONS, _softmax_code_object_launch(False),
+                                             "pyasc_amd/csrc/co/asc2_softmax.hip")
+SOFTMAX_BLOCKS_CODE_OBJECT = module.CodeObject("asc2_softmax", SOFTMAX_CO_FUNCTIONS, _softmax_code_object_launch(True),
+                                               "pyasc_amd/csrc/co/asc2_softmax.hip")
+
+
 @register("softmax_kernel", ("x_ptr", "out_ptr", "num_rows", "num_cols", "tile_size"),
-          "python/test/asc2/kernels/test_softmax.py:16-27")
+          "python/test/asc2/kernels/test_softmax.py:16-27", code_object=SOFTMAX_ROWS_CODE_OBJECT)
 def _softmax_rows(call: KernelCall) -> None:
     kernels.softmax_rows(call.args["x_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
                          int(call.get("num_cols")), int(call.get("tile_size")), call.grid, call.stream)
 
 
 @register("softmax_kernel", ("x_ptr", "out_ptr", "num_rows", "num_cols", "block_size"),
-          "python/test/asc2/kernels/test_softmax_fused.py:16-24")
+          "python/test/asc2/kernels/test_softmax_fused.py:16-24", code_object=SOFTMAX_BLOCKS_CODE_OBJECT)
 def _softmax_blocks(call: KernelCall) -> None:
     kernels.softmax_blocks(call.args["x_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
                            int(call.get("num_cols")), int(call.get("block_size")), call.grid, call.stream)

@@ -121,3 +121,105 @@ def test_reference_test_through_code_object(device, cache_dir):
     _vadd()[16](x, y, out, 8192, 128, asc.ceildiv(asc.ceildiv(8192, 128), 16))
     np.testing.assert_array_equal(out, x + y)
     assert os.path.isdir(cache_dir)
+
+
+# --------------------------------------------------------------------------------------- softmax
+
+def _softmax_rows(**options):
+    # python/test/asc2/kernels/test_softmax.py:16-27
+    @asc2.jit(**options)
+    def softmax_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: int, num_cols: int,
+                       tile_size: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [num_rows, num_cols])
+        out_gm = asc2.tensor(out_ptr, [num_rows, num_cols])
+        for i in range(asc2.block_idx(), num_rows, asc2.block_num(), parallel=True):
+            row = asc2.load(x_gm, [1, tile_size], offsets=[i, 0])
+            row_minus_max = row - asc2.reduce_max(row)
+            numerator = asc2.exp(row_minus_max)
+            denominator = asc2.reduce_sum(numerator)
+            out = numerator / denominator
+            asc2.store(out, out_gm, offsets=[i, 0])
+
+    return softmax_kernel
+
+
+def _softmax_fused(**options):
+    # python/test/asc2/kernels/test_softmax_fused.py:16-24
+    @asc2.jit(**options)
+    def softmax_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: int,
+                       num_cols: asc.ConstExpr[int], block_size: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [num_rows, num_cols])
+        out_gm = asc2.tensor(out_ptr, [num_rows, num_cols])
+        start_rows = asc2.block_idx() * block_size
+        rows = asc2.load(x_gm, [block_size, num_cols], offsets=[start_rows, 0])
+        out = asc2.softmax(rows)
+        asc2.store(out, out_gm, offsets=[start_rows, 0])
+
+    return softmax_kernel
+
+
+def _softmax_inputs(dtype, rows, cols, seed, device, offset=0):
+    g = torch.Generator().manual_seed(seed)
+    base = (torch.randn(rows * cols + offset, generator=g) * 4).to(dtype).to(device)
+    x = base[offset:].view(rows, cols)  # offset 1: rows no longer start 16-byte aligned
+    out = torch.full((rows * cols + offset,), 7.0, dtype=dtype, device=device)[offset:].view(rows, cols)
+    return x, out
+
+
+@pytest.mark.parametrize("dtype,rows,cols,tile,offset", [
+    # one case per planned kernel: wave_1x2, wave_2x2, block_2x128 / 2x256 / 4x256 / 8x256, long
+    (torch.float32, 37, 100, 100, 0), (torch.float32, 64, 300, 300, 0), (torch.float32, 33, 1000, 1000, 0),
+    (torch.float32, 16, 2000, 2000, 0), (torch.float32, 9, 4000, 4000, 0), (torch.float32, 5, 8000, 8000, 0),
+    (torch.float32, 3, 9000, 9000, 0),
+    (torch.float32, 64, 1024, 1000, 0),   # tile narrower than the row: the rest is untouched
+    (torch.float32, 64, 1024, 1024, 1),   # unaligned rows
+    (torch.float32, 30, 100, 128, 0),     # tile wider than the row: padded_f32
+    (torch.float16, 64, 1024, 1024, 0), (torch.float16, 10, 100, 100, 1),  # f16
+    (torch.float16, 30, 100, 128, 0),     # padded_f16
+])
+def test_softmax_code_object_matches_library(device, cache_dir, dtype, rows, cols, tile, offset):
+    x, out_co = _softmax_inputs(dtype, rows, cols, rows * cols + tile, device, offset)
+    out_lib = out_co.clone()
+    plan = kernels.softmax_plan(x, out_co, rows, cols, tile, 16, False)
+    _softmax_rows()[16](x, out_co, rows, cols, tile)
+    kernels.softmax_rows(x, out_lib, rows, cols, tile, 16)
+    torch.cuda.synchronize()
+    assert torch.equal(out_co.view(torch.int16 if dtype == torch.float16 else torch.int32),
+                       out_lib.view(torch.int16 if dtype == torch.float16 else torch.int32)), plan.kernel
+    n = min(tile, cols)
+    assert (out_co[:, n:] == 7.0).all()
+    if tile <= cols:
+        torch.testing.assert_close(out_co[:, :n].float(), torch.softmax(x[:, :n].float(), dim=1),
+                                   rtol=1e-3 if dtype == torch.float16 else 1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype,rows,cols,block_size", [(torch.float32, 64, 1024, 4), (torch.float32, 100, 300, 3),
+                                                        (torch.float16, 64, 1024, 4)])
+def test_softmax_fused_code_object_matches_library(device, cache_dir, dtype, rows, cols, block_size):
+    x, out_co = _softmax_inputs(dtype, rows, cols, rows + cols, device)
+    out_lib = out_co.clone()
+    _softmax_fused()[16](x, out_co, rows, cols, block_size)
+    kernels.softmax_blocks(x, out_lib, rows, cols, block_size, 16)
+    torch.cuda.synchronize()
+    assert torch.equal(out_co, out_lib)
+    covered = min(rows, 16 * block_size)
+    assert (out_co[covered:] == 7.0).all()
+    torch.testing.assert_close(out_co[:covered].float(), torch.softmax(x[:covered].float(), dim=1),
+                               rtol=1e-3 if dtype == torch.float16 else 1e-5, atol=1e-6)
+
+
+def test_softmax_code_object_cache(device, cache_dir):
+    x, out = _softmax_inputs(torch.float32, 64, 1024, 3, device)
+    k = _softmax_rows()
+    loads = module.stats["module_loads"]
+    launches = module.stats["launches"]
+    for _ in range(4):  # one load, then memory-cache hits
+        k[16](x, out, 64, 1024, 1024)
+    assert module.stats["module_loads"] == loads + 1 and module.stats["launches"] == launches + 4
+    assert len(list(cache_dir.rglob("softmax_kernel.hsaco"))) == 1
+    always = _softmax_rows(always_compile=True)
+    always[16](x, out, 64, 1024, 1024)
+    always[16](x, out, 64, 1024, 1024)
+    assert module.stats["module_loads"] == loads + 3
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out, torch.softmax(x, dim=1), rtol=1e-5, atol=1e-6)
