@@ -91,6 +91,13 @@ class Workload:
     def cpu_baseline(self):
         return None
 
+    # The same operation through the ROCm library torch calls for it (None: no such
+    # library kernel), launched by vendor_launch on the workload's own inputs.
+    vendor_expression = None
+
+    def vendor_launch(self, i: int) -> None:
+        raise NotImplementedError
+
 
 def _sets_for(bytes_per_set: int) -> int:
     if bytes_per_set < SMALL_SET_BYTES:
@@ -164,7 +171,12 @@ def _cpu(work: float, scale: float, unit: str, expression: str, sample: str, tim
 
 class Softmax(Workload):
     bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "softmax"
-    sources = ("softmax.hip", "rows.h", "numeric.h", "common.h")
+    sources = ("softmax.hip", "softmax_kernels.h", "rows.h", "numeric.h", "common.h")
+    vendor_expression = "torch.softmax(x, dim=1) (PyTorch's ROCm softmax kernel)"
+
+    def vendor_launch(self, i: int) -> None:
+        import torch
+        torch.softmax(self.xs[i % len(self.xs)], dim=1)
 
     def __init__(self, rows: int, cols: int):
         self.rows, self.cols = rows, cols
@@ -242,7 +254,13 @@ class Copy(Workload):
 
 class Vadd(Workload):
     bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "vadd"
-    sources = ("vadd.hip", "numeric.h", "common.h")
+    sources = ("vadd.hip", "vadd_kernels.h", "numeric.h", "common.h")
+    vendor_expression = "torch.add(x, y, out=out) (PyTorch's ROCm elementwise kernel)"
+
+    def vendor_launch(self, i: int) -> None:
+        import torch
+        x, y, out = self.sets[i % len(self.sets)]
+        torch.add(x, y, out=out)
 
     def __init__(self, n: int):
         self.n = n
@@ -287,7 +305,7 @@ class Asc2VaddPlumbing(Workload):
     is device time per launch in microseconds; the launches are captured in a HIP graph, so host
     launch cost is not in it (launch_latency reports that)."""
     bound, unit, dtype, kernel_hint = "latency", "us", "f32", "vadd"
-    sources = ("vadd.hip", "numeric.h", "common.h")
+    sources = ("vadd.hip", "vadd_kernels.h", "numeric.h", "common.h")
     name = "asc2_vadd_kernel_8192_grid16"
 
     def setup(self, dev):
@@ -552,6 +570,16 @@ class Matmul(Workload):
     def work(self) -> float:
         return 2.0 * self.n ** 3
 
+    @property
+    def vendor_expression(self):
+        # the plain product only: torch has no fused bias + leaky-relu GEMM
+        return None if self.bias_leaky else "torch.matmul(a, b, out=c) (hipBLASLt)"
+
+    def vendor_launch(self, i: int) -> None:
+        import torch
+        a, b, c = self.sets[i % len(self.sets)]
+        torch.matmul(a, b, out=c)
+
     def config(self) -> dict:
         cfg = {"workload": self.name, "M": self.n, "N": self.n, "K": self.n, "layout": "A row-major, B row-major",
                "input": "randn/sqrt(K), seed 2", "accumulate": "fp32", "out": self.dtype,
@@ -609,6 +637,14 @@ class MatmulI8(Workload):
     def work(self) -> float:
         return 2.0 * self.M * self.N * self.K
 
+    # int8 GEMM with int32 output and no dequant: less epilogue work than this kernel's
+    vendor_expression = "torch._int_mm(a, b) (hipBLASLt int8, int32 C, no dequant)"
+
+    def vendor_launch(self, i: int) -> None:
+        import torch
+        a, b, _, _ = self.sets[i % len(self.sets)]
+        torch._int_mm(a, b)
+
     def config(self) -> dict:
         return {"workload": self.name, "M": self.M, "N": self.N, "K": self.K, "accumulate": "int32 (exact)",
                 "epilogue": "fp16(fp32(acc) * scale[n])", "input": "int8 uniform[-127,127], seed 3",
@@ -650,6 +686,13 @@ class FlashAttention(Workload):
         from pyasc_amd import kernels
         q, k, v, o = self.sets[i % len(self.sets)]
         kernels.flash_attention_fwd(q, k, v, o, 1 / math.sqrt(self.D), self.causal)
+
+    vendor_expression = "torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal) (ROCm SDPA)"
+
+    def vendor_launch(self, i: int) -> None:
+        import torch
+        q, k, v, _ = self.sets[i % len(self.sets)]
+        torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=self.causal)
 
     def work(self) -> float:
         full = 4.0 * self.B * self.H * self.S * self.S * self.D
@@ -754,6 +797,33 @@ def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True) -> di
     return {"workload": w.name, "ms_per_step": ms, "kernel_ms": kernel_ms, "value": value, "unit": w.unit,
             "rate": w.rate(kernel_ms / 1e3), "bound": w.bound, "config": w.config(),
             "timing": "hip-graph replay" if graph else "per-launch events"}
+
+
+def vendor(w: Workload, steps: int, res: dict):
+    """The workload's operation through torch's ROCm library kernel on the same inputs
+    (after ``measure``, which set them up), timed with one event pair per launch; None
+    when there is no library equivalent.  ``this_over_vendor`` = this build's rate / the
+    library's."""
+    if w.vendor_expression is None:
+        return None
+    import torch
+    try:
+        for i in range(3):
+            w.vendor_launch(i)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i in range(steps):
+            ev[i][0].record(stream)
+            w.vendor_launch(3 + i)
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+    except RuntimeError as e:  # the library refuses the shape or dtype
+        return {"expression": w.vendor_expression, "error": str(e).splitlines()[0][:200]}
+    ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    value = w.value(ms / 1e3)
+    return {"value": round(value, 3), "unit": w.unit, "ms_per_launch": ms, "expression": w.vendor_expression,
+            "timing": "per-launch events", "this_over_vendor": round(res["value"] / value, 3)}
 
 
 def roofline(w: Workload, res: dict) -> dict:
@@ -907,6 +977,7 @@ def main() -> int:
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time with per-launch event pairs, no HIP graph")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the ROCm library comparisons")
     ap.add_argument("--cpu-all", action="store_true", help=argparse.SUPPRESS)  # the default now
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
@@ -927,6 +998,7 @@ def main() -> int:
 
     head = WORKLOADS[args.workload]()
     res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph)
+    head_vendor = None if args.no_vendor else vendor(head, args.steps, res)
     print(f"bench: {head.name} {res['value']:.2f} {head.unit}", file=sys.stderr, flush=True)
     suite = {}
     if not args.no_suite:
@@ -936,10 +1008,13 @@ def main() -> int:
             w = WORKLOADS[name]()
             r = measure(w, max(5, args.steps // 2), max(2, args.warmup // 2), dev, graph=not args.no_graph)
             r["roofline"] = roofline(w, r)
+            r["vendor"] = None if args.no_vendor else vendor(w, max(5, args.steps // 2), r)
             if not args.no_cpu:
                 r["cpu_baseline"] = w.cpu_baseline()
             suite[name] = r
-            print(f"bench: {w.name} {r['value']:.2f} {w.unit}", file=sys.stderr, flush=True)
+            v = r["vendor"]
+            print(f"bench: {w.name} {r['value']:.2f} {w.unit}" +
+                  (f" (vendor {v['value']:.2f})" if v and "value" in v else ""), file=sys.stderr, flush=True)
             del w
             torch.cuda.empty_cache()
     latency = None if args.no_suite else launch_latency(dev)
@@ -970,6 +1045,7 @@ def main() -> int:
         "config": head.config(),
         "roofline": roofline(head, res),
         "cpu_baseline": cpu,
+        "vendor": head_vendor,
         "device": _native.device_info(0),
         "suite": suite,
         "launch_latency": latency,
