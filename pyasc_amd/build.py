@@ -49,6 +49,7 @@ PER_FILE_FLAGS = {
     "asc2_softmax.hip": ["-ffp-contract=off"],
     "matmul_i8.hip": ["-ffp-contract=off"],
     "elementwise.hip": ["-ffp-contract=off"],
+    "asc2_elementwise.hip": ["-ffp-contract=off"],
     "tile_ops.hip": ["-ffp-contract=off"],
 }
 

@@ -110,34 +110,46 @@ def _check_tiling(size: int, tile_size: int, tile_per_block: int, grid: int, wha
                          f"tile_per_block={tile_per_block}, grid={grid}")
 
 
+def leaky_relu_check(x: torch.Tensor, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
+                     grid: int) -> int:
+    """Host checks of a leaky_relu launch; returns the covered element count."""
+    _check_tiling(size, tile_size, tile_per_block, grid, "leaky_relu")
+    covered = vadd_covered(size, tile_size, tile_per_block, grid)
+    _check_stream_operands(((x, "x"), (out, "out")), covered)
+    return covered
+
+
 def leaky_relu(x: torch.Tensor, alpha: float, out: torch.Tensor, size: int, tile_size: int, tile_per_block: int,
                grid: int, stream: Any = None) -> None:
     """asc2 leaky_relu_kernel (python/test/asc2/kernels/test_leaky_relu.py:16-26):
     out = where(x >= 0, x, x * alpha) over the vadd-style covered range; ``alpha`` is
     used at its float value (a 0-dim bf16 tensor's exact value)."""
-    _check_tiling(size, tile_size, tile_per_block, grid, "leaky_relu")
+    leaky_relu_check(x, out, size, tile_size, tile_per_block, grid)
+    _native.call("asc_leaky_relu", _DTYPE_CODES[x.dtype], x.data_ptr(), float(alpha), out.data_ptr(), size,
+                 tile_size, tile_per_block, grid, _stream(stream))
+
+
+def vmuladd_check(x: torch.Tensor, y: torch.Tensor, z: torch.Tensor, out: torch.Tensor, size: int, tile_size: int,
+                  tile_per_block: int, grid: int) -> int:
+    """Host checks of a vmuladd launch; returns the covered element count."""
+    _check_tiling(size, tile_size, tile_per_block, grid, "vmuladd")
     covered = vadd_covered(size, tile_size, tile_per_block, grid)
-    code = _check_stream_operands(((x, "x"), (out, "out")), covered)
-    _native.call("asc_leaky_relu", code, x.data_ptr(), float(alpha), out.data_ptr(), size, tile_size,
-                 tile_per_block, grid, _stream(stream))
+    _check_stream_operands(((x, "x"), (y, "y"), (z, "z"), (out, "out")), covered)
+    return covered
 
 
 def vmuladd(x: torch.Tensor, y: torch.Tensor, z: torch.Tensor, out: torch.Tensor, size: int, tile_size: int,
             tile_per_block: int, grid: int, stream: Any = None) -> None:
     """asc2 vmuladd_kernel (python/test/asc2/kernels/test_vmuladd.py:16-31): out = x * y + z,
     multiply and add rounded separately."""
-    _check_tiling(size, tile_size, tile_per_block, grid, "vmuladd")
-    covered = vadd_covered(size, tile_size, tile_per_block, grid)
-    code = _check_stream_operands(((x, "x"), (y, "y"), (z, "z"), (out, "out")), covered)
-    _native.call("asc_vmuladd", code, x.data_ptr(), y.data_ptr(), z.data_ptr(), out.data_ptr(), size, tile_size,
-                 tile_per_block, grid, _stream(stream))
+    vmuladd_check(x, y, z, out, size, tile_size, tile_per_block, grid)
+    _native.call("asc_vmuladd", _DTYPE_CODES[x.dtype], x.data_ptr(), y.data_ptr(), z.data_ptr(), out.data_ptr(),
+                 size, tile_size, tile_per_block, grid, _stream(stream))
 
 
-def gelu_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, approximate: bool,
-              grid: int, stream: Any = None) -> None:
-    """asc2 gelu_kernel (python/test/asc2/kernels/test_gelu.py:19-33) on fp32 rows.  A tile
-    wider than the row computes the row's own columns (the padding is zeros and gelu is
-    element-wise) and writes nothing past them."""
+def gelu_rows_check(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int,
+                    grid: int) -> None:
+    """Host checks of a gelu launch."""
     if tile_size <= 0 or grid <= 0 or num_rows < 0 or num_cols < 0:
         raise ValueError(f"invalid gelu launch: rows={num_rows}, cols={num_cols}, tile={tile_size}, grid={grid}")
     for t, n in ((x, "x"), (out, "out")):
@@ -146,6 +158,14 @@ def gelu_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, 
             raise TypeError(f"gelu supports float32 only, '{n}' is {t.dtype}")
         if t.numel() < num_rows * num_cols:
             raise ValueError(f"'{n}' holds {t.numel()} elements but the launch touches {num_rows}x{num_cols}")
+
+
+def gelu_rows(x: torch.Tensor, out: torch.Tensor, num_rows: int, num_cols: int, tile_size: int, approximate: bool,
+              grid: int, stream: Any = None) -> None:
+    """asc2 gelu_kernel (python/test/asc2/kernels/test_gelu.py:19-33) on fp32 rows.  A tile
+    wider than the row computes the row's own columns (the padding is zeros and gelu is
+    element-wise) and writes nothing past them."""
+    gelu_rows_check(x, out, num_rows, num_cols, tile_size, grid)
     _native.call("asc_gelu_rows_f32", x.data_ptr(), out.data_ptr(), num_rows, num_cols, tile_size,
                  int(bool(approximate)), grid, _stream(stream))
 

@@ -47,37 +47,49 @@ def _asc2_matmul_dtype(t: torch.Tensor) -> None:
         raise TypeError(f"asc2 matmul supports float32, float16 and bfloat16 operands, got {t.dtype}")
 
 
-# ---------------------------------------------------------------------------------------------- vadd
+# ------------------------------------------------ vadd / leaky_relu / vmuladd / gelu code objects
 
-_VADD_CO_SUFFIX = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16", torch.int32: "i32"}
+STREAM_THREADS, STREAM_UNROLL = 256, 4  # kThreads, kUnroll of vadd_kernels.h and elementwise_kernels.h
+ELEM_MAX_GRID = 4096   # the elementwise element kernels are grid-stride (elementwise_kernels.h)
+GELU_MAX_GRID = 8192   # so are gelu's rows
+_CO_SUFFIX = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16", torch.int32: "i32"}
+
+
+def _stream_code_object(functions, vec: str, elem: str, tensors, covered: int, extra, stream: int,
+                        elem_max_grid: int = 0) -> None:
+    """The library's streaming launch (csrc/vadd.hip, csrc/elementwise.hip) through a code
+    object: kernel ``vec`` over the 16-byte vectors of [0, covered) when every tensor is
+    16-byte aligned, kernel ``elem`` over the rest; the kernels take the tensors'
+    pointers, then the range, then ``extra``."""
+    ptrs = [("ptr", t.data_ptr()) for t in tensors]
+    per_vec = 16 // tensors[0].element_size()
+    done = 0
+    if all(t.data_ptr() % 16 == 0 for t in tensors):
+        n_vec = covered // per_vec
+        if n_vec:
+            module.launch(functions[vec], ceildiv(n_vec, STREAM_THREADS * STREAM_UNROLL), STREAM_THREADS,
+                          ptrs + [("i64", n_vec)] + extra, stream)
+        done = n_vec * per_vec
+    if done < covered:
+        grid = ceildiv(covered - done, STREAM_THREADS)
+        if elem_max_grid:
+            grid = min(grid, elem_max_grid)
+        module.launch(functions[elem], grid, STREAM_THREADS, ptrs + [("i64", done), ("i64", covered)] + extra,
+                      stream)
 
 
 def _vadd_code_object_launch(call: KernelCall, functions) -> None:
-    """vadd_kernel through the asc2_vadd code object: the same device bodies and launch
-    geometry as asc_vadd (csrc/vadd.hip, vadd_kernels.h) -- 16-byte vectors of the
-    covered range when all three buffers are 16-byte aligned, one thread per element for
-    the rest -- with the kernels' arguments packed into one blob."""
+    """vadd_kernel through the asc2_vadd code object (the device bodies of vadd_kernels.h);
+    its element kernel takes one element per thread."""
     x, y, out = call.args["x_ptr"], call.args["y_ptr"], call.args["out_ptr"]
     covered = kernels.vadd_check(x, y, out, int(call.args["size"]), int(call.consts["tile_size"]),
                                  int(call.consts["tile_per_block"]), call.grid)
-    if covered == 0:
-        return
-    sfx = _VADD_CO_SUFFIX[x.dtype]
-    ptrs = [("ptr", x.data_ptr()), ("ptr", y.data_ptr()), ("ptr", out.data_ptr())]
-    per_vec = 16 // x.element_size()
-    done = 0
-    if all(t.data_ptr() % 16 == 0 for t in (x, y, out)):
-        n_vec = covered // per_vec
-        if n_vec:
-            module.launch(functions[f"asc2_vadd_vec_{sfx}"], ceildiv(n_vec, VADD_THREADS * VADD_UNROLL),
-                          VADD_THREADS, ptrs + [("i64", n_vec)], call.stream)
-        done = n_vec * per_vec
-    if done < covered:
-        module.launch(functions[f"asc2_vadd_elem_{sfx}"], ceildiv(covered - done, VADD_THREADS), VADD_THREADS,
-                      ptrs + [("i64", done), ("i64", covered)], call.stream)
+    if covered:
+        sfx = _CO_SUFFIX[x.dtype]
+        _stream_code_object(functions, f"asc2_vadd_vec_{sfx}", f"asc2_vadd_elem_{sfx}", (x, y, out), covered, [],
+                            call.stream)
 
 
-VADD_THREADS, VADD_UNROLL = 256, 4  # vadd_kernels.h: kThreads, kUnroll
 VADD_CODE_OBJECT = module.CodeObject(
     "asc2_vadd", tuple(f"asc2_vadd_{kind}_{sfx}" for sfx in ("f32", "f16", "bf16", "i32") for kind in ("vec", "elem")),
     _vadd_code_object_launch, "pyasc_amd/csrc/co/asc2_vadd.hip")
@@ -90,8 +102,6 @@ def _vadd(call: KernelCall) -> None:
                  int(call.consts["tile_size"]), int(call.consts["tile_per_block"]), call.grid, call.stream)
 
 
-# ------------------------------------------------------------------ leaky_relu / vmuladd / gelu
-
 def _scalar(v) -> float:
     """A by-value float argument: a python number or a 0-dim tensor (its exact value)."""
     if isinstance(v, torch.Tensor):
@@ -101,8 +111,56 @@ def _scalar(v) -> float:
     return float(v)
 
 
+# The kernels of the asc2_elementwise code object (csrc/co/asc2_elementwise.hip).
+ELEMENTWISE_CO_FUNCTIONS = tuple(
+    f"asc2_{op}_{kind}_{sfx}" for op in ("leaky_relu", "vmuladd") for kind in ("vec", "elem")
+    for sfx in ("f32", "f16", "bf16")) + ("asc2_gelu_rows_f32",)
+
+
+def _leaky_relu_code_object_launch(call: KernelCall, functions) -> None:
+    x, out = call.args["x_ptr"], call.args["out_ptr"]
+    covered = kernels.leaky_relu_check(x, out, int(call.args["size"]), int(call.consts["tile_size"]),
+                                       int(call.consts["tile_per_block"]), call.grid)
+    if covered:
+        sfx = _CO_SUFFIX[x.dtype]
+        _stream_code_object(functions, f"asc2_leaky_relu_vec_{sfx}", f"asc2_leaky_relu_elem_{sfx}", (x, out),
+                            covered, [("f32", _scalar(call.args["alpha"]))], call.stream, ELEM_MAX_GRID)
+
+
+def _vmuladd_code_object_launch(call: KernelCall, functions) -> None:
+    x, y, z, out = (call.args[n] for n in ("x_ptr", "y_ptr", "z_ptr", "out_ptr"))
+    covered = kernels.vmuladd_check(x, y, z, out, int(call.args["size"]), int(call.consts["tile_size"]),
+                                    int(call.consts["tile_per_block"]), call.grid)
+    if covered:
+        sfx = _CO_SUFFIX[x.dtype]
+        _stream_code_object(functions, f"asc2_vmuladd_vec_{sfx}", f"asc2_vmuladd_elem_{sfx}", (x, y, z, out),
+                            covered, [], call.stream, ELEM_MAX_GRID)
+
+
+def _gelu_code_object_launch(call: KernelCall, functions) -> None:
+    """gelu_kernel through the code object with asc_gelu_rows_f32's geometry: rows b, b +
+    grid, ... of min(rows, GELU_MAX_GRID) workgroups, the row's first min(tile, cols)
+    columns, 16-byte vectors when both buffers are aligned and rows are whole vectors."""
+    x, out = call.args["x_ptr"], call.args["out_ptr"]
+    rows, cols, tile = int(call.get("num_rows")), int(call.get("num_columns")), int(call.get("tile_size"))
+    kernels.gelu_rows_check(x, out, rows, cols, tile, call.grid)
+    if rows == 0:
+        return
+    vec_ok = x.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0 and cols % 4 == 0
+    module.launch(functions["asc2_gelu_rows_f32"], min(rows, GELU_MAX_GRID), STREAM_THREADS,
+                  [("ptr", x.data_ptr()), ("ptr", out.data_ptr()), ("i64", rows), ("i64", cols),
+                   ("i32", min(tile, cols)), ("i32", int(bool(call.get("approximate")))), ("i32", int(vec_ok))],
+                  call.stream)
+
+
+def _elementwise_code_object(launch) -> module.CodeObject:
+    return module.CodeObject("asc2_elementwise", ELEMENTWISE_CO_FUNCTIONS, launch,
+                             "pyasc_amd/csrc/co/asc2_elementwise.hip")
+
+
 @register("leaky_relu_kernel", ("x_ptr", "alpha", "out_ptr", "size", "tile_size", "tile_per_block"),
-          "python/test/asc2/kernels/test_leaky_relu.py:16-26")
+          "python/test/asc2/kernels/test_leaky_relu.py:16-26",
+          code_object=_elementwise_code_object(_leaky_relu_code_object_launch))
 def _leaky_relu(call: KernelCall) -> None:
     kernels.leaky_relu(call.args["x_ptr"], _scalar(call.args["alpha"]), call.args["out_ptr"],
                        int(call.args["size"]), int(call.consts["tile_size"]), int(call.consts["tile_per_block"]),
@@ -111,7 +169,8 @@ def _leaky_relu(call: KernelCall) -> None:
 
 @register("vmuladd_kernel", ("x_ptr", "y_ptr", "z_ptr", "out_ptr", "size", "tile_size", "tile_per_block",
                              "buffer_factor"),
-          "python/test/asc2/kernels/test_vmuladd.py:16-31")
+          "python/test/asc2/kernels/test_vmuladd.py:16-31",
+          code_object=_elementwise_code_object(_vmuladd_code_object_launch))
 def _vmuladd(call: KernelCall) -> None:
     # buffer_factor is the reference loop's unroll/double-buffer hint; it does not change the result
     kernels.vmuladd(call.args["x_ptr"], call.args["y_ptr"], call.args["z_ptr"], call.args["out_ptr"],
@@ -120,7 +179,7 @@ def _vmuladd(call: KernelCall) -> None:
 
 
 @register("gelu_kernel", ("x_ptr", "out_ptr", "num_rows", "num_columns", "tile_size", "approximate"),
-          "python/test/asc2/kernels/test_gelu.py:19-33")
+          "python/test/asc2/kernels/test_gelu.py:19-33", code_object=_elementwise_code_object(_gelu_code_object_launch))
 def _gelu(call: KernelCall) -> None:
     kernels.gelu_rows(call.args["x_ptr"], call.args["out_ptr"], int(call.get("num_rows")),
                       int(call.get("num_columns")), int(call.get("tile_size")), bool(call.get("approximate")),

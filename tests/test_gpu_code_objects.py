@@ -223,3 +223,127 @@ def test_softmax_code_object_cache(device, cache_dir):
     assert module.stats["module_loads"] == loads + 3
     torch.cuda.synchronize()
     torch.testing.assert_close(out, torch.softmax(x, dim=1), rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------- leaky_relu / vmuladd / gelu
+
+def _leaky_relu():
+    # python/test/asc2/kernels/test_leaky_relu.py:16-26
+    @asc2.jit
+    def leaky_relu_kernel(x_ptr: asc.GlobalAddress, alpha: float, out_ptr: asc.GlobalAddress, size: int,
+                          tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [size])
+        out_gm = asc2.tensor(out_ptr, [size])
+        base_offset = asc2.block_idx() * tile_size * tile_per_block
+        for i in range(tile_per_block):
+            tile_offset = base_offset + i * tile_size
+            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
+            out = asc2.where(x >= 0, x, x * alpha)
+            asc2.store(out, out_gm, offsets=[tile_offset])
+
+    return leaky_relu_kernel
+
+
+def _vmuladd():
+    # python/test/asc2/kernels/test_vmuladd.py:16-31
+    @asc2.jit(vf_fusion=True)
+    def vmuladd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, z_ptr: asc.GlobalAddress,
+                       out_ptr: asc.GlobalAddress, size: int, tile_size: asc.ConstExpr[int],
+                       tile_per_block: asc.ConstExpr[int], buffer_factor: asc.ConstExpr[int]):
+        x_gm = asc2.tensor(x_ptr, [size])
+        y_gm = asc2.tensor(y_ptr, [size])
+        z_gm = asc2.tensor(z_ptr, [size])
+        out_gm = asc2.tensor(out_ptr, [size])
+        base_offset = asc2.block_idx() * tile_size * tile_per_block
+        for i in range(tile_per_block):
+            tile_offset = base_offset + i * tile_size
+            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
+            y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
+            z = asc2.load(z_gm, [tile_size], offsets=[tile_offset])
+            asc2.store(x * y + z, out_gm, offsets=[tile_offset])
+
+    return vmuladd_kernel
+
+
+def _gelu():
+    # python/test/asc2/kernels/test_gelu.py:19-33
+    @asc2.jit
+    def gelu_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: asc.ConstExpr,
+                    num_columns: asc.ConstExpr, tile_size: asc.ConstExpr, approximate: asc.ConstExpr):
+        x_gm = asc2.tensor(x_ptr, [num_rows, num_columns])
+        out_gm = asc2.tensor(out_ptr, [num_rows, num_columns])
+        for i in range(asc2.block_idx(), num_rows, asc2.block_num()):
+            row = asc2.load(x_gm, [1, tile_size], offsets=[i, 0])
+            if approximate:
+                pi = 3.141592653589793238462643383279502884
+                k1 = 2 * asc2.sqrt(2 / pi)
+                k2 = 2 * asc2.sqrt(2 / pi) * 0.044715
+                param = row * (row * row * k2 + k1)
+                out = row - row / (asc2.exp(param) + 1)
+            else:
+                k = asc2.sqrt(0.5)
+                out = row * (asc2.erf(row * k) + 1) * 0.5
+            asc2.store(out, out_gm, offsets=[i, 0])
+
+    return gelu_kernel
+
+
+def _bits_equal(a, b):
+    view = torch.int16 if a.element_size() == 2 else torch.int32
+    return torch.equal(a.view(view), b.view(view))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("size,tile,tpb,grid,offset", [(8192, 128, 4, 16, 0), (3001, 7, 5, 11, 0),
+                                                      (1 << 20, 128, 512, 16, 0), (5000, 64, 5, 16, 1),
+                                                      (1 << 21, 128, 1024, 16, 1)])
+def test_leaky_relu_and_vmuladd_code_objects_match_library(device, cache_dir, dtype, size, tile, tpb, grid,
+                                                           offset):
+    # offset 1: unaligned views take the element kernel (past 2^20 elements: its grid-stride loop)
+    g = torch.Generator().manual_seed(size + tile)
+    x, y, z = ((torch.randn(size + offset, generator=g) * 3).to(dtype).to(device)[offset:] for _ in range(3))
+    alpha = 0.1 if dtype == torch.float32 else float(torch.tensor(0.1, dtype=dtype).item())
+    fill = torch.full((size + offset,), 5.0, dtype=dtype, device=device)[offset:]
+    co, lib = fill.clone(), fill.clone()
+    _leaky_relu()[grid](x, alpha, co, size, tile, tpb)
+    kernels.leaky_relu(x, alpha, lib, size, tile, tpb, grid)
+    torch.cuda.synchronize()
+    assert _bits_equal(co, lib)
+    co, lib = fill.clone(), fill.clone()
+    _vmuladd()[grid](x, y, z, co, size, tile, tpb, 2)
+    kernels.vmuladd(x, y, z, lib, size, tile, tpb, grid)
+    torch.cuda.synchronize()
+    assert _bits_equal(co, lib)
+    covered = min(size, grid * tpb * tile)
+    assert (co[covered:] == 5.0).all()
+    if dtype != torch.float32:  # torch's own mul-then-add in that dtype, bit-exact
+        assert _bits_equal(co[:covered], (x[:covered] * y[:covered] + z[:covered]))
+
+
+@pytest.mark.parametrize("approximate", [True, False])
+@pytest.mark.parametrize("rows,cols,tile,offset", [(30, 1024, 1024, 0), (37, 1000, 1000, 0), (64, 4096, 3000, 0),
+                                                   (9, 100, 128, 0), (10000, 64, 64, 0), (33, 256, 256, 1)])
+def test_gelu_code_object_matches_library(device, cache_dir, approximate, rows, cols, tile, offset):
+    g = torch.Generator().manual_seed(rows * cols)
+    x = (torch.randn(rows * cols + offset, generator=g) * 3).to(device)[offset:].view(rows, cols)
+    fill = torch.full((rows * cols + offset,), 5.0, device=device)[offset:].view(rows, cols)
+    co, lib = fill.clone(), fill.clone()
+    _gelu()[16](x, co, rows, cols, tile, approximate)
+    kernels.gelu_rows(x, lib, rows, cols, tile, approximate, 16)
+    torch.cuda.synchronize()
+    assert _bits_equal(co, lib)
+    n = min(tile, cols)
+    assert (co[:, n:] == 5.0).all()
+
+
+def test_elementwise_code_object_loaded_once(device, cache_dir):
+    x = torch.randn(8192, device=device)
+    out = torch.empty_like(x)
+    k = _leaky_relu()
+    loads = module.stats["module_loads"]
+    for _ in range(3):
+        k[16](x, 0.2, out, 8192, 128, 4)
+    assert module.stats["module_loads"] == loads + 1
+    assert len(list(cache_dir.rglob("leaky_relu_kernel.hsaco"))) == 1
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.where(x >= 0, x, x * torch.tensor(0.2, dtype=torch.float32)))

@@ -644,6 +644,20 @@ def test_code_object_compiled_path(tmp_path, monkeypatch):
         assert name.encode() + b".kd" in data
 
 
+def test_every_code_object_holds_its_kernels():
+    # each registered code object is built and is a gfx950 ELF with every kernel its launcher names
+    from pyasc_amd import launchers  # noqa: F401  (registers the kernels)
+    from pyasc_amd.registry import entries
+    with_co = {(name, params): e.code_object for (name, params), e in entries().items() if e.code_object}
+    assert {name for name, _ in with_co} == {"vadd_kernel", "softmax_kernel", "leaky_relu_kernel", "vmuladd_kernel",
+                                             "gelu_kernel"}
+    for co in set(with_co.values()):
+        data = co.path.read_bytes()
+        assert data[:4] == b"\x7fELF" and b"gfx950" in data, co.name
+        for name in co.functions:
+            assert name.encode() + b".kd" in data, (co.name, name)
+
+
 def test_pack_args_layout():
     from pyasc_amd.asc.runtime import module
     blob = module.pack_args([("ptr", 0x1000), ("i32", 7), ("i64", -2), ("f32", 1.5), ("ptr", 0x2000)])
