@@ -349,7 +349,7 @@ class Asc2VaddPlumbing(Workload):
 
 class LeakyRelu(Workload):
     """test_leaky_relu.py's kernel at a bandwidth size: bf16, alpha a 0-dim bf16 tensor (0.1)."""
-    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "bf16", "map_vec_kernel"
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "bf16", "leaky_relu_vec"
     sources = ("elementwise.hip", "elementwise_kernels.h", "numeric.h", "common.h")
 
     def __init__(self, n: int):
@@ -388,7 +388,7 @@ class LeakyRelu(Workload):
 
 class VMulAdd(Workload):
     """test_vmuladd.py's kernel at a bandwidth size (fp32, tile 32 as in vmuladd_launch)."""
-    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "map_vec_kernel"
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "vmuladd_vec"
     sources = ("elementwise.hip", "elementwise_kernels.h", "numeric.h", "common.h")
 
     def __init__(self, n: int):
@@ -427,7 +427,7 @@ class VMulAdd(Workload):
 
 class Gelu(Workload):
     """test_gelu.py's kernel at softmax's second shape (fp32 rows, tile = row length)."""
-    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "gelu_rows_kernel"
+    bound, unit, dtype, kernel_hint = "hbm", "GB/s", "f32", "gelu_rows_f32"
     sources = ("elementwise.hip", "elementwise_kernels.h", "numeric.h", "common.h")
 
     def __init__(self, rows: int, cols: int, approximate: bool):
