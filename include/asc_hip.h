@@ -93,6 +93,20 @@ int32_t asc_module_launch(void* function, uint32_t grid, uint32_t block,
                           const void* args, uint64_t args_size,
                           asc_stream_t stream);
 
+/* A launch of one kernel of a prebuilt code object whose argument is a single
+ * struct: the kernel's symbol, its grid and block, and the struct's bytes as the
+ * argument blob asc_module_launch takes.  asc_flash_attention_plan,
+ * asc_matmul_plan and asc_matmul_i8_plan fill it with exactly the launch their
+ * library entry points make.  No counterpart in the reference, whose compiler
+ * fixes the launch inside the kernel binary. */
+typedef struct asc_launch_plan {
+  char kernel[64];   /* NUL-terminated symbol; empty when there is nothing to launch */
+  uint32_t grid;     /* workgroups (0: nothing to launch) */
+  uint32_t block;    /* threads per workgroup */
+  uint64_t args_size;
+  uint64_t args[16]; /* the first args_size bytes are the argument blob */
+} asc_launch_plan_t;
+
 /* ---- vadd ----------------------------------------------------------------
  * asc2 vadd_kernel(x_ptr, y_ptr, out_ptr, size: int, tile_size: ConstExpr[int],
  *                  tile_per_block: ConstExpr[int])
@@ -276,6 +290,15 @@ int32_t asc_matmul_bias_act(int32_t in_dtype, int32_t out_dtype, const void* a,
                             int64_t M, int64_t N, int64_t K, int64_t lda,
                             int64_t ldb, int64_t ldc, int32_t act, float alpha,
                             asc_stream_t stream);
+/* The launch asc_matmul_bias_act makes with these arguments (asc_matmul(...,
+ * relu) is act = relu, bias NULL), as a kernel of the code object
+ * pyasc_amd/lib/co/asc2_matmul.hsaco (asc_launch_plan_t; the blob is the
+ * kernel's argument struct).  Same checks and errors. */
+int32_t asc_matmul_plan(int32_t in_dtype, int32_t out_dtype, const void* a,
+                        const void* b, void* c, const float* bias, int64_t M,
+                        int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                        int64_t ldc, int32_t act, float alpha,
+                        asc_launch_plan_t* plan);
 
 /* ---- int8 matmul with per-channel dequant -----------------------------------
  * asc1 matmul_kernel(a, b, c, tiling, workspace, quant_vector) with
@@ -297,6 +320,13 @@ int32_t asc_matmul_i8_dequant_f16(const int8_t* a, const int8_t* b,
                                   const float* scale, void* c, int64_t M,
                                   int64_t N, int64_t K, int32_t trunc19,
                                   asc_stream_t stream);
+/* The launch asc_matmul_i8_i32 (dequant 0; scale and trunc19 ignored) or
+ * asc_matmul_i8_dequant_f16 (dequant 1) makes, as a kernel of the code object
+ * pyasc_amd/lib/co/asc2_matmul_i8.hsaco.  Same checks and errors. */
+int32_t asc_matmul_i8_plan(const int8_t* a, const int8_t* b, const float* scale,
+                           void* c, int64_t M, int64_t N, int64_t K,
+                           int32_t dequant, int32_t trunc19,
+                           asc_launch_plan_t* plan);
 
 /* ---- flash-attention forward ---------------------------------------------------
  * No reference function exists (the reference has no attention kernel); this
@@ -314,6 +344,14 @@ int32_t asc_flash_attention_fwd_bf16(const void* q, const void* k,
                                      int64_t seq_len, int32_t head_dim,
                                      float sm_scale, int32_t causal,
                                      asc_stream_t stream);
+/* The launch asc_flash_attention_fwd_bf16 makes with these arguments, as a
+ * kernel of the code object pyasc_amd/lib/co/asc2_flash_attention.hsaco.  Same
+ * checks and errors (a causal plan reads the current device's CU count). */
+int32_t asc_flash_attention_plan(const void* q, const void* k, const void* v,
+                                 void* o, float* lse, int64_t batch,
+                                 int64_t heads, int64_t seq_len,
+                                 int32_t head_dim, float sm_scale,
+                                 int32_t causal, asc_launch_plan_t* plan);
 
 /* ---- element-wise tile operations ------------------------------------------------
  * The generic kernels of the reference's operation tests, one op per launch:

@@ -41,6 +41,15 @@ class SoftmaxPlan(ctypes.Structure):
                 ("rows", _c_i64), ("stride", _c_i64), ("len", _c_i32), ("flag", _c_i32)]
 
 
+class LaunchPlan(ctypes.Structure):
+    """asc_launch_plan_t: a code-object kernel's name, grid, block and argument blob."""
+    _fields_ = [("kernel", ctypes.c_char * 64), ("grid", ctypes.c_uint32), ("block", ctypes.c_uint32),
+                ("args_size", ctypes.c_uint64), ("args", ctypes.c_uint64 * 16)]
+
+    def blob(self) -> bytes:
+        return ctypes.string_at(ctypes.addressof(self.args), self.args_size)
+
+
 # name -> argtypes; every entry point returns int32_t.
 SIGNATURES = {
     "asc_device_info": [_c_i32, ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32),
@@ -69,6 +78,11 @@ SIGNATURES = {
     "asc_matmul_i8_dequant_f16": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
     "asc_flash_attention_fwd_bf16": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_f32, _c_i32,
                                      _c_p],
+    "asc_flash_attention_plan": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_f32, _c_i32,
+                                 ctypes.POINTER(LaunchPlan)],
+    "asc_matmul_plan": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
+                        _c_f32, ctypes.POINTER(LaunchPlan)],
+    "asc_matmul_i8_plan": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, ctypes.POINTER(LaunchPlan)],
     "asc_unary_f32": [_c_i32, _c_p, _c_p, _c_i64, _c_p],
     "asc_binary": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f64, _c_i64, _c_p],
     "asc_where_cmp": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f64, _c_i64, _c_f64, _c_f64, _c_p],

@@ -111,11 +111,24 @@ def pack_args(fields: Sequence[Tuple[str, object]]) -> bytes:
 
 
 def launch(function: int, grid: int, block: int, fields: Sequence[Tuple[str, object]], stream: int) -> None:
-    """One launch of a loaded kernel on ``stream`` (asc_module_launch)."""
+    """One launch of a loaded kernel on ``stream`` (asc_module_launch), its arguments
+    packed from ``fields``."""
+    launch_blob(function, grid, block, pack_args(fields), stream)
+
+
+def launch_blob(function: int, grid: int, block: int, blob: bytes, stream: int) -> None:
+    """One launch of a loaded kernel on ``stream`` with an argument blob laid out as the
+    kernel declares its arguments."""
     from ... import _native
     if grid <= 0 or grid >= 1 << 32:
         raise ValueError(f"grid {grid} outside the launch range")
-    blob = pack_args(fields)
     buf = ctypes.create_string_buffer(blob, len(blob))
     _native.call("asc_module_launch", ctypes.c_void_p(function), grid, block, buf, len(blob), ctypes.c_void_p(stream))
     stats["launches"] += 1
+
+
+def launch_plan(functions: Dict[str, int], plan, stream: int) -> None:
+    """Launches an asc_launch_plan_t (``_native.LaunchPlan``) filled by one of the
+    library's plan functions; nothing when its grid is 0."""
+    if plan.grid:
+        launch_blob(functions[plan.kernel.decode()], plan.grid, plan.block, plan.blob(), stream)

@@ -48,6 +48,7 @@ PER_FILE_FLAGS = {
     "softmax.hip": ["-ffp-contract=off"],
     "asc2_softmax.hip": ["-ffp-contract=off"],
     "matmul_i8.hip": ["-ffp-contract=off"],
+    "asc2_matmul_i8.hip": ["-ffp-contract=off"],
     "elementwise.hip": ["-ffp-contract=off"],
     "asc2_elementwise.hip": ["-ffp-contract=off"],
     "tile_ops.hip": ["-ffp-contract=off"],

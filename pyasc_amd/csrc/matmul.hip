@@ -1,356 +1,47 @@
 // Dense matmul C = epilogue(A . B) for the asc2 cube path
 // (python/asc/language/tile/binary_ops.py:180-221; kernels in
-// python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py).
-//
-// fp16/bf16 inputs run on MFMA (v_mfma_f32_32x32x16_{bf16,f16}) with fp32
-// accumulation and a 256x256 output tile per workgroup:
-//   - tile-aligned shapes (M, N multiples of 256, K of 32, offsets within
-//     32 bits): the direct-to-LDS loop of gemm_direct.h with 8 waves in 2x4,
-//     each 128x64 = 4x2 MFMA blocks, two waves per SIMD -- operands go from HBM
-//     straight into five 32 KiB LDS stages, B stays row-major and its
-//     K-contiguous MFMA operand comes from LDS transpose reads;
-//   - other shapes: the register-staged loop of gemm_core.h (4 waves in 2x2,
-//     each 128x128) with bounds-checked loads (zero fill), B transposed in
-//     registers, masked stores;
-//   - XCD-aware, grouped tile order (gemm_common.h).
-// The epilogue applies the fixpipe relu and the RNE cast to fp16/bf16, or
-// stores fp32 as is.
-//
-// fp32 inputs (test_matmul_fixpipe.py's float32 case; the asc1 kernels of
-// python/test/kernels/test_matmul.py, test_matmul_torch.py) run on
-// v_mfma_f32_16x16x4_f32 up to 2048x2048 outputs, and on a plain LDS-tiled FMA
-// kernel beyond that.
-#include "common.h"
-#include "gemm_common.h"
-#include "gemm_core.h"
-#include "gemm_direct.h"
-#include "numeric.h"
+// python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py): the
+// library's entry points and the launch plan the asc2 code-object path replays.
+// The device code and the choice of kernels are described in matmul_kernels.h.
+#include "matmul_kernels.h"
 
 namespace {
 
-using asc::gemm::u32x4;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+using asc::mm::BM;
+using asc::mm::BN;
+using asc::mm::Epilogue;
+using asc::mm::GemmArgs;
 
-constexpr int BM = asc::gemm::kTileM;
-constexpr int BN = asc::gemm::kTileN;
-constexpr int BK = 64;  // 16-bit elements per LDS row = 128 bytes
-constexpr int kThreads = asc::gemm::kGemmThreads;
-constexpr int kStageBytes = asc::gemm::kStageBytes;
+ASC_MM_KERNELS(, mm_)
 
-enum OutKind { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
+// Kernel index = 6 * output dtype (f32, f16, bf16) + kind, kind 0-5 in the order below.
+constexpr int kKinds = 6;
+constexpr const char* kKindNames[kKinds] = {"mfma_bf16_fast_", "mfma_bf16_checked_", "mfma_f16_fast_",
+                                            "mfma_f16_checked_", "f32_mfma_", "f32_fma_"};
+constexpr const char* kOutNames[3] = {"f32", "f16", "bf16"};
+using KernelFn = void (*)(GemmArgs);
+const KernelFn kKernels[3 * kKinds] = {
+    mm_mfma_bf16_fast_f32,  mm_mfma_bf16_checked_f32,  mm_mfma_f16_fast_f32,  mm_mfma_f16_checked_f32,
+    mm_f32_mfma_f32,        mm_f32_fma_f32,            mm_mfma_bf16_fast_f16, mm_mfma_bf16_checked_f16,
+    mm_mfma_f16_fast_f16,   mm_mfma_f16_checked_f16,   mm_f32_mfma_f16,       mm_f32_fma_f16,
+    mm_mfma_bf16_fast_bf16, mm_mfma_bf16_checked_bf16, mm_mfma_f16_fast_bf16, mm_mfma_f16_checked_bf16,
+    mm_f32_mfma_bf16,       mm_f32_fma_bf16};
 
-// Epilogue on the fp32 accumulator, before the output cast: optional
-// per-column bias (fp32 add), then an activation -- 0 none, 1 relu (fixpipe
-// relu), 2 leaky relu v >= 0 ? v : v * alpha.
-struct Epilogue {
-  const float* bias;  // [N] or null
-  int act;
-  float alpha;
-  __device__ __forceinline__ float operator()(float v, float bias_n) const {
-    if (bias != nullptr) v += bias_n;
-    if (act == 1) {
-      v = fmaxf(v, 0.0f);
-    } else if (act == 2) {
-      v = v >= 0.0f ? v : v * alpha;
-    }
-    return v;
-  }
-  __device__ __forceinline__ float bias_at(int n) const { return bias != nullptr ? bias[n] : 0.0f; }
+// One matmul launch: kernel index, arguments, grid.
+struct MmLaunch {
+  int kernel = 0;
+  GemmArgs p{};
+  int64_t blocks = 0;  // 0: nothing to launch
+  int threads = 0;
 };
 
-struct GemmArgs {
-  const uint16_t* a;
-  const uint16_t* b;
-  void* c;
-  int M, N, K;
-  int64_t lda, ldb, ldc;
-  Epilogue epi;
-  int tiles_m, tiles_n;
-};
-
-// 8 consecutive 16-bit elements of row `row`, columns col..col+7 of a row-major
-// [rows x cols] matrix; out-of-range elements read as 0.
-template <bool kChecked>
-__device__ __forceinline__ u32x4 load_chunk(const uint16_t* base, int64_t ld, int row, int col, int rows, int cols,
-                                            bool vec_ok) {
-  const uint16_t* p = base + row * ld + col;
-  if (!kChecked) return *reinterpret_cast<const u32x4*>(p);
-  if (row < rows && vec_ok && col + 7 < cols) return *reinterpret_cast<const u32x4*>(p);
-  uint16_t e[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) e[i] = (row < rows && col + i < cols) ? p[i] : uint16_t(0);
-  u32x4 v;
-  __builtin_memcpy(&v, e, 16);
-  return v;
+int out_index(int32_t out_dtype) {
+  return out_dtype == ASC_DT_FLOAT32 ? 0 : out_dtype == ASC_DT_FLOAT16 ? 1 : out_dtype == ASC_DT_BFLOAT16 ? 2 : -1;
 }
 
-template <bool kBf16>
-struct Tr16 {
-  using Elem = uint16_t;
-  using Acc = f32x16;
-  using BReg = u32x4;
-  static constexpr int kBK = BK;
-  static constexpr int kBRows = 8;
-  template <bool kChecked>
-  __device__ __forceinline__ static u32x4 load_a(const uint16_t* base, int64_t ld, int row, int col, int rows,
-                                                 int cols, bool vec_ok) {
-    return load_chunk<kChecked>(base, ld, row, col, rows, cols, vec_ok);
-  }
-  template <bool kChecked>
-  __device__ __forceinline__ static u32x4 load_b(const uint16_t* base, int64_t ld, int row, int col, int rows,
-                                                 int cols, bool vec_ok) {
-    return load_chunk<kChecked>(base, ld, row, col, rows, cols, vec_ok);
-  }
-  __device__ __forceinline__ static void transpose_b(const u32x4 (&in)[8], u32x4 (&out)[8]) {
-    asc::gemm::transpose8x8_b16(in, out);
-  }
-  __device__ __forceinline__ static f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
-    if constexpr (kBf16) {
-      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                     c, 0, 0, 0);
-    } else {
-      return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                    0, 0, 0);
-    }
-  }
-};
-
-// Waves across the 256 columns of the fast path's tile: 2 (one wave per SIMD,
-// 128x128 accumulators each) or 4 (two waves per SIMD, 128x64 each).
-constexpr int kFastWavesN = 4;
-using FastLoopBf16 = asc::gemm::GemmDirectLoop<Tr16<true>, kFastWavesN>;
-constexpr int kFastThreads = FastLoopBf16::kThreads;
-
-template <bool kBf16, bool kChecked, int kOut>
-__global__ void __launch_bounds__(kChecked ? kThreads : kFastThreads, 1) gemm_mfma_kernel(GemmArgs p) {
-  int tm, tn;
-  asc::gemm::tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, asc::gemm::kGroupM, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int lane = threadIdx.x & 63;
-  if constexpr (!kChecked) {
-    // the LDS stages as distinct objects (see gemm_direct.h)
-    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds2[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds3[asc::gemm::kDirectStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds4[asc::gemm::kDirectStageBytes];
-    static_assert(asc::gemm::kDirectStages == 5, "one __shared__ stage object per ring stage");
-    using Loop = asc::gemm::GemmDirectLoop<Tr16<kBf16>, kFastWavesN>;
-    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave-uniform (SGPR)
-    Loop L;
-    L.a = p.a;
-    L.b = p.b;
-    L.m0 = m0;
-    L.n0 = n0;
-    L.lane = lane;
-    L.wave = wave;
-    L.wm = wave / kFastWavesN;
-    L.wn = wave % kFastWavesN;
-    L.lds[0] = lds0;
-    L.lds[1] = lds1;
-    L.lds[2] = lds2;
-    L.lds[3] = lds3;
-    L.lds[4] = lds4;
-    L.init(p.lda, p.ldb);
-    f32x16 acc[4][Loop::kJ];
-    L.run(p.K, acc);
-    // Epilogue: the whole tile is in bounds and C's rows are 16-byte aligned, so the
-    // results leave through quad-transposed wide stores.
-    const int n_base = n0 + L.wn * 32 * Loop::kJ;
-    float bias_n[Loop::kJ];
-#pragma unroll
-    for (int j = 0; j < Loop::kJ; ++j) bias_n[j] = p.epi.bias_at(n_base + j * 32 + (lane & 31));
-    const auto conv = [&](int j, float x) -> uint32_t {
-      const float v = p.epi(x, bias_n[j]);
-      if constexpr (kOut == kOutF32) return __float_as_uint(v);
-      else if constexpr (kOut == kOutF16) return asc::f32_to_f16_rne(v);
-      else return asc::f32_to_bf16_rne(v);
-    };
-    asc::gemm::store_wave_tile<kOut == kOutF32 ? 4 : 2, Loop::kJ>(acc, conv, p.c, p.ldc, m0 + L.wm * 128, n_base,
-                                                                   lane);
-  } else {
-    const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
-    f32x16 acc[4][4];
-    __shared__ __attribute__((aligned(16))) uint8_t lds0[asc::gemm::kStageBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds1[asc::gemm::kStageBytes];
-    asc::gemm::GemmMainLoop<Tr16<kBf16>, true> L;
-    L.a = p.a;
-    L.b = p.b;
-    L.s = asc::gemm::GemmShape{p.M, p.N, p.K, p.lda, p.ldb, p.tiles_m, p.tiles_n};
-    L.m0 = m0;
-    L.n0 = n0;
-    L.tid = threadIdx.x;
-    L.lane = lane;
-    L.wm = wm;
-    L.wn = wn;
-    // vector loads need 16-byte aligned chunks
-    L.a_vec = ((reinterpret_cast<uintptr_t>(p.a) | (p.lda * 2)) & 15) == 0;
-    L.b_vec = ((reinterpret_cast<uintptr_t>(p.b) | (p.ldb * 2)) & 15) == 0;
-    L.lds[0] = lds0;
-    L.lds[1] = lds1;
-    L.run(acc);
-    // Epilogue.  MFMA 32x32 result layout: lane holds column lane%32 of the block,
-    // register r holds row 8*(r/4) + 4*(lane/32) + r%4.
-    const int col_in = lane & 31;
-    const int row_q = (lane >> 5) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 128 + j * 32 + col_in;
-        const float bias_n = n < p.N ? p.epi.bias_at(n) : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + row_q + (r & 3);
-          if (m >= p.M || n >= p.N) continue;
-          const float v = p.epi(acc[i][j][r], bias_n);
-          const int64_t off = static_cast<int64_t>(m) * p.ldc + n;
-          if constexpr (kOut == kOutF32) {
-            static_cast<float*>(p.c)[off] = v;
-          } else if constexpr (kOut == kOutF16) {
-            static_cast<uint16_t*>(p.c)[off] = asc::f32_to_f16_rne(v);
-          } else {
-            static_cast<uint16_t*>(p.c)[off] = asc::f32_to_bf16_rne(v);
-          }
-        }
-      }
-    }
-  }
-}
-
-// ---- fp32 inputs, small outputs: v_mfma_f32_16x16x4_f32.  A 256-thread workgroup
-// owns one 16x16 output block and splits K over its four waves: wave w takes the
-// 16-value k-groups w, w+4, ...; the four partial blocks meet in LDS and wave 0 sums
-// them in wave order, then runs the epilogue.  Operands come from global memory (L2)
-// straight into registers.  Lane l holds row l%16 of A and column l%16 of B; in
-// k-group g, MFMA step j uses k = 16g + 4*(l/16) + j in both operands, so the four
-// steps of a group cover its 16 values once (the order of k within a sum is free).
-// D layout: lane l holds rows 4*(l/16) + r (r = 0..3) of column l%16.
-// Out-of-range rows, columns and k read a clamped in-bounds address and use 0.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr int kF32MfmaMaxBlocks = 16384;  // 16x16 output blocks: up to 2048 x 2048 outputs
-
-template <int kOut>
-__global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float* __restrict__ a,
-                                                            const float* __restrict__ b, void* c, int M, int N,
-                                                            int K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                            Epilogue epi) {
-  __shared__ f32x4 partial[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
-  const int r = lane & 15, q = lane >> 4;
-  const bool a_ok = m0 + r < M, b_ok = n0 + r < N;
-  const float* arow = a + static_cast<int64_t>(a_ok ? m0 + r : 0) * lda;
-  const float* bcol = b + (b_ok ? n0 + r : 0);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int groups = (K + 15) / 16;
-  for (int g = wave; g < groups; g += 4) {
-    const int kb = 16 * g + 4 * q;
-    float av[4], bv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool k_ok = kb + j < K;
-      const int k = k_ok ? kb + j : 0;
-      av[j] = a_ok && k_ok ? arow[k] : 0.f;
-      bv[j] = b_ok && k_ok ? bcol[static_cast<int64_t>(k) * ldb] : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc, 0, 0, 0);
-  }
-  partial[wave][lane] = acc;
-  __syncthreads();
-  if (wave != 0) return;
-  acc = partial[0][lane];
-#pragma unroll
-  for (int w = 1; w < 4; ++w) acc += partial[w][lane];
-  const int n = n0 + r;
-  if (n >= N) return;
-  const float bias_n = epi.bias_at(n);
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int m = m0 + 4 * q + rr;
-    if (m >= M) continue;
-    const float v = epi(acc[rr], bias_n);
-    const int64_t off = static_cast<int64_t>(m) * ldc + n;
-    if constexpr (kOut == kOutF32) static_cast<float*>(c)[off] = v;
-    else if constexpr (kOut == kOutF16) static_cast<uint16_t*>(c)[off] = asc::f32_to_f16_rne(v);
-    else static_cast<uint16_t*>(c)[off] = asc::f32_to_bf16_rne(v);
-  }
-}
-
-// ---- fp32 inputs, large outputs: LDS-tiled FMA kernel (64x64 tile, 256 threads, 4x4 per thread)
-template <int kOut>
-__global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
-                                                       void* c, int M, int N, int K, int64_t lda, int64_t ldb,
-                                                       int64_t ldc, Epilogue epi) {
-  __shared__ float as[16][64 + 1];
-  __shared__ float bs[16][64 + 1];
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-      const int kk = i & 15, mm = i >> 4;
-      as[kk][mm] = (m0 + mm < M && k0 + kk < K) ? a[(m0 + mm) * lda + k0 + kk] : 0.f;
-      const int nn = i & 63, kb = i >> 6;
-      bs[kb][nn] = (n0 + nn < N && k0 + kb < K) ? b[(k0 + kb) * ldb + n0 + nn] : 0.f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(as[kk][ty * 4 + i], bs[kk][tx * 4 + j], acc[i][j]);
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
-      if (m >= M || n >= N) continue;
-      const float v = epi(acc[i][j], epi.bias_at(n));
-      const int64_t off = static_cast<int64_t>(m) * ldc + n;
-      if constexpr (kOut == kOutF32) static_cast<float*>(c)[off] = v;
-      else if constexpr (kOut == kOutF16) static_cast<uint16_t*>(c)[off] = asc::f32_to_f16_rne(v);
-      else static_cast<uint16_t*>(c)[off] = asc::f32_to_bf16_rne(v);
-    }
-  }
-}
-
-template <bool kBf16, bool kChecked, int kOut>
-int32_t launch_mfma(const GemmArgs& p, hipStream_t stream) {
-  const int blocks = p.tiles_m * p.tiles_n;
-  hipLaunchKernelGGL((gemm_mfma_kernel<kBf16, kChecked, kOut>), dim3(blocks), dim3(kChecked ? kThreads : kFastThreads),
-                     0, stream, p);
-  return asc::check_launch("asc_matmul");
-}
-
-template <bool kBf16, int kOut>
-int32_t dispatch_checked(const GemmArgs& p, bool fast, hipStream_t stream) {
-  return fast ? launch_mfma<kBf16, false, kOut>(p, stream) : launch_mfma<kBf16, true, kOut>(p, stream);
-}
-
-template <bool kBf16>
-int32_t dispatch_out(const GemmArgs& p, int out_dtype, bool fast, hipStream_t stream) {
-  switch (out_dtype) {
-    case ASC_DT_FLOAT32: return dispatch_checked<kBf16, kOutF32>(p, fast, stream);
-    case ASC_DT_FLOAT16: return dispatch_checked<kBf16, kOutF16>(p, fast, stream);
-    case ASC_DT_BFLOAT16: return dispatch_checked<kBf16, kOutBF16>(p, fast, stream);
-    default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
-  }
-}
-
-}  // namespace
-
-namespace {
-
-int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
-                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi, asc_stream_t stream) {
+int32_t make_launch(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
+                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi, MmLaunch& L) {
+  L = MmLaunch{};
   ASC_REQUIRE(M >= 0 && N >= 0 && K >= 0, ASC_ERR_INVALID_ARG, "asc_matmul: negative shape");
   ASC_REQUIRE(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), ASC_ERR_UNSUPPORTED, "asc_matmul: shape too large");
   ASC_REQUIRE(lda >= K && ldb >= N && ldc >= N, ASC_ERR_INVALID_ARG,
@@ -359,53 +50,13 @@ int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const vo
   if (M == 0 || N == 0) return ASC_OK;
   // with K == 0 no operand element is read (C receives the epilogue of 0)
   ASC_REQUIRE(c && (K == 0 || (a && b)), ASC_ERR_INVALID_ARG, "asc_matmul: null buffer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (in_dtype == ASC_DT_FLOAT32) {
-    const float* af = static_cast<const float*>(a);
-    const float* bf = static_cast<const float*>(b);
-    const int64_t blocks16 = ((M + 15) / 16) * ((N + 15) / 16);
-    if (blocks16 <= kF32MfmaMaxBlocks) {
-      const dim3 grid16(static_cast<uint32_t>((N + 15) / 16), static_cast<uint32_t>((M + 15) / 16));
-      switch (out_dtype) {
-        case ASC_DT_FLOAT32:
-          hipLaunchKernelGGL(gemm_f32_mfma_kernel<kOutF32>, grid16, dim3(256), 0, s, af, bf, c, (int)M, (int)N,
-                             (int)K, lda, ldb, ldc, epi);
-          break;
-        case ASC_DT_FLOAT16:
-          hipLaunchKernelGGL(gemm_f32_mfma_kernel<kOutF16>, grid16, dim3(256), 0, s, af, bf, c, (int)M, (int)N,
-                             (int)K, lda, ldb, ldc, epi);
-          break;
-        case ASC_DT_BFLOAT16:
-          hipLaunchKernelGGL(gemm_f32_mfma_kernel<kOutBF16>, grid16, dim3(256), 0, s, af, bf, c, (int)M, (int)N,
-                             (int)K, lda, ldb, ldc, epi);
-          break;
-        default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
-      }
-      return asc::check_launch("asc_matmul");
-    }
-    dim3 grid(static_cast<uint32_t>((N + 63) / 64), static_cast<uint32_t>((M + 63) / 64));
-    switch (out_dtype) {
-      case ASC_DT_FLOAT32:
-        hipLaunchKernelGGL(gemm_f32_kernel<kOutF32>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
-                           ldb, ldc, epi);
-        break;
-      case ASC_DT_FLOAT16:
-        hipLaunchKernelGGL(gemm_f32_kernel<kOutF16>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
-                           ldb, ldc, epi);
-        break;
-      case ASC_DT_BFLOAT16:
-        hipLaunchKernelGGL(gemm_f32_kernel<kOutBF16>, grid, dim3(256), 0, s, af, bf, c, (int)M, (int)N, (int)K, lda,
-                           ldb, ldc, epi);
-        break;
-      default: return asc::set_error(ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
-    }
-    return asc::check_launch("asc_matmul");
-  }
-  ASC_REQUIRE(in_dtype == ASC_DT_FLOAT16 || in_dtype == ASC_DT_BFLOAT16, ASC_ERR_UNSUPPORTED,
-              "asc_matmul: unsupported input dtype %d", in_dtype);
-  GemmArgs p;
-  p.a = static_cast<const uint16_t*>(a);
-  p.b = static_cast<const uint16_t*>(b);
+  const int out = out_index(out_dtype);
+  ASC_REQUIRE(in_dtype == ASC_DT_FLOAT32 || in_dtype == ASC_DT_FLOAT16 || in_dtype == ASC_DT_BFLOAT16,
+              ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported input dtype %d", in_dtype);
+  ASC_REQUIRE(out >= 0, ASC_ERR_UNSUPPORTED, "asc_matmul: unsupported out dtype %d", out_dtype);
+  GemmArgs& p = L.p;
+  p.a = a;
+  p.b = b;
   p.c = c;
   p.M = static_cast<int>(M);
   p.N = static_cast<int>(N);
@@ -416,18 +67,44 @@ int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const vo
   p.epi = epi;
   p.tiles_m = static_cast<int>((M + BM - 1) / BM);
   p.tiles_n = static_cast<int>((N + BN - 1) / BN);
-  const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
-                       (lda % 8) == 0 && (ldb % 8) == 0;
-  // the direct-to-LDS path addresses each operand with 31-bit buffer offsets
-  const bool offsets_fit = (BM * lda + K) * 2 < (int64_t{1} << 31) && (K + 64) * ldb * 2 < (int64_t{1} << 31);
-  // the fast path's epilogue stores 8 (16-bit C) or 16 (fp32 C) bytes per lane at 4-column steps
-  const int64_t out_bytes = out_dtype == ASC_DT_FLOAT32 ? 4 : 2;
-  const bool c_rows_aligned = (reinterpret_cast<uintptr_t>(c) & 15) == 0 && (ldc * out_bytes) % 16 == 0;
-  const bool fast = aligned && c_rows_aligned && offsets_fit && (M % BM) == 0 && (N % BN) == 0 && (K % 32) == 0 &&
-                    K > 0;
-  // K == 0 takes the checked kernel: no k-tile runs and C receives cast(0).
-  return in_dtype == ASC_DT_BFLOAT16 ? dispatch_out<true>(p, out_dtype, fast, s)
-                                     : dispatch_out<false>(p, out_dtype, fast, s);
+  int kind;
+  if (in_dtype == ASC_DT_FLOAT32) {
+    // one workgroup per 16x16 output block up to 2048 x 2048 outputs, per 64x64 tile above
+    const int64_t blocks16 = ((M + 15) / 16) * ((N + 15) / 16);
+    const bool small = blocks16 <= asc::mm::kF32MfmaMaxBlocks;
+    kind = small ? 4 : 5;
+    L.blocks = small ? blocks16 : ((M + 63) / 64) * ((N + 63) / 64);
+    L.threads = 256;
+  } else {
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
+                         (lda % 8) == 0 && (ldb % 8) == 0;
+    // the direct-to-LDS path addresses each operand with 31-bit buffer offsets
+    const bool offsets_fit = (BM * lda + K) * 2 < (int64_t{1} << 31) && (K + 64) * ldb * 2 < (int64_t{1} << 31);
+    // the fast path's epilogue stores 8 (16-bit C) or 16 (fp32 C) bytes per lane at 4-column steps
+    const int64_t out_bytes = out_dtype == ASC_DT_FLOAT32 ? 4 : 2;
+    const bool c_rows_aligned = (reinterpret_cast<uintptr_t>(c) & 15) == 0 && (ldc * out_bytes) % 16 == 0;
+    // K == 0 takes the checked kernel: no k-tile runs and C receives cast(0).
+    const bool fast = aligned && c_rows_aligned && offsets_fit && (M % BM) == 0 && (N % BN) == 0 &&
+                      (K % 32) == 0 && K > 0;
+    kind = (in_dtype == ASC_DT_BFLOAT16 ? 0 : 2) + (fast ? 0 : 1);
+    L.blocks = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+    L.threads = fast ? asc::mm::kFastThreads : asc::mm::kThreads;
+  }
+  L.kernel = kKinds * out + kind;
+  // one workgroup per output tile: the grid's thread count must fit 32 bits
+  ASC_REQUIRE(L.blocks * L.threads < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED,
+              "asc_matmul: %lld output tiles exceed one launch", static_cast<long long>(L.blocks));
+  return ASC_OK;
+}
+
+int32_t run(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
+            int64_t K, int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi, asc_stream_t stream) {
+  MmLaunch L;
+  const int32_t rc = make_launch(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, epi, L);
+  if (rc != ASC_OK || L.blocks == 0) return rc;
+  hipLaunchKernelGGL(kKernels[L.kernel], dim3(static_cast<uint32_t>(L.blocks)), dim3(L.threads), 0,
+                     static_cast<hipStream_t>(stream), L.p);
+  return asc::check_launch("asc_matmul");
 }
 
 }  // namespace
@@ -435,13 +112,31 @@ int32_t matmul_impl(int32_t in_dtype, int32_t out_dtype, const void* a, const vo
 extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M,
                               int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,
                               asc_stream_t stream) {
-  return matmul_impl(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{nullptr, relu ? 1 : 0, 0.0f},
-                     stream);
+  return run(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{nullptr, relu ? 1 : 0, 0.0f}, stream);
 }
 
 extern "C" int32_t asc_matmul_bias_act(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c,
                                        const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                        int64_t ldc, int32_t act, float alpha, asc_stream_t stream) {
   ASC_REQUIRE(act >= 0 && act <= 2, ASC_ERR_INVALID_ARG, "asc_matmul_bias_act: act must be 0, 1 or 2, got %d", act);
-  return matmul_impl(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{bias, act, alpha}, stream);
+  return run(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{bias, act, alpha}, stream);
+}
+
+extern "C" int32_t asc_matmul_plan(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c,
+                                   const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                   int64_t ldc, int32_t act, float alpha, asc_launch_plan_t* plan) {
+  ASC_REQUIRE(plan, ASC_ERR_INVALID_ARG, "asc_matmul_plan: null plan");
+  *plan = asc_launch_plan_t{};
+  ASC_REQUIRE(act >= 0 && act <= 2, ASC_ERR_INVALID_ARG, "asc_matmul_plan: act must be 0, 1 or 2, got %d", act);
+  MmLaunch L;
+  const int32_t rc = make_launch(in_dtype, out_dtype, a, b, c, M, N, K, lda, ldb, ldc, Epilogue{bias, act, alpha}, L);
+  if (rc != ASC_OK || L.blocks == 0) return rc;
+  static_assert(sizeof(GemmArgs) <= sizeof(plan->args), "argument blob");
+  __builtin_snprintf(plan->kernel, sizeof(plan->kernel), "asc2_mm_%s%s", kKindNames[L.kernel % kKinds],
+                     kOutNames[L.kernel / kKinds]);
+  plan->grid = static_cast<uint32_t>(L.blocks);
+  plan->block = static_cast<uint32_t>(L.threads);
+  plan->args_size = sizeof(GemmArgs);
+  __builtin_memcpy(plan->args, &L.p, sizeof(GemmArgs));
+  return ASC_OK;
 }

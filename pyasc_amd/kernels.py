@@ -308,11 +308,11 @@ def _row_major_2d(t: torch.Tensor, name: str) -> int:
 ACT_NONE, ACT_RELU, ACT_LEAKY_RELU = 0, 1, 2
 
 
-def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False, stream: Any = None,
-           bias: Optional[torch.Tensor] = None, leaky_alpha: Optional[float] = None) -> None:
-    """c = cast(act(a @ b + bias)) with fp32 accumulation; the cast is chosen by c's dtype
-    (float32: no cast; float16/bfloat16: RNE).  ``bias``: float32 with N elements (added
-    per column), ``relu``: max(v, 0), ``leaky_alpha``: v >= 0 ? v : v * alpha (excludes relu)."""
+def _matmul_args(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool, bias: Optional[torch.Tensor],
+                 leaky_alpha: Optional[float]) -> tuple:
+    """Checks a matmul and returns the C arguments of asc_matmul_bias_act (and of
+    asc_matmul_plan) without the stream: in/out dtype codes, pointers, M, N, K, the leading
+    dimensions, the activation code and alpha."""
     for t, n in ((a, "a"), (b, "b"), (c, "c")):
         _device_tensor(t, n)
     in_code = _code(a, "a", (torch.float32, torch.float16, torch.bfloat16))
@@ -326,10 +326,6 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False
         raise ValueError(f"inner dimensions differ: a is {tuple(a.shape)}, b is {tuple(b.shape)}")
     if tuple(c.shape) != (M, N):
         raise ValueError(f"c must be {(M, N)}, got {tuple(c.shape)}")
-    if bias is None and leaky_alpha is None:
-        _native.call("asc_matmul", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, lda, ldb,
-                     ldc, int(bool(relu)), _stream(stream))
-        return
     if relu and leaky_alpha is not None:
         raise ValueError("relu and leaky_alpha are exclusive")
     bias_ptr = 0
@@ -339,14 +335,38 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False
             raise ValueError(f"bias must be float32 with {N} elements, got {bias.dtype} with {bias.numel()}")
         bias_ptr = bias.data_ptr()
     act = ACT_LEAKY_RELU if leaky_alpha is not None else (ACT_RELU if relu else ACT_NONE)
-    _native.call("asc_matmul_bias_act", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), bias_ptr, M, N,
-                 K, lda, ldb, ldc, act, float(leaky_alpha or 0.0), _stream(stream))
+    return (in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), bias_ptr, M, N, K, lda, ldb, ldc, act,
+            float(leaky_alpha or 0.0))
 
 
-def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional[torch.Tensor] = None,
-              trunc19: bool = False, stream: Any = None) -> None:
-    """int8 GEMM with exact int32 accumulation.  c int32: raw accumulators.  c float16:
-    c = fp16(fp32(acc) * scale[n]) (scale required, fp32 of length N)."""
+def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False, stream: Any = None,
+           bias: Optional[torch.Tensor] = None, leaky_alpha: Optional[float] = None) -> None:
+    """c = cast(act(a @ b + bias)) with fp32 accumulation; the cast is chosen by c's dtype
+    (float32: no cast; float16/bfloat16: RNE).  ``bias``: float32 with N elements (added
+    per column), ``relu``: max(v, 0), ``leaky_alpha``: v >= 0 ? v : v * alpha (excludes relu)."""
+    args = _matmul_args(a, b, c, relu, bias, leaky_alpha)
+    if bias is None and leaky_alpha is None:
+        in_code, out_code, ap, bp, cp, _, M, N, K, lda, ldb, ldc, _, _ = args
+        _native.call("asc_matmul", in_code, out_code, ap, bp, cp, M, N, K, lda, ldb, ldc, int(bool(relu)),
+                     _stream(stream))
+        return
+    _native.call("asc_matmul_bias_act", *args, _stream(stream))
+
+
+def matmul_plan(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False,
+                bias: Optional[torch.Tensor] = None, leaky_alpha: Optional[float] = None) -> "_native.LaunchPlan":
+    """The launch matmul(...) makes, as a kernel of the asc2_matmul code object with its
+    grid, block and argument blob (asc_matmul_plan); plan.grid == 0 when there is nothing
+    to launch.  Same checks and errors as matmul."""
+    plan = _native.LaunchPlan()
+    _native.call("asc_matmul_plan", *_matmul_args(a, b, c, relu, bias, leaky_alpha), ctypes.byref(plan))
+    return plan
+
+
+def _matmul_i8_args(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional[torch.Tensor],
+                    trunc19: bool) -> tuple:
+    """Checks an int8 matmul and returns the C arguments of asc_matmul_i8_plan: pointers
+    a, b, scale (0 for int32 output), c, then M, N, K, the dequant flag and trunc19."""
     for t, n in ((a, "a"), (b, "b"), (c, "c")):
         _contiguous(_device_tensor(t, n), n)
     _code(a, "a", (torch.int8,))
@@ -357,10 +377,8 @@ def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional
     K2, N = b.shape
     if K2 != K or tuple(c.shape) != (M, N):
         raise ValueError(f"shape mismatch: a {tuple(a.shape)}, b {tuple(b.shape)}, c {tuple(c.shape)}")
-    s = _stream(stream)
     if c.dtype == torch.int32:
-        _native.call("asc_matmul_i8_i32", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, s)
-        return
+        return (a.data_ptr(), b.data_ptr(), 0, c.data_ptr(), M, N, K, 0, 0)
     if c.dtype != torch.float16:
         raise TypeError(f"c must be int32 (accumulators) or float16 (dequantised), got {c.dtype}")
     if scale is None:
@@ -368,8 +386,27 @@ def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional
     _contiguous(_device_tensor(scale, "scale"), "scale")
     if scale.dtype != torch.float32 or scale.numel() != N:
         raise ValueError(f"scale must be float32 with {N} elements, got {scale.dtype} with {scale.numel()}")
-    _native.call("asc_matmul_i8_dequant_f16", a.data_ptr(), b.data_ptr(), scale.data_ptr(), c.data_ptr(), M, N, K,
-                 int(bool(trunc19)), s)
+    return (a.data_ptr(), b.data_ptr(), scale.data_ptr(), c.data_ptr(), M, N, K, 1, int(bool(trunc19)))
+
+
+def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional[torch.Tensor] = None,
+              trunc19: bool = False, stream: Any = None) -> None:
+    """int8 GEMM with exact int32 accumulation.  c int32: raw accumulators.  c float16:
+    c = fp16(fp32(acc) * scale[n]) (scale required, fp32 of length N)."""
+    ap, bp, sp, cp, M, N, K, dequant, t19 = _matmul_i8_args(a, b, c, scale, trunc19)
+    if not dequant:
+        _native.call("asc_matmul_i8_i32", ap, bp, cp, M, N, K, _stream(stream))
+        return
+    _native.call("asc_matmul_i8_dequant_f16", ap, bp, sp, cp, M, N, K, t19, _stream(stream))
+
+
+def matmul_i8_plan(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional[torch.Tensor] = None,
+                   trunc19: bool = False) -> "_native.LaunchPlan":
+    """The launch matmul_i8(...) makes, as a kernel of the asc2_matmul_i8 code object with
+    its grid, block and argument blob (asc_matmul_i8_plan).  Same checks as matmul_i8."""
+    plan = _native.LaunchPlan()
+    _native.call("asc_matmul_i8_plan", *_matmul_i8_args(a, b, c, scale, trunc19), ctypes.byref(plan))
+    return plan
 
 
 # --------------------------------------------------------------------------------------- attention
@@ -377,9 +414,10 @@ def matmul_i8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: Optional
 FA_HEAD_DIMS = (64, 128)
 
 
-def flash_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, sm_scale: float,
-                        causal: bool, lse: Optional[torch.Tensor] = None, stream: Any = None) -> None:
-    """o = softmax(q k^T * sm_scale + causal mask) v for bf16 [batch, heads, seq, head_dim]."""
+def _attention_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, sm_scale: float,
+                    causal: bool, lse: Optional[torch.Tensor]) -> tuple:
+    """Checks an attention call and returns the C arguments of
+    asc_flash_attention_fwd_bf16 without the stream."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
         _contiguous(_device_tensor(t, n), n)
         if t.dtype != torch.bfloat16:
@@ -397,8 +435,25 @@ def flash_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: to
         if lse.dtype != torch.float32 or lse.numel() != batch * heads * seq_len:
             raise ValueError("lse must be float32 [batch, heads, seq_len]")
         lse_ptr = lse.data_ptr()
-    _native.call("asc_flash_attention_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse_ptr,
-                 batch, heads, seq_len, head_dim, float(sm_scale), int(bool(causal)), _stream(stream))
+    return (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse_ptr, batch, heads, seq_len, head_dim,
+            float(sm_scale), int(bool(causal)))
+
+
+def flash_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, sm_scale: float,
+                        causal: bool, lse: Optional[torch.Tensor] = None, stream: Any = None) -> None:
+    """o = softmax(q k^T * sm_scale + causal mask) v for bf16 [batch, heads, seq, head_dim]."""
+    _native.call("asc_flash_attention_fwd_bf16", *_attention_args(q, k, v, o, sm_scale, causal, lse),
+                 _stream(stream))
+
+
+def flash_attention_plan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, sm_scale: float,
+                         causal: bool, lse: Optional[torch.Tensor] = None) -> "_native.LaunchPlan":
+    """The launch flash_attention_fwd(...) makes, as a kernel of the asc2_flash_attention
+    code object with its grid, block and argument blob (asc_flash_attention_plan)."""
+    plan = _native.LaunchPlan()
+    _native.call("asc_flash_attention_plan", *_attention_args(q, k, v, o, sm_scale, causal, lse),
+                 ctypes.byref(plan))
+    return plan
 
 
 # ------------------------------------------------------------------ element-wise tile operations

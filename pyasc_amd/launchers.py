@@ -326,22 +326,30 @@ def _merge_full(rects: List[Tuple[int, int, int, int]], M: int, N: int) -> List[
     return [(0, M, 0, N)] if bool(covered.all()) else rects
 
 
-@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "m_tile",
-                            "m_tiles_per_block", "n_tile", "n_tiles_per_block"),
-          "python/test/asc2/kernels/test_matmul_mnblock.py:17-36")
-def _matmul_mnblock(call: KernelCall) -> None:
+# The asc2 matmul bodies take the matmul they launch: kernels.matmul (the library's
+# asc_matmul) or, for a code-object launch, the same call replayed from asc_matmul_plan
+# through the asc2_matmul code object.  Either way the same kernels run with the same
+# arguments.
+
+def _matmul_through(functions, stream):
+    """kernels.matmul's call form, launched through the asc2_matmul code object."""
+    def mm(a, b, c, relu=False, stream=stream, bias=None, leaky_alpha=None):
+        module.launch_plan(functions, kernels.matmul_plan(a, b, c, relu=relu, bias=bias, leaky_alpha=leaky_alpha),
+                           stream)
+    return mm
+
+
+def _mnblock_body(call: KernelCall, mm) -> None:
     M, N, K = _check_shapes(call)
     a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
     _asc2_matmul_dtype(a)
     rects = mnblock_rectangles(M, N, call.grid, int(call.consts["m_tile"]), int(call.consts["m_tiles_per_block"]),
                                int(call.consts["n_tile"]), int(call.consts["n_tiles_per_block"]))
     for m0, m1, n0, n1 in _merge_full(rects, M, N):
-        kernels.matmul(a[m0:m1], b[:, n0:n1], c[m0:m1, n0:n1], stream=call.stream)
+        mm(a[m0:m1], b[:, n0:n1], c[m0:m1, n0:n1], stream=call.stream)
 
 
-@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "k_tiles"),
-          "python/test/asc2/kernels/test_matmul_tiled.py:17-31")
-def _matmul_ktiled(call: KernelCall) -> None:
+def _ktiled_body(call: KernelCall, mm) -> None:
     M, N, K = _check_shapes(call)
     k_tiles = int(call.consts["k_tiles"])
     if k_tiles <= 0:
@@ -353,22 +361,18 @@ def _matmul_ktiled(call: KernelCall) -> None:
     if k_used == 0:
         c.zero_()
         return
-    kernels.matmul(a[:, :k_used], b[:k_used], c, stream=call.stream)
+    mm(a[:, :k_used], b[:k_used], c, stream=call.stream)
 
 
-@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape"),
-          "python/test/asc2/kernels/test_matmul_fixpipe.py:17-27")
-def _matmul_fixpipe(call: KernelCall) -> None:
+def _fixpipe_body(call: KernelCall, mm) -> None:
     # c = relu(a @ b).to(c's dtype), relu and cast fused into the store
     M, N, K = _check_shapes(call)
     a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
     _asc2_matmul_dtype(a)
-    kernels.matmul(a, b, c, relu=True, stream=call.stream)
+    mm(a, b, c, relu=True, stream=call.stream)
 
 
-@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "dtype"),
-          "python/test/asc2/kernels/test_matmul_l0c_to_l1.py:17-30")
-def _matmul_chained(call: KernelCall) -> None:
+def _chained_body(call: KernelCall, mm) -> None:
     # t = (a @ b).to(dtype); c = t @ b  (needs N == K)
     M, N, K = _check_shapes(call)
     if N != K:
@@ -379,46 +383,109 @@ def _matmul_chained(call: KernelCall) -> None:
     if mid_dtype != b.dtype:
         raise TypeError(f"the intermediate dtype {mid_dtype} must match b's dtype {b.dtype} for the second matmul")
     t = torch.empty((M, N), dtype=mid_dtype, device=a.device)
-    kernels.matmul(a, b, t, stream=call.stream)
-    kernels.matmul(t, b, c, stream=call.stream)
+    mm(a, b, t, stream=call.stream)
+    mm(t, b, c, stream=call.stream)
+
+
+# The kernels of the asc2_matmul code object (csrc/co/asc2_matmul.hip).
+MATMUL_CO_FUNCTIONS = tuple(
+    f"asc2_mm_{kind}_{out}" for out in ("f32", "f16", "bf16")
+    for kind in ("mfma_bf16_fast", "mfma_bf16_checked", "mfma_f16_fast", "mfma_f16_checked", "f32_mfma", "f32_fma"))
+
+
+def _matmul_code_object(body) -> module.CodeObject:
+    return module.CodeObject("asc2_matmul", MATMUL_CO_FUNCTIONS,
+                             lambda call, functions: body(call, _matmul_through(functions, call.stream)),
+                             "pyasc_amd/csrc/co/asc2_matmul.hip")
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "m_tile",
+                            "m_tiles_per_block", "n_tile", "n_tiles_per_block"),
+          "python/test/asc2/kernels/test_matmul_mnblock.py:17-36", code_object=_matmul_code_object(_mnblock_body))
+def _matmul_mnblock(call: KernelCall) -> None:
+    _mnblock_body(call, kernels.matmul)
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "k_tiles"),
+          "python/test/asc2/kernels/test_matmul_tiled.py:17-31", code_object=_matmul_code_object(_ktiled_body))
+def _matmul_ktiled(call: KernelCall) -> None:
+    _ktiled_body(call, kernels.matmul)
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape"),
+          "python/test/asc2/kernels/test_matmul_fixpipe.py:17-27", code_object=_matmul_code_object(_fixpipe_body))
+def _matmul_fixpipe(call: KernelCall) -> None:
+    _fixpipe_body(call, kernels.matmul)
+
+
+@register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "dtype"),
+          "python/test/asc2/kernels/test_matmul_l0c_to_l1.py:17-30", code_object=_matmul_code_object(_chained_body))
+def _matmul_chained(call: KernelCall) -> None:
+    _chained_body(call, kernels.matmul)
 
 
 # ------------------------------------------------------------- int8 matmul (build-defined asc2 style)
 
+def _int8_body(call: KernelCall, mm8) -> None:
+    M, N, K = _check_shapes(call)
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    mm8(a, b, c)
+
+
+def _dequant_body(call: KernelCall, mm8, trunc19: bool) -> None:
+    M, N, K = _check_shapes(call)
+    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
+    mm8(a, b, c, scale=call.args["quant_ptr"].reshape(-1), trunc19=trunc19)
+
+
+def _trunc_scale(call: KernelCall) -> bool:
+    return bool(call.consts["trunc_scale"]) if "trunc_scale" in call.consts else False
+
+
+# The kernels of the asc2_matmul_i8 code object (csrc/co/asc2_matmul_i8.hip).
+MATMUL_I8_CO_FUNCTIONS = tuple(f"asc2_i8_{path}_{out}" for path in ("fast", "checked") for out in ("i32", "f16"))
+
+
+def _i8_code_object(launch) -> module.CodeObject:
+    def run(call: KernelCall, functions) -> None:
+        def mm8(a, b, c, scale=None, trunc19=False):
+            module.launch_plan(functions, kernels.matmul_i8_plan(a, b, c, scale=scale, trunc19=trunc19),
+                               call.stream)
+        launch(call, mm8)
+    return module.CodeObject("asc2_matmul_i8", MATMUL_I8_CO_FUNCTIONS, run, "pyasc_amd/csrc/co/asc2_matmul_i8.hip")
+
+
+def _library_i8(call: KernelCall):
+    def mm8(a, b, c, scale=None, trunc19=False):
+        kernels.matmul_i8(a, b, c, scale=scale, trunc19=trunc19, stream=call.stream)
+    return mm8
+
+
 @register("matmul_int8_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape"),
-          "python/test/generalization/adv/test_matmul_iterate_all.py:106-120 (int8 -> int32 case)")
+          "python/test/generalization/adv/test_matmul_iterate_all.py:106-120 (int8 -> int32 case)",
+          code_object=_i8_code_object(_int8_body))
 def _matmul_int8(call: KernelCall) -> None:
-    M, N, K = _check_shapes(call)
-    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
-    kernels.matmul_i8(a, b, c, stream=call.stream)
-
-
-def _dequant(call: KernelCall, trunc19: bool) -> None:
-    M, N, K = _check_shapes(call)
-    a, b, c = _as2d(call.args["a_ptr"], M, K), _as2d(call.args["b_ptr"], K, N), _as2d(call.args["c_ptr"], M, N)
-    scale = call.args["quant_ptr"].reshape(-1)
-    kernels.matmul_i8(a, b, c, scale=scale, trunc19=trunc19, stream=call.stream)
+    _int8_body(call, _library_i8(call))
 
 
 @register("matmul_dequant_kernel", ("a_ptr", "b_ptr", "c_ptr", "quant_ptr", "a_shape", "b_shape", "c_shape"),
-          "python/test/generalization/adv/test_matmul_quant.py:23-51")
+          "python/test/generalization/adv/test_matmul_quant.py:23-51",
+          code_object=_i8_code_object(lambda call, mm8: _dequant_body(call, mm8, False)))
 def _matmul_dequant(call: KernelCall) -> None:
-    _dequant(call, False)
+    _dequant_body(call, _library_i8(call), False)
 
 
 @register("matmul_dequant_kernel",
           ("a_ptr", "b_ptr", "c_ptr", "quant_ptr", "a_shape", "b_shape", "c_shape", "trunc_scale"),
-          "python/test/generalization/adv/test_matmul_quant.py:23-51,94-106")
+          "python/test/generalization/adv/test_matmul_quant.py:23-51,94-106",
+          code_object=_i8_code_object(lambda call, mm8: _dequant_body(call, mm8, _trunc_scale(call))))
 def _matmul_dequant_trunc(call: KernelCall) -> None:
-    _dequant(call, bool(call.consts["trunc_scale"]))
+    _dequant_body(call, _library_i8(call), _trunc_scale(call))
 
 
 # -------------------------------------------------------- flash attention (build-defined asc2 style)
 
-@register("flash_attention_fwd_kernel",
-          ("q_ptr", "k_ptr", "v_ptr", "o_ptr", "batch", "heads", "seq_len", "head_dim", "sm_scale", "causal",
-           "block_m", "block_n"), "none (the reference has no attention kernel)")
-def _flash_attention(call: KernelCall) -> None:
+def _attention_views(call: KernelCall):
     batch, heads, seq = int(call.get("batch")), int(call.get("heads")), int(call.get("seq_len"))
     head_dim = int(call.get("head_dim"))
     if int(call.get("block_m")) <= 0 or int(call.get("block_n")) <= 0:
@@ -431,7 +498,25 @@ def _flash_attention(call: KernelCall) -> None:
         if t.numel() < n:
             raise ValueError(f"'{name}' holds {t.numel()} elements, {shape} needed")
         views.append(t.reshape(-1)[:n].view(shape))
-    q, k, v, o = views
+    return views
+
+
+def _attention_code_object_launch(call: KernelCall, functions) -> None:
+    q, k, v, o = _attention_views(call)
+    module.launch_plan(functions, kernels.flash_attention_plan(q, k, v, o, float(call.get("sm_scale")),
+                                                               bool(call.get("causal"))), call.stream)
+
+
+ATTENTION_CODE_OBJECT = module.CodeObject("asc2_flash_attention", ("asc2_fa_fwd_d64", "asc2_fa_fwd_d128"),
+                                          _attention_code_object_launch,
+                                          "pyasc_amd/csrc/co/asc2_flash_attention.hip")
+
+
+@register("flash_attention_fwd_kernel",
+          ("q_ptr", "k_ptr", "v_ptr", "o_ptr", "batch", "heads", "seq_len", "head_dim", "sm_scale", "causal",
+           "block_m", "block_n"), "none (the reference has no attention kernel)", code_object=ATTENTION_CODE_OBJECT)
+def _flash_attention(call: KernelCall) -> None:
+    q, k, v, o = _attention_views(call)
     kernels.flash_attention_fwd(q, k, v, o, float(call.get("sm_scale")), bool(call.get("causal")),
                                 stream=call.stream)
 

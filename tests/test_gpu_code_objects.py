@@ -347,3 +347,108 @@ def test_elementwise_code_object_loaded_once(device, cache_dir):
     assert len(list(cache_dir.rglob("leaky_relu_kernel.hsaco"))) == 1
     torch.cuda.synchronize()
     assert torch.equal(out, torch.where(x >= 0, x, x * torch.tensor(0.2, dtype=torch.float32)))
+
+
+# ------------------------------------------------------------- matmul / int8 / attention code objects
+
+@pytest.fixture
+def library_path(monkeypatch):
+    """Calling it makes the registered kernels launch through the library's entry points
+    instead of their code objects for the rest of the test (calls that resolve afresh:
+    always_compile)."""
+    import dataclasses
+    from pyasc_amd import registry
+
+    def force():
+        for key, entry in list(registry._REGISTRY.items()):
+            if entry.code_object is not None:
+                monkeypatch.setitem(registry._REGISTRY, key, dataclasses.replace(entry, code_object=None))
+    return force
+
+
+def _both_paths(library_path, run):
+    """run() through the code object, then through the library; returns both results."""
+    launches = module.stats["launches"]
+    first = run()
+    torch.cuda.synchronize()
+    assert module.stats["launches"] > launches  # the first call went through a code object
+    library_path()
+    launches = module.stats["launches"]
+    second = run()
+    torch.cuda.synchronize()
+    assert module.stats["launches"] == launches  # the second did not
+    return first, second
+
+
+@pytest.mark.parametrize("form,dtype,m,k,n", [
+    ("mnblock", torch.float16, 480, 224, 1344), ("mnblock", torch.bfloat16, 512, 256, 512),
+    ("tiled", torch.float16, 64, 128, 256), ("fixpipe", torch.float32, 64, 128, 128),
+    ("fixpipe", torch.float16, 64, 128, 256), ("fixpipe", torch.bfloat16, 1024, 512, 768),
+    ("chained", torch.bfloat16, 64, 64, 64), ("chained", torch.float16, 256, 256, 256)])
+def test_matmul_code_object_matches_library(device, cache_dir, library_path, form, dtype, m, k, n):
+    import test_gpu_reference_style as ref
+    g = torch.Generator().manual_seed(m + k + n)
+    a = ((torch.rand((m, k), generator=g) - .5) * 4).to(dtype).to(device)
+    b = ((torch.rand((k, n), generator=g) - .5) * 4).to(dtype).to(device)
+
+    def run():
+        if form == "mnblock":
+            c = torch.zeros((m, n), device=device)
+            cores, m_tile, n_tile, ntpb = (30, 48, 32, 7) if m == 480 else (4, 128, 64, 2)
+            mtpb = ref._m_tiles_per_block(m, k, n, cores, m_tile, n_tile, ntpb)
+            ref._mnblock_kernel()[cores](a, b, c, a.shape, b.shape, c.shape, m_tile, mtpb, n_tile, ntpb)
+        elif form == "tiled":
+            c = torch.zeros((m, n), device=device)
+            ref._tiled_kernel()[1](a, b, c, a.shape, b.shape, c.shape, 4)
+        elif form == "fixpipe":
+            c = torch.zeros((m, n), dtype=torch.float16, device=device)
+            ref._fixpipe_kernel()[1](a, b, c, a.shape, b.shape, c.shape)
+        else:
+            c = torch.zeros((m, n), device=device)
+            ref._chained_kernel()[1](a, b, c, a.shape, b.shape, c.shape,
+                                     asc.float16 if dtype == torch.float16 else asc.bfloat16)
+        return c
+
+    co, lib = _both_paths(library_path, run)
+    assert _bits_equal(co, lib)
+    expect = a.float() @ b.float()
+    if form == "fixpipe":
+        expect = expect.relu()
+    if form != "chained":
+        torch.testing.assert_close(co.float(), expect, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 256, 512), (100, 64, 300), (256, 4096, 256)])
+def test_int8_code_object_matches_library(device, cache_dir, library_path, m, k, n):
+    import test_gpu_reference_style as ref
+    g = torch.Generator().manual_seed(m * n + k)
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).to(device)
+    b = torch.randint(-127, 128, (k, n), dtype=torch.int8, generator=g).to(device)
+    scale = (torch.rand(n, generator=g) * 0.009 + 0.001).to(device)
+
+    def run():
+        acc = torch.zeros((m, n), dtype=torch.int32, device=device)
+        out = torch.zeros((m, n), dtype=torch.float16, device=device)
+        ref.matmul_int8_kernel[16](a, b, acc, a.shape, b.shape, acc.shape, always_compile=True)
+        ref.matmul_dequant_kernel[16](a, b, out, scale, a.shape, b.shape, out.shape, True, always_compile=True)
+        return acc, out
+
+    (acc_co, out_co), (acc_lib, out_lib) = _both_paths(library_path, run)
+    assert torch.equal(acc_co, acc_lib) and _bits_equal(out_co, out_lib)
+    assert torch.equal(acc_co.cpu(), (a.cpu().double() @ b.cpu().double()).to(torch.int32))
+
+
+@pytest.mark.parametrize("B,H,S,D,causal", [(2, 4, 512, 128, False), (2, 4, 512, 128, True), (1, 3, 300, 64, True),
+                                            (1, 8, 1024, 64, False)])
+def test_attention_code_object_matches_library(device, cache_dir, library_path, B, H, S, D, causal):
+    from test_gpu_attention import flash_attention_fwd_kernel
+    g = torch.Generator().manual_seed(S + D)
+    q, k, v = ((torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16).to(device) for _ in range(3))
+
+    def run():
+        o = torch.empty_like(q)
+        flash_attention_fwd_kernel[16](q, k, v, o, B, H, S, D, 1 / D ** 0.5, causal, 128, 64, always_compile=True)
+        return o
+
+    co, lib = _both_paths(library_path, run)
+    assert _bits_equal(co, lib)

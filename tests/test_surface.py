@@ -650,7 +650,10 @@ def test_every_code_object_holds_its_kernels():
     from pyasc_amd.registry import entries
     with_co = {(name, params): e.code_object for (name, params), e in entries().items() if e.code_object}
     assert {name for name, _ in with_co} == {"vadd_kernel", "softmax_kernel", "leaky_relu_kernel", "vmuladd_kernel",
-                                             "gelu_kernel"}
+                                             "gelu_kernel", "matmul_kernel", "matmul_int8_kernel",
+                                             "matmul_dequant_kernel", "flash_attention_fwd_kernel"}
+    # every asc2 matmul form (mnblock, K-tiled, fixpipe, chained) goes through the code object
+    assert sum(name == "matmul_kernel" for name, _ in with_co) == 4
     for co in set(with_co.values()):
         data = co.path.read_bytes()
         assert data[:4] == b"\x7fELF" and b"gfx950" in data, co.name
