@@ -536,8 +536,9 @@ class ReduceRows(Workload):
 
 
 class Matmul(Workload):
-    bound, unit, kernel_hint = "mfma", "TFLOP/s", "gemm_mfma"
-    sources = ("matmul.hip", "gemm_direct.h", "gemm_core.h", "gemm_common.h", "numeric.h", "common.h")
+    bound, unit, kernel_hint = "mfma", "TFLOP/s", "mm_mfma"
+    sources = ("matmul.hip", "matmul_kernels.h", "gemm_direct.h", "gemm_core.h", "gemm_common.h", "numeric.h",
+               "common.h")
 
     def __init__(self, n: int, dtype: str, bias_leaky: bool = False):
         self.n, self.dt, self.bias_leaky = n, dtype, bias_leaky
@@ -612,7 +613,8 @@ class Matmul(Workload):
 class MatmulI8(Workload):
     bound, unit, dtype, kernel_hint = "mfma", "TOPS", "int8", "gemm_i8"
     peak = INT8_PEAK_TOPS
-    sources = ("matmul_i8.hip", "gemm_direct.h", "gemm_core.h", "gemm_common.h", "numeric.h", "common.h")
+    sources = ("matmul_i8.hip", "matmul_i8_kernels.h", "gemm_direct.h", "gemm_core.h", "gemm_common.h", "numeric.h",
+               "common.h")
 
     def __init__(self, M: int, N: int, K: int):
         self.M, self.N, self.K = M, N, K
@@ -667,7 +669,7 @@ class MatmulI8(Workload):
 class FlashAttention(Workload):
     bound, unit, dtype, kernel_hint = "mfma", "TFLOP/s", "bf16", "fa_fwd"
     peak = BF16_PEAK_TFLOPS
-    sources = ("flash_attn.hip", "numeric.h", "common.h")
+    sources = ("flash_attn.hip", "flash_attn_kernels.h", "numeric.h", "common.h")
 
     def __init__(self, B: int, H: int, S: int, D: int, causal: bool):
         self.B, self.H, self.S, self.D, self.causal = B, H, S, D, causal

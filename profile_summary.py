@@ -9,13 +9,13 @@ the commands the summaries print:
 
   traffic: DIR/<workload>_FETCH_SIZE and DIR/<workload>_WRITE_SIZE, from
       rocprofv3 --pmc FETCH_SIZE -f csv -d DIR/<workload>_FETCH_SIZE -o run -- \
-          python3 bench.py --workload <workload> --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration
+          python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --copy-calibration
   trace: DIR/<workload>_TRACE and the bench's output in DIR/<workload>_TRACE.log, from
       rocprofv3 --kernel-trace --stats -f csv -d DIR/<workload>_TRACE -o run -- \
-          python3 bench.py --workload <workload> --no-suite --no-cpu --steps 20 --warmup 3 > DIR/<workload>_TRACE.log
+          python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 20 --warmup 3 > DIR/<workload>_TRACE.log
   mfma: DIR/<workload>_MFMA, from
       rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv \
-          -d DIR/<workload>_MFMA -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --steps 5 \
+          -d DIR/<workload>_MFMA -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 \
           --warmup 1
 
 FETCH_SIZE and WRITE_SIZE are KiB per dispatch past the L2.  ``--copy-calibration``
@@ -142,9 +142,9 @@ def _write_traffic_md(table: dict) -> None:
         "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
         "```",
         "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc/${W}_FETCH_SIZE -o run -- python3 bench.py "
-        "--workload $W --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration",
+        "--workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --copy-calibration",
         "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc/${W}_WRITE_SIZE -o run -- python3 bench.py "
-        "--workload $W --no-suite --no-cpu --steps 5 --warmup 1 --copy-calibration",
+        "--workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --copy-calibration",
         "```", "",
         "`FETCH_SIZE` and `WRITE_SIZE` count the bytes that pass the L2 (misses and write-backs, including "
         "those the 256 MiB MALL then serves), so for kernels with operand reuse (the GEMMs) they bound HBM "
@@ -182,7 +182,7 @@ def mfma(folder: str) -> int:
         "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
         "```",
         "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv "
-        "-d gpurun_out/pmc/${W}_MFMA -o run -- python3 bench.py --workload $W --no-suite --no-cpu --steps 5 "
+        "-d gpurun_out/pmc/${W}_MFMA -o run -- python3 bench.py --workload $W --no-suite --no-cpu --no-vendor --steps 5 "
         "--warmup 1",
         "```", "",
         f"Device: {info}.  `SQ_VALU_MFMA_BUSY_CYCLES` is summed over all SIMDs; `GRBM_GUI_ACTIVE` over the "
@@ -241,7 +241,7 @@ def trace(folder: str) -> int:
         "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
         "```",
         "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof/${W}_TRACE -o run -- python3 bench.py "
-        "--workload $W --no-suite --no-cpu --steps 20 --warmup 3 > gpurun_out/prof/${W}_TRACE.log",
+        "--workload $W --no-suite --no-cpu --no-vendor --steps 20 --warmup 3 > gpurun_out/prof/${W}_TRACE.log",
         "```", "",
         "Durations in microseconds: average, minimum and maximum of the timed replay's dispatches "
         "(Start/End timestamps), the bench's figure for the same replay (HIP events around the graph "
