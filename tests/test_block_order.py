@@ -1,5 +1,5 @@
-"""CPU model of the attention kernel's block order (pyasc_amd/csrc/flash_attn.hip,
-block order in fa_fwd_kernel and the head-group size in launch): for many shapes,
+"""CPU model of the attention kernel's block order (pyasc_amd/csrc/flash_attn_kernels.h:
+fa_fwd_body; the head-group size: flash_attn.hip, geometry): for many shapes,
 every (batch*head, query block) pair runs exactly once, on the XCD that holds its
 head, and causal blocks of one head start heaviest first.  The GPU tests check the
 outputs of a few of these shapes; this covers the mapping over many more."""
