@@ -385,6 +385,10 @@ def _chained_body(call: KernelCall, mm) -> None:
     t = torch.empty((M, N), dtype=mid_dtype, device=a.device)
     mm(a, b, t, stream=call.stream)
     mm(t, b, c, stream=call.stream)
+    # t is freed on return; on a stream other than torch's current one the caching
+    # allocator must not hand its memory out again before these launches have run
+    if call.stream != torch.cuda.current_stream(a.device).cuda_stream:
+        t.record_stream(torch.cuda.ExternalStream(call.stream, device=a.device))
 
 
 # The kernels of the asc2_matmul code object (csrc/co/asc2_matmul.hip).

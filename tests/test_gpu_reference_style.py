@@ -270,6 +270,25 @@ def test_matmul_l0c_to_l1(device, m, k, n, torch_dtype, pyasc_dtype):
     torch.testing.assert_close(c, c_ref, atol=1e-3, rtol=1e-3)
 
 
+def test_matmul_l0c_to_l1_on_a_side_stream(device):
+    # the chained kernel's intermediate lives on the launch stream until its matmuls ran:
+    # allocations on torch's current stream meanwhile must not reuse it
+    g = torch.Generator().manual_seed(5)
+    a = ((torch.rand((256, 256), generator=g) - .5) * 4).to(torch.bfloat16).to(device)
+    b = ((torch.rand((256, 256), generator=g) - .5) * 4).to(torch.bfloat16).to(device)
+    expect = torch.zeros((256, 256), device=device)
+    matmul_chained_kernel[1](a, b, expect, a.shape, b.shape, expect.shape, asc.bfloat16)
+    torch.cuda.synchronize()
+    c = torch.zeros((256, 256), device=device)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    matmul_chained_kernel[1, s](a, b, c, a.shape, b.shape, c.shape, asc.bfloat16)
+    junk = [torch.full((256, 256), 7.0, dtype=torch.bfloat16, device=device) for _ in range(8)]
+    torch.cuda.synchronize()
+    assert torch.equal(c, expect)  # the same kernels on the same data: bit for bit
+    assert all(bool((j == 7.0).all()) for j in junk)
+
+
 def test_matmul_mnblock_device_tensors(device):
     # the same launch on device tensors: zero-copy, asynchronous on the current stream
     m, k, n, core_num, m_tile, n_tile, ntpb = 480, 224, 1344, 30, 48, 32, 7
