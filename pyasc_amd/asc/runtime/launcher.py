@@ -130,6 +130,12 @@ class Launcher:
         require_device()
         device_args, copy_back = self.prepare(runtime_args)
         stream = stream_handle(self.options.stream)
+        if copy_back and self.options.stream is not None:
+            # host buffers were copied in on torch's current stream; a launch on another
+            # stream must not start before those copies are done
+            import torch
+            if stream != int(torch.cuda.current_stream().cuda_stream):
+                torch.cuda.current_stream().synchronize()
         call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream,
                           {"options": dict(options or {})})
         if entry.code_object is None:

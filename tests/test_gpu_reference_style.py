@@ -56,6 +56,18 @@ def test_vadd_device_tensors_and_stream(device):
     assert torch.equal(out.cpu(), x.cpu() + y.cpu())
 
 
+def test_vadd_host_arrays_on_a_side_stream(device):
+    # host inputs are copied in on torch's current stream; the launch on another stream
+    # waits for them, and the outputs are copied back after it
+    rng = np.random.default_rng(seed=7)
+    x = rng.random(1 << 20, dtype=np.float32)
+    y = rng.random(1 << 20, dtype=np.float32)
+    out = np.zeros_like(x)
+    s = torch.cuda.Stream()
+    vadd_kernel[16, s](x, y, out, x.size, 128, (x.size // 128 + 15) // 16)
+    np.testing.assert_array_equal(out, x + y)
+
+
 @asc2.jit(always_compile=True, vf_fusion=True)
 def softmax_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: int, num_cols: int,
                    tile_size: asc.ConstExpr[int]):
