@@ -1,4 +1,5 @@
-"""asc_matmul_plan, asc_matmul_i8_plan and asc_flash_attention_plan without a GPU: the
+"""asc_matmul_plan, asc_matmul_i8_plan, asc_flash_attention_plan (and, over random shapes,
+asc_softmax_plan) without a GPU: the
 launch each library entry point makes, as a code-object kernel name, grid, block and the
 kernel's argument struct as a blob.  The asc2 code-object path replays these plans; the GPU
 tests compare its results with the library's bit for bit.  Here: the kernel choice, the
@@ -8,10 +9,11 @@ import math
 import struct
 
 import pytest
+from hypothesis import given, settings, strategies as st
 
 from pyasc_amd import _native
 from pyasc_amd.launchers import (ATTENTION_CODE_OBJECT, MATMUL_CO_FUNCTIONS, MATMUL_I8_CO_FUNCTIONS,
-                                 _matmul_code_object, _mnblock_body)
+                                 SOFTMAX_CO_FUNCTIONS, _matmul_code_object, _mnblock_body)
 
 A, B, C, BIAS = 0x100000, 0x200000, 0x300000, 0x400000  # 16-byte aligned stand-ins, never dereferenced
 F32, F16, BF16 = _native.DT_FLOAT32, _native.DT_FLOAT16, _native.DT_BFLOAT16
@@ -157,3 +159,85 @@ def test_code_object_images_hold_the_planned_kernels():
         data = co.path.read_bytes()
         for name in names:
             assert name.encode() + b".kd" in data, name
+
+
+# ------------------------------------------------------------------ properties over random shapes
+
+@settings(max_examples=400, deadline=None)
+@given(half=st.booleans(), fused=st.booleans(), rows=st.integers(0, 3_000_000), cols=st.integers(0, 40000),
+       size=st.integers(1, 50000), grid=st.integers(1, 128), x_off=st.sampled_from([0, 2, 4, 8, 16]))
+def test_softmax_plan_properties(half, fused, rows, cols, size, grid, x_off):
+    """Every successful plan names a code-object kernel, covers exactly the rows the
+    reference kernel writes, and fits one launch (grid x block < 2^32)."""
+    p = _native.SoftmaxPlan()
+    rc = lib().asc_softmax_plan(F16 if half else F32, int(fused), A + x_off, C, rows, cols, size, grid,
+                                ctypes.byref(p))
+    if rc != 0:
+        assert rc in (_native.ERR_UNSUPPORTED, _native.ERR_INVALID_ARG)
+        return
+    covered = min(rows, grid * size) if fused else rows
+    padded = not fused and size > cols
+    if p.grid == 0:
+        assert covered == 0 or (not padded and cols == 0 and fused)
+        return
+    assert p.kernel.decode() in SOFTMAX_CO_FUNCTIONS and p.grid * p.block < 2 ** 32
+    assert (p.rows, p.stride) == (covered, cols)
+    assert p.len == (cols if fused or padded else size)
+    if padded:
+        assert p.flag == size - cols and p.kernel.decode().startswith("asc2_softmax_padded")
+    else:
+        assert p.len <= cols
+        kind = p.kernel.decode()
+        # every row is launched: one workgroup per row, or four waves of two rows
+        if "wave" in kind:
+            assert p.grid * 8 >= covered and p.block == 256
+        elif half:
+            assert p.grid == min(covered, 65536)  # grid-stride rows
+        else:
+            assert p.grid == covered
+        if x_off % 16:
+            assert p.flag == 0  # unaligned rows never take 16-byte vectors
+
+
+@settings(max_examples=400, deadline=None)
+@given(in_dt=st.sampled_from([F32, F16, BF16]), out_dt=st.sampled_from([F32, F16, BF16]),
+       M=st.integers(0, 20000), N=st.integers(0, 20000), K=st.integers(0, 20000), pad=st.integers(0, 64),
+       a_off=st.sampled_from([0, 2, 16]))
+def test_matmul_plan_properties(in_dt, out_dt, M, N, K, pad, a_off):
+    """The direct-to-LDS kernels are only planned for shapes and buffers they can take
+    without bounds checks; every plan's blob carries the call's shape and fits one launch."""
+    rc, p = mm_plan(in_dt, out_dt, M, N, K, lda=K + pad, ldb=N, ldc=N, a=A + a_off)
+    if rc != 0:
+        assert rc == _native.ERR_UNSUPPORTED  # only a grid over 2^32 threads is refused here
+        return
+    if M == 0 or N == 0:
+        assert p.grid == 0
+        return
+    name = p.kernel.decode()
+    assert name in MATMUL_CO_FUNCTIONS and p.grid * p.block < 2 ** 32
+    a, b, c, m, n, k, lda, ldb, ldc, bias, act, alpha, tm, tn = GEMM_ARGS.unpack(p.blob())
+    assert (a, m, n, k, lda) == (A + a_off, M, N, K, K + pad)
+    if "_fast_" in name:
+        assert in_dt != F32 and M % 256 == 0 and N % 256 == 0 and K % 32 == 0 and K > 0
+        assert a_off % 16 == 0 and (K + pad) % 8 == 0
+    if in_dt == F32:
+        assert name.startswith("asc2_mm_f32_")
+    assert name.endswith({F32: "_f32", F16: "_f16", BF16: "_bf16"}[out_dt])
+
+
+@settings(max_examples=300, deadline=None)
+@given(M=st.integers(0, 30000), N=st.integers(0, 30000), K=st.integers(0, 1 << 17), dequant=st.booleans(),
+       c_off=st.sampled_from([0, 8, 16]))
+def test_int8_plan_properties(M, N, K, dequant, c_off):
+    p = _native.LaunchPlan()
+    rc = lib().asc_matmul_i8_plan(A, B, BIAS, C + c_off, M, N, K, int(dequant), 0, ctypes.byref(p))
+    assert rc == 0
+    if M == 0 or N == 0:
+        assert p.grid == 0
+        return
+    name = p.kernel.decode()
+    assert name in MATMUL_I8_CO_FUNCTIONS and p.grid * p.block < 2 ** 32
+    assert name.endswith("_f16" if dequant else "_i32")
+    if "_fast_" in name:
+        assert M % 256 == 0 and N % 256 == 0 and K % 64 == 0 and K > 0 and c_off % 16 == 0
+    assert p.grid == ((M + 255) // 256) * ((N + 255) // 256)
