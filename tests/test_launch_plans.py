@@ -1,7 +1,6 @@
 """asc_matmul_plan, asc_matmul_i8_plan, asc_flash_attention_plan (and, over random shapes,
-asc_softmax_plan) without a GPU: the
-launch each library entry point makes, as a code-object kernel name, grid, block and the
-kernel's argument struct as a blob.  The asc2 code-object path replays these plans; the GPU
+asc_softmax_plan) without a GPU: the launch each library entry point makes, as a
+code-object kernel name, grid, block and the kernel's argument struct as a blob.  The asc2 code-object path replays these plans; the GPU
 tests compare its results with the library's bit for bit.  Here: the kernel choice, the
 blob's fields, and that a plan fails exactly where its entry point does."""
 import ctypes
