@@ -120,8 +120,8 @@ def launch_blob(function: int, grid: int, block: int, blob: bytes, stream: int) 
     """One launch of a loaded kernel on ``stream`` with an argument blob laid out as the
     kernel declares its arguments."""
     from ... import _native
-    if grid <= 0 or grid >= 1 << 32:
-        raise ValueError(f"grid {grid} outside the launch range")
+    if grid <= 0 or block <= 0 or grid * block >= 1 << 32:
+        raise ValueError(f"{grid} workgroups of {block} threads: outside the launch range (under 2^32 threads)")
     buf = ctypes.create_string_buffer(blob, len(blob))
     _native.call("asc_module_launch", ctypes.c_void_p(function), grid, block, buf, len(blob), ctypes.c_void_p(stream))
     stats["launches"] += 1

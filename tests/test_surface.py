@@ -661,6 +661,14 @@ def test_every_code_object_holds_its_kernels():
             assert name.encode() + b".kd" in data, (co.name, name)
 
 
+def test_launch_refuses_grids_beyond_one_launch():
+    # checked before any HIP call: 2^24 workgroups of 256 threads is 2^32 threads
+    from pyasc_amd.asc.runtime import module
+    for grid, block in ((0, 256), (1 << 24, 256), (1 << 32, 1)):
+        with pytest.raises(ValueError, match="launch range"):
+            module.launch_blob(1, grid, block, b"", 0)
+
+
 def test_pack_args_layout():
     from pyasc_amd.asc.runtime import module
     blob = module.pack_args([("ptr", 0x1000), ("i32", 7), ("i64", -2), ("f32", 1.5), ("ptr", 0x2000)])
