@@ -117,6 +117,17 @@ def test_no_device_fails_loudly(monkeypatch):
         vadd_kernel[1](np.zeros(4, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 4, 1)
 
 
+def test_missing_library_or_code_object_fails_loudly(tmp_path):
+    # no CPU fallback: an unbuilt library or code object is an error naming the build step
+    from pyasc_amd import _native
+    from pyasc_amd.asc.runtime import module
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.load_library(tmp_path / "libasc_hip.so")
+    missing = module.CodeObject("absent", ("k",), lambda call, functions: None, "pyasc_amd/csrc/co/absent.hip")
+    with pytest.raises(RuntimeError, match="not built"):
+        module.compiled_path(missing, None, "k")
+
+
 def test_tile_ops_are_not_callable_outside_kernels():
     with pytest.raises(RuntimeError, match="only appear inside"):
         asc2.load(None, [1], offsets=[0])
