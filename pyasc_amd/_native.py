@@ -130,6 +130,16 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         return lib
 
 
+def current_stream_handle() -> int:
+    """hipStream_t of torch's current stream on the current device, read without building
+    a torch Stream object (the launch paths ask for it on every call)."""
+    import torch
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is None:
+        return int(torch.cuda.current_stream().cuda_stream)
+    return int(raw(torch.cuda.current_device()))
+
+
 def last_error() -> str:
     msg = load_library().asc_last_error()
     return msg.decode() if msg else ""

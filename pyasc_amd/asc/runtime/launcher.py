@@ -32,9 +32,9 @@ class LaunchOptions:
 
 def stream_handle(stream: Any) -> int:
     """hipStream_t of ``stream`` (None -> torch's current stream)."""
-    import torch
     if stream is None:
-        return int(torch.cuda.current_stream().cuda_stream)
+        from ... import _native
+        return _native.current_stream_handle()
     if isinstance(stream, int):
         return stream
     handle = getattr(stream, "cuda_stream", None)
@@ -134,7 +134,8 @@ class Launcher:
             # host buffers were copied in on torch's current stream; a launch on another
             # stream must not start before those copies are done
             import torch
-            if stream != int(torch.cuda.current_stream().cuda_stream):
+            from ... import _native
+            if stream != _native.current_stream_handle():
                 torch.cuda.current_stream().synchronize()
         call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream,
                           {"options": dict(options or {})})

@@ -26,7 +26,7 @@ _DTYPE_CODES = {
 
 def _stream(stream: Any) -> int:
     if stream is None:
-        return int(torch.cuda.current_stream().cuda_stream)
+        return _native.current_stream_handle()
     if isinstance(stream, int):
         return stream
     return int(stream.cuda_stream)
