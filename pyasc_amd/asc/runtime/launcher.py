@@ -21,6 +21,7 @@ from typing import Any, Dict, List, Optional, Tuple
 
 import numpy as np
 
+from ... import _native
 from ...registry import KernelCall, KernelEntry
 
 
@@ -33,7 +34,6 @@ class LaunchOptions:
 def stream_handle(stream: Any) -> int:
     """hipStream_t of ``stream`` (None -> torch's current stream)."""
     if stream is None:
-        from ... import _native
         return _native.current_stream_handle()
     if isinstance(stream, int):
         return stream
@@ -134,7 +134,6 @@ class Launcher:
             # host buffers were copied in on torch's current stream; a launch on another
             # stream must not start before those copies are done
             import torch
-            from ... import _native
             if stream != _native.current_stream_handle():
                 torch.cuda.current_stream().synchronize()
         call = KernelCall(function_name, device_args, constexprs, int(self.options.core_num), stream,
@@ -144,7 +143,6 @@ class Launcher:
         else:
             self._launch_code_object(entry, call, resolved)
         if copy_back:
-            from ... import _native
             _native.call("asc_stream_synchronize", stream)
             for host, dev in copy_back:
                 if isinstance(host, np.ndarray):
@@ -168,7 +166,6 @@ class Launcher:
             return
         try:  # caches bypassed: the module lives for this launch only
             co.launch(call, launched.functions)
-            from ... import _native
             _native.call("asc_stream_synchronize", call.stream)
         finally:
             module.unload(launched)

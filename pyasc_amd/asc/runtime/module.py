@@ -23,10 +23,13 @@ Loaded modules belong to the process and the current device; a cached
 from __future__ import annotations
 
 import ctypes
+import functools
 import struct
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Callable, Dict, Optional, Sequence, Tuple
+
+from ... import _native
 
 CODE_OBJECT_DIR = Path(__file__).resolve().parents[2] / "lib" / "co"
 
@@ -75,7 +78,6 @@ def compiled_path(co: CodeObject, file_cache_key: Optional[str], fn_name: str) -
 
 def load(co: CodeObject, path: str) -> LaunchedKernel:
     """hipModuleLoad of ``path`` and the handles of the code object's kernels."""
-    from ... import _native
     module = ctypes.c_void_p()
     _native.call("asc_module_load", path.encode(), ctypes.byref(module))
     stats["module_loads"] += 1
@@ -92,22 +94,31 @@ def load(co: CodeObject, path: str) -> LaunchedKernel:
 
 
 def unload(lk: LaunchedKernel) -> None:
-    from ... import _native
     _native.call("asc_module_unload", ctypes.c_void_p(lk.module))
     stats["module_unloads"] += 1
+
+
+_FIELD_CODES = {"ptr": "Q", "i64": "q", "i32": "i", "f32": "f"}
+
+
+@functools.lru_cache(maxsize=256)
+def _layout(kinds: Tuple[str, ...]) -> struct.Struct:
+    """struct layout of one argument list: each field at its natural alignment, the
+    padding spelled out as pad bytes."""
+    fmt, offset = "<", 0
+    for kind in kinds:
+        code = _FIELD_CODES[kind]
+        size = struct.calcsize(code)
+        pad = -offset % size
+        fmt += "x" * pad + code
+        offset += pad + size
+    return struct.Struct(fmt)
 
 
 def pack_args(fields: Sequence[Tuple[str, object]]) -> bytes:
     """Kernel arguments as one blob: each field ("ptr" / "i64" / "i32" / "f32", value)
     at its natural alignment, the way the kernel's argument list lays them out."""
-    fmt = {"ptr": "Q", "i64": "q", "i32": "i", "f32": "f"}
-    blob = bytearray()
-    for kind, value in fields:
-        code = fmt[kind]
-        size = struct.calcsize(code)
-        blob += b"\0" * (-len(blob) % size)
-        blob += struct.pack("<" + code, value)
-    return bytes(blob)
+    return _layout(tuple(kind for kind, _ in fields)).pack(*(value for _, value in fields))
 
 
 def launch(function: int, grid: int, block: int, fields: Sequence[Tuple[str, object]], stream: int) -> None:
@@ -119,7 +130,6 @@ def launch(function: int, grid: int, block: int, fields: Sequence[Tuple[str, obj
 def launch_blob(function: int, grid: int, block: int, blob: bytes, stream: int) -> None:
     """One launch of a loaded kernel on ``stream`` with an argument blob laid out as the
     kernel declares its arguments."""
-    from ... import _native
     if grid <= 0 or block <= 0 or grid * block >= 1 << 32:
         raise ValueError(f"{grid} workgroups of {block} threads: outside the launch range (under 2^32 threads)")
     buf = ctypes.create_string_buffer(blob, len(blob))
