@@ -105,6 +105,9 @@ _lib: Optional[ctypes.CDLL] = None
 def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
     """Loads libasc_hip.so once and declares every entry point's prototype."""
     global _lib
+    lib = _lib
+    if lib is not None and path is None:  # loaded: no lock on the per-launch path
+        return lib
     with _lock:
         if _lib is not None and path is None:
             return _lib
