@@ -277,6 +277,9 @@ def _reduce_all(call: KernelCall) -> None:
     out_n = 1
     for d in call.consts["output_shape"]:
         out_n *= int(d)
+    for t, name, need in ((x, "input_ptr", n), (out, "output_ptr", out_n)):
+        if t.numel() < need:
+            raise ValueError(f"'{name}' holds {t.numel()} elements, its shape needs {need}")
     kernels.reduce_f32(x.reshape(-1)[:n], out.reshape(-1)[:out_n], _reduce_name(call.consts["op"]), None,
                        call.stream)
 

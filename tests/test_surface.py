@@ -610,6 +610,26 @@ def test_launcher_refuses_noncontiguous_device_tensors():
     assert launcher_mod.require_contiguous("c_ptr", t) is t
 
 
+def test_reduce_all_refuses_shapes_beyond_the_tensors(no_native):
+    # kernel_all's input_shape / output_shape must fit the tensors; a shape larger than the
+    # tensor is an error, not a reduction over the elements that happen to exist
+    import asc2
+    from pyasc_amd import launchers
+    from pyasc_amd.registry import KernelCall
+
+    def call(x, out, in_shape, out_shape):
+        consts = {"input_shape": in_shape, "input_offsets": [0] * len(in_shape), "output_shape": out_shape,
+                  "output_offsets": [0] * len(out_shape), "op": asc2.reduce_sum}
+        return KernelCall("kernel_all", {"input_ptr": x, "output_ptr": out}, consts, 1, 0, {})
+    with pytest.raises(ValueError, match="'input_ptr' holds 60 elements, its shape needs 64"):
+        launchers._reduce_all(call(torch.zeros(60), torch.zeros(8), [8, 8], [8]))
+    with pytest.raises(ValueError, match="'output_ptr' holds 4 elements, its shape needs 8"):
+        launchers._reduce_all(call(torch.zeros(64), torch.zeros(4), [8, 8], [8]))
+    assert not no_native
+    launchers._reduce_all(call(torch.zeros(64), torch.zeros(8), [8, 8], [8]))
+    assert no_native[-1][0] == "asc_reduce_f32" and no_native[-1][4:8] == (1, 64, -1, 8)
+
+
 @pytest.mark.parametrize("dtype,bad", [(torch.int32, 32), (torch.int32, -1), (torch.int16, 16)])
 def test_shift_amount_range(no_native, dtype, bad):
     from pyasc_amd import kernels
