@@ -85,7 +85,8 @@ int32_t asc_stream_synchronize(asc_stream_t stream);
  *                       `grid` workgroups of `block` threads on `stream`, the
  *                       kernel's arguments as one blob of `args_size` bytes laid
  *                       out as the kernel declares them (natural alignment,
- *                       8-byte pointers). */
+ *                       8-byte pointers).  block <= 1024 and grid * block
+ *                       < 2^32 (else ASC_ERR_INVALID_ARG / ASC_ERR_UNSUPPORTED). */
 int32_t asc_module_load(const char* path, void** module);
 int32_t asc_module_unload(void* module);
 int32_t asc_module_get_function(void* module, const char* name, void** function);

@@ -101,6 +101,9 @@ int32_t asc_module_launch(void* function, uint32_t grid, uint32_t block, const v
   ASC_REQUIRE(function, ASC_ERR_INVALID_ARG, "asc_module_launch: null function");
   ASC_REQUIRE(grid > 0 && block > 0 && block <= 1024, ASC_ERR_INVALID_ARG,
               "asc_module_launch: grid %u / block %u out of range", grid, block);
+  // one dispatch covers fewer than 2^32 threads
+  ASC_REQUIRE(static_cast<uint64_t>(grid) * block < (uint64_t{1} << 32), ASC_ERR_UNSUPPORTED,
+              "asc_module_launch: %u workgroups of %u threads exceed one launch", grid, block);
   ASC_REQUIRE(args_size == 0 || args, ASC_ERR_INVALID_ARG, "asc_module_launch: null argument blob");
   size_t size = static_cast<size_t>(args_size);
   void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,

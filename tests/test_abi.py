@@ -60,6 +60,7 @@ def test_version_string():
     ("asc_module_launch", (1, 0, 64, None, 0, None), _native.ERR_INVALID_ARG),  # empty grid
     ("asc_module_launch", (1, 1, 2048, None, 0, None), _native.ERR_INVALID_ARG),  # block too large
     ("asc_module_launch", (1, 1, 64, None, 8, None), _native.ERR_INVALID_ARG),  # null argument blob
+    ("asc_module_launch", (1, 1 << 22, 1024, None, 0, None), _native.ERR_UNSUPPORTED),  # 2^32 threads
     ("asc_copy_bytes", (16, 32, -16, None), _native.ERR_INVALID_ARG),
     ("asc_copy_bytes", (0, 32, 16, None), _native.ERR_INVALID_ARG),  # null src
     ("asc_copy_bytes", (16, 32, 24, None), _native.ERR_ALIGNMENT),  # size not a multiple of 16
