@@ -120,8 +120,11 @@ __global__ void __launch_bounds__(1024) reduce_all_kernel(ReduceArgs p) {
 template <int kOp>
 int32_t launch_reduce(const ReduceArgs& p, int dim, hipStream_t s) {
   if (dim == 1) {
-    hipLaunchKernelGGL(reduce_rows_kernel<kOp>, dim3(static_cast<uint32_t>(asc::ceil_div(p.rows, 4))), dim3(256), 0,
-                       s, p);
+    // four rows per 256-thread workgroup; one dispatch covers fewer than 2^32 threads
+    const int64_t blocks = asc::ceil_div(p.rows, 4);
+    ASC_REQUIRE(blocks * 256 < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED, "asc_reduce_f32: %lld rows exceed one launch",
+                static_cast<long long>(p.rows));
+    hipLaunchKernelGGL(reduce_rows_kernel<kOp>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, p);
   } else if (dim == 0) {
     hipLaunchKernelGGL(reduce_cols_kernel<kOp>, dim3(static_cast<uint32_t>(asc::ceil_div(p.cols, 256))), dim3(256),
                        0, s, p);
@@ -288,8 +291,12 @@ __global__ void __launch_bounds__(256) rms_norm_long_kernel(RmsArgs p) {
 
 template <class E>
 int32_t launch_rms(const RmsArgs& p, hipStream_t s) {
-  const dim3 grid(static_cast<uint32_t>(p.rows));
   constexpr int kP = E::kPerVec;
+  // one workgroup per row; one dispatch covers fewer than 2^32 threads
+  const int64_t threads = p.len <= 1024 * kP ? 128 : 256;
+  ASC_REQUIRE(p.rows * threads < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED, "asc_rms_norm: %lld rows exceed one launch",
+              static_cast<long long>(p.rows));
+  const dim3 grid(static_cast<uint32_t>(p.rows));
   // 128 threads per row while 8 vectors per thread suffice (two waves per row
   // keep more rows in flight), 256 threads above, two passes beyond 2048 vectors
   if (p.len <= 128 * kP) {

@@ -61,6 +61,8 @@ def test_version_string():
     ("asc_module_launch", (1, 1, 2048, None, 0, None), _native.ERR_INVALID_ARG),  # block too large
     ("asc_module_launch", (1, 1, 64, None, 8, None), _native.ERR_INVALID_ARG),  # null argument blob
     ("asc_module_launch", (1, 1 << 22, 1024, None, 0, None), _native.ERR_UNSUPPORTED),  # 2^32 threads
+    ("asc_reduce_f32", (0, 1, 1, 1 << 26, 1, 1, 1 << 26, None), _native.ERR_UNSUPPORTED),  # 2^32 threads
+    ("asc_rms_norm", (0, 1, 1, 1, 1 << 25, 4, 4, 1e-6, None), _native.ERR_UNSUPPORTED),  # 2^25 rows x 128
     ("asc_copy_bytes", (16, 32, -16, None), _native.ERR_INVALID_ARG),
     ("asc_copy_bytes", (0, 32, 16, None), _native.ERR_INVALID_ARG),  # null src
     ("asc_copy_bytes", (16, 32, 24, None), _native.ERR_ALIGNMENT),  # size not a multiple of 16
