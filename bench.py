@@ -750,7 +750,80 @@ SUITE = ["asc2_vadd_8192", "softmax_16384x1024", "copy_128MiB", "vadd_268435456"
          "gelu_erf_16384x1024", "rms_norm_4096x4096", "reduce_sum_dim1_16384x4096"]
 
 
-def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True) -> dict:
+class PowerSampler:
+    """Samples the board's socket power and the graphics clock with ``amd-smi metric -p -c``
+    in a background thread (each call takes about 0.4 s) from ``start()`` to ``stop()``.
+    ``summary()`` drops the first ``skip`` samples (the clock ramps up as the launches
+    begin) and reports the median, minimum and maximum of the rest; the clock is the mean
+    over the XCDs' GFX_n domains of one sample."""
+
+    def __init__(self, skip: int = 2):
+        import threading
+        self.skip = skip
+        self.samples = []  # (seconds since start, watts, MHz)
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._t0 = 0.0
+
+    @staticmethod
+    def parse(text: str):
+        watts, mhz, in_gfx = None, [], False
+        for line in text.splitlines():
+            s = line.strip()
+            if s.startswith("SOCKET_POWER:"):
+                try:
+                    watts = float(s.split()[1])
+                except (IndexError, ValueError):
+                    pass
+            elif s.startswith("GFX_") and s.endswith(":"):
+                in_gfx = True
+            elif s.endswith(":") and not s.startswith("GFX_"):
+                in_gfx = False
+            elif in_gfx and s.startswith("CLK:"):
+                try:
+                    mhz.append(float(s.split()[1]))
+                except (IndexError, ValueError):
+                    pass
+        return watts, (sum(mhz) / len(mhz) if mhz else None)
+
+    def _run(self):
+        import subprocess
+        while not self._stop.is_set():
+            try:
+                out = subprocess.run(["amd-smi", "metric", "-p", "-c", "-g", "0"], capture_output=True, text=True,
+                                     timeout=10).stdout
+            except (OSError, subprocess.SubprocessError):
+                return
+            watts, mhz = self.parse(out)
+            if watts is not None and mhz is not None:
+                self.samples.append((time.perf_counter() - self._t0, watts, mhz))
+            self._stop.wait(0.2)
+
+    def start(self):
+        self._t0 = time.perf_counter()
+        self._thread.start()
+
+    def stop(self):
+        self._stop.set()
+        self._thread.join(timeout=15)
+
+    def summary(self) -> dict:
+        kept = self.samples[self.skip:]
+        if not kept:
+            return {"samples": 0, "note": "amd-smi gave no reading (run a longer --warmup)"}
+
+        def med(v):
+            v = sorted(v)
+            return v[len(v) // 2]
+        w = [s[1] for s in kept]
+        c = [s[2] for s in kept]
+        return {"samples": len(kept), "seconds": round(kept[-1][0] - kept[0][0], 2),
+                "socket_w_median": med(w), "socket_w_min": min(w), "socket_w_max": max(w),
+                "gfx_mhz_median": round(med(c)), "gfx_mhz_min": round(min(c)), "gfx_mhz_max": round(max(c)),
+                "source": "amd-smi metric -p -c -g 0 (SOCKET_POWER; mean of the GFX_n CLK readings)"}
+
+
+def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True, sampler: PowerSampler = None) -> dict:
     """Times exactly ``steps`` launches on the launch stream with HIP events.
 
     Default: the ``steps`` launches are captured once into a HIP graph and the
@@ -761,6 +834,8 @@ def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True) -> di
     2 us of event overhead per launch)."""
     import torch
     w.setup(dev)
+    if sampler is not None:
+        sampler.start()
     for i in range(warmup):
         w.launch(i)
     torch.cuda.synchronize()
@@ -795,6 +870,8 @@ def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True) -> di
         torch.cuda.synchronize()
         ms = ev[0][0].elapsed_time(ev[-1][1]) / steps
         kernel_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    if sampler is not None:
+        sampler.stop()
     value = w.value(kernel_ms / 1e3)
     return {"workload": w.name, "ms_per_step": ms, "kernel_ms": kernel_ms, "value": value, "unit": w.unit,
             "rate": w.rate(kernel_ms / 1e3), "bound": w.bound, "config": w.config(),
@@ -981,6 +1058,9 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="time with per-launch event pairs, no HIP graph")
     ap.add_argument("--no-vendor", action="store_true", help="skip the ROCm library comparisons")
     ap.add_argument("--cpu-all", action="store_true", help=argparse.SUPPRESS)  # the default now
+    ap.add_argument("--power", action="store_true",
+                    help="sample socket power and graphics clock with amd-smi from the start of the headline's "
+                         "warm-up to the end of its timed replay (give a warm-up of several seconds)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -999,7 +1079,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
 
     head = WORKLOADS[args.workload]()
-    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph)
+    sampler = PowerSampler() if args.power else None
+    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph, sampler=sampler)
     head_vendor = None if args.no_vendor else vendor(head, args.steps, res)
     print(f"bench: {head.name} {res['value']:.2f} {head.unit}", file=sys.stderr, flush=True)
     suite = {}
@@ -1053,6 +1134,8 @@ def main() -> int:
         "launch_latency": latency,
         "reference_published": published,
     }
+    if sampler is not None:
+        line["power"] = sampler.summary()
     print(json.dumps(line), flush=True)
     return 0
 
