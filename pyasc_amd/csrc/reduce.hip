@@ -14,8 +14,8 @@
 // asc_rms_norm covers asc2.rms_norm (python/asc/language/tile/unary_ops.py:225-237,
 // AscendC RmsNorm): y = x * rsqrt(mean(x^2) + eps) * gamma along the last dim,
 // fp32 or fp16 rows computed in fp32 (a block per row, the row held in
-// registers up to 8192 fp32 / 16384 fp16 columns; 128 threads per row up to
-// 4096 fp32 / 8192 fp16 columns).
+// registers up to 8192 fp32 / 16384 fp16 columns, two 16-byte vectors per lane
+// from 1024 fp32 / 2048 fp16 columns up).
 #include <math.h>
 
 #include "common.h"
@@ -292,23 +292,28 @@ __global__ void __launch_bounds__(256) rms_norm_long_kernel(RmsArgs p) {
 template <class E>
 int32_t launch_rms(const RmsArgs& p, hipStream_t s) {
   constexpr int kP = E::kPerVec;
-  // one workgroup per row; one dispatch covers fewer than 2^32 threads
-  const int64_t threads = p.len <= 1024 * kP ? 128 : 256;
+  // One workgroup per row, two 16-byte vectors per lane above 256 vectors per row:
+  // more, shorter waves per row finish each row's loads, reduction and stores sooner
+  // (4096 fp32 columns, 64 MiB in and out, same box: 5480-5530 GB/s with 128 threads
+  // x 8 vectors, 5730-5740 with 512 x 2, 5040 with 1024 x 1; 2048 columns: 5500-5550
+  // with 128 x 4, 5650-5680 with 256 x 2; 8192: 5370 with 256 x 8, 5510 with 512 x 4,
+  // 5560-5570 with 1024 x 2).  Two passes over longer rows.
+  const int64_t vecs = (static_cast<int64_t>(p.len) + kP - 1) / kP;
+  const int64_t threads = vecs <= 256 ? 128 : vecs <= 512 ? 256 : vecs <= 1024 ? 512 : vecs <= 2048 ? 1024 : 256;
+  // one dispatch covers fewer than 2^32 threads
   ASC_REQUIRE(p.rows * threads < (int64_t{1} << 32), ASC_ERR_UNSUPPORTED, "asc_rms_norm: %lld rows exceed one launch",
               static_cast<long long>(p.rows));
   const dim3 grid(static_cast<uint32_t>(p.rows));
-  // 128 threads per row while 8 vectors per thread suffice (two waves per row
-  // keep more rows in flight), 256 threads above, two passes beyond 2048 vectors
-  if (p.len <= 128 * kP) {
+  if (vecs <= 128) {
     hipLaunchKernelGGL((rms_norm_kernel<E, 1, 128>), grid, dim3(128), 0, s, p);
-  } else if (p.len <= 256 * kP) {
+  } else if (vecs <= 256) {
     hipLaunchKernelGGL((rms_norm_kernel<E, 2, 128>), grid, dim3(128), 0, s, p);
-  } else if (p.len <= 512 * kP) {
-    hipLaunchKernelGGL((rms_norm_kernel<E, 4, 128>), grid, dim3(128), 0, s, p);
-  } else if (p.len <= 1024 * kP) {
-    hipLaunchKernelGGL((rms_norm_kernel<E, 8, 128>), grid, dim3(128), 0, s, p);
-  } else if (p.len <= 2048 * kP) {
-    hipLaunchKernelGGL((rms_norm_kernel<E, 8, 256>), grid, dim3(256), 0, s, p);
+  } else if (vecs <= 512) {
+    hipLaunchKernelGGL((rms_norm_kernel<E, 2, 256>), grid, dim3(256), 0, s, p);
+  } else if (vecs <= 1024) {
+    hipLaunchKernelGGL((rms_norm_kernel<E, 2, 512>), grid, dim3(512), 0, s, p);
+  } else if (vecs <= 2048) {
+    hipLaunchKernelGGL((rms_norm_kernel<E, 2, 1024>), grid, dim3(1024), 0, s, p);
   } else {
     hipLaunchKernelGGL(rms_norm_long_kernel<E>, grid, dim3(256), 0, s, p);
   }

@@ -16,7 +16,7 @@ enum Kernel : int32_t {
   kWave2x2,
   kBlock2x128,
   kBlock2x256,
-  kBlock4x256,
+  kBlock2x512,
   kBlock8x256,
   kLong,
   kF16,
@@ -30,12 +30,12 @@ using KernelFn = void (*)(const void*, void*, int64_t, int64_t, int32_t, int32_t
 // The library's kernels and the code object's names for the same bodies
 // (co/asc2_softmax.hip), in Kernel order.
 const KernelFn kKernels[kNumKernels] = {softmax_wave_1x2,    softmax_wave_2x2,    softmax_block_2x128,
-                                        softmax_block_2x256, softmax_block_4x256, softmax_block_8x256,
+                                        softmax_block_2x256, softmax_block_2x512, softmax_block_8x256,
                                         softmax_long,        softmax_f16,         softmax_padded_f32,
                                         softmax_padded_f16};
 const char* const kCodeObjectNames[kNumKernels] = {
     "asc2_softmax_wave_1x2",    "asc2_softmax_wave_2x2",    "asc2_softmax_block_2x128", "asc2_softmax_block_2x256",
-    "asc2_softmax_block_4x256", "asc2_softmax_block_8x256", "asc2_softmax_long",        "asc2_softmax_f16",
+    "asc2_softmax_block_2x512", "asc2_softmax_block_8x256", "asc2_softmax_long",        "asc2_softmax_f16",
     "asc2_softmax_padded_f32",  "asc2_softmax_padded_f16"};
 
 struct Plan {
@@ -49,13 +49,16 @@ struct Plan {
 };
 
 // Row-resident fp32 body for rows of `len` columns.  Above 512 columns a row takes
-// several waves with 2-4 vectors per lane: more, shorter waves than one wave per
-// row, and each wave's loads, cross-wave reductions and stores finish sooner
-// (fp32 rows, 64 MiB in and out, same box: 1024 columns 5500-5560 GB/s with one
-// wave per two rows, 5950 with block_2x128; 2048: 5680 with two waves per row,
-// 5870 with four; 4096: 5560-5590 with two waves per row, 5740-5780 with four,
-// beside a 5840-5850 GB/s copy).  Up to 512 columns a wave takes two rows
-// (measured faster at 1024 columns than one).
+// several waves with 2 vectors per lane (8 at 8192 columns): more, shorter waves than
+// one wave per row, and each wave's loads, cross-wave reductions and stores finish
+// sooner (fp32 rows, 64 MiB in and out, same box: 1024 columns 5500-5560 GB/s with
+// one wave per two rows, 5950 with block_2x128, 5500 with block_1x256; 2048: 5680 with
+// two waves per row, 5870-5970 with four, 5210-5360 with eight; 4096: 5560-5590 with
+// two waves per row, 5690-5740 with four (4 vectors), 5890-5900 with eight
+// (block_2x512), 5200-5260 with sixteen; 8192: 5650-5670 with four waves of 8
+// vectors, 5580-5610 with eight, 5480-5510 with sixteen; a plain copy of the same
+// bytes 5840-5850).  Up to 512 columns a wave takes two rows (measured faster at
+// 1024 columns than one).
 void plan_f32_rows(Plan& p) {
   const int64_t L = p.len;
   p.block = 256;
@@ -71,7 +74,8 @@ void plan_f32_rows(Plan& p) {
   } else if (L <= 2048) {
     p.kernel = kBlock2x256;
   } else if (L <= 4096) {
-    p.kernel = kBlock4x256;
+    p.kernel = kBlock2x512;
+    p.block = 512;
   } else if (L <= 8192) {
     p.kernel = kBlock8x256;
   } else {

@@ -393,7 +393,7 @@ __device__ __forceinline__ void padded_body(const void* x, void* out, int64_t ro
   ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##wave_2x2, 256, (asc::softmax::wave_body<2, 2>))                              \
   ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##block_2x128, 128, (asc::softmax::block_body<2, 128>))                        \
   ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##block_2x256, 256, (asc::softmax::block_body<2, 256>))                        \
-  ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##block_4x256, 256, (asc::softmax::block_body<4, 256>))                        \
+  ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##block_2x512, 512, (asc::softmax::block_body<2, 512>))                        \
   ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##block_8x256, 256, (asc::softmax::block_body<8, 256>))                        \
   ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##long, 256, asc::softmax::long_body)                                          \
   ASC_SOFTMAX_KERNEL(LINKAGE, PREFIX##f16, 256, asc::softmax::f16_body)                                            \

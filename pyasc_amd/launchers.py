@@ -190,7 +190,7 @@ def _gelu(call: KernelCall) -> None:
 
 # The kernels of the asc2_softmax code object (csrc/co/asc2_softmax.hip), one per row body.
 SOFTMAX_CO_FUNCTIONS = tuple(f"asc2_softmax_{body}" for body in (
-    "wave_1x2", "wave_2x2", "block_2x128", "block_2x256", "block_4x256", "block_8x256", "long", "f16", "padded_f32",
+    "wave_1x2", "wave_2x2", "block_2x128", "block_2x256", "block_2x512", "block_8x256", "long", "f16", "padded_f32",
     "padded_f16"))
 
 

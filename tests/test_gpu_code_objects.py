@@ -167,7 +167,7 @@ def _softmax_inputs(dtype, rows, cols, seed, device, offset=0):
 
 
 @pytest.mark.parametrize("dtype,rows,cols,tile,offset", [
-    # one case per planned kernel: wave_1x2, wave_2x2, block_2x128 / 2x256 / 4x256 / 8x256, long
+    # one case per planned kernel: wave_1x2, wave_2x2, block_2x128 / 2x256 / 2x512 / 8x256, long
     (torch.float32, 37, 100, 100, 0), (torch.float32, 64, 300, 300, 0), (torch.float32, 33, 1000, 1000, 0),
     (torch.float32, 16, 2000, 2000, 0), (torch.float32, 9, 4000, 4000, 0), (torch.float32, 5, 8000, 8000, 0),
     (torch.float32, 3, 9000, 9000, 0),

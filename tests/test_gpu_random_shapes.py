@@ -134,7 +134,7 @@ def test_softmax_draws_reach_every_row_body(device):
     for rows, cols, pad in SOFTMAX_DRAWS:
         x = torch.empty(rows, cols, device=device)
         seen.add(kernels.softmax_plan(x, x, rows, cols, cols + pad, 16, False).kernel.decode())
-    body = {"wave_1x2", "wave_2x2", "block_2x128", "block_2x256", "block_4x256", "block_8x256", "long",
+    body = {"wave_1x2", "wave_2x2", "block_2x128", "block_2x256", "block_2x512", "block_8x256", "long",
             "padded_f32"}
     assert {s.split("asc2_softmax_")[-1] for s in seen} == body
 

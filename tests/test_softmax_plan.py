@@ -22,7 +22,7 @@ def plan(dtype, fused, x, out, rows, cols, size, grid):
 @pytest.mark.parametrize("length,kernel,block", [
     (1, "wave_1x2", 256), (256, "wave_1x2", 256), (257, "wave_2x2", 256), (512, "wave_2x2", 256),
     (513, "block_2x128", 128), (1024, "block_2x128", 128), (1025, "block_2x256", 256), (2048, "block_2x256", 256),
-    (2049, "block_4x256", 256), (4096, "block_4x256", 256), (4097, "block_8x256", 256), (8192, "block_8x256", 256),
+    (2049, "block_2x512", 512), (4096, "block_2x512", 512), (4097, "block_8x256", 256), (8192, "block_8x256", 256),
     (8193, "long", 256), (100000, "long", 256)])
 def test_f32_kernel_per_row_length(length, kernel, block):
     rows = 1001
