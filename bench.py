@@ -1,6 +1,6 @@
 """Benchmark of the asc2 hot-path kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-suite] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-suite] [--no-cpu] [--no-power]
 
 A "step" is one launch of the headline kernel over one batch of synthetic,
 device-resident input.  The headline workload is BASELINE.json's configs[1],
@@ -23,6 +23,11 @@ reference test's torch CPU golden expression (oracle/cpu_golden.py), timed on
 the host cores on the full workload (repeated to at least 2 s of CPU work, 10 s
 for the headline); each names the host (thread count, os.cpu_count(), CPU
 model) it ran on.
+
+With the suite, a power phase follows: the headline and each MFMA workload launch for
+about 3 s while amd-smi samples socket power and graphics clock ("power" in the line;
+for the MFMA workloads also the dense peak at the sampled clock and the fraction of it
+reached).
 
 `roofline.traffic` comes from profiles/traffic.json (rocprofv3 FETCH_SIZE /
 WRITE_SIZE passes summarised by profile_summary.py).  Each entry is stamped with
@@ -915,6 +920,41 @@ def roofline(w: Workload, res: dict) -> dict:
             "frac": round(res["value"] / w.peak, 4), "traffic": traffic_for(w)}
 
 
+POWER_WORKLOADS = ["softmax_4096x4096", "matmul_bf16_8192", "matmul_i8_4096x11008x4096", "fa_fwd_noncausal",
+                   "fa_fwd_causal"]
+POWER_SECONDS = 3.0
+
+
+def power_phase(dev, kernel_ms: dict) -> dict:
+    """Socket power and graphics clock while each of POWER_WORKLOADS that ran (``kernel_ms``:
+    workload key -> ms per launch) launches for about POWER_SECONDS (its warm-up), sampled
+    with PowerSampler.  For an MFMA workload the entry also gives the dense peak at the
+    sampled clock (peak x MHz / 2400) and the fraction of it this run reached: the MFMA
+    kernels hold the board at its power limit, which sets the clock."""
+    import torch
+    out = {}
+    for key in POWER_WORKLOADS:
+        ms = kernel_ms.get(key)
+        if not ms:
+            continue
+        w = WORKLOADS[key]()
+        sampler = PowerSampler()
+        warmup = max(10, min(400000, int(POWER_SECONDS / (ms * 1e-3))))
+        r = measure(w, 20, warmup, dev, sampler=sampler)
+        entry = {"value": round(r["value"], 3), "unit": w.unit, "warmup_launches": warmup, **sampler.summary()}
+        mhz = entry.get("gfx_mhz_median")
+        if mhz and w.bound == "mfma":
+            peak = w.peak * mhz / 2400.0
+            entry["dense_peak_at_clock"] = round(peak, 1)
+            entry["frac_at_clock"] = round(r["value"] / peak, 4)
+        out[w.name] = entry
+        print(f"bench: power {w.name} {r['value']:.1f} {w.unit}, {entry.get('socket_w_median')} W, "
+              f"{mhz} MHz", file=sys.stderr, flush=True)
+        del w
+        torch.cuda.empty_cache()
+    return out
+
+
 def launch_latency(dev, n: int = 2000) -> dict:
     """Host time per launch of the reference-size vadd (8192 fp32, grid 16, tile 128,
     tpb 4; test_vadd.py:31-38) on device tensors, through the asc2 surface with the
@@ -1058,9 +1098,9 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="time with per-launch event pairs, no HIP graph")
     ap.add_argument("--no-vendor", action="store_true", help="skip the ROCm library comparisons")
     ap.add_argument("--cpu-all", action="store_true", help=argparse.SUPPRESS)  # the default now
-    ap.add_argument("--power", action="store_true",
-                    help="sample socket power and graphics clock with amd-smi from the start of the headline's "
-                         "warm-up to the end of its timed replay (give a warm-up of several seconds)")
+    ap.add_argument("--no-power", action="store_true",
+                    help="skip the power phase (with the suite: socket power and graphics clock sampled with "
+                         "amd-smi during about 3 s of launches of the headline and of each MFMA workload)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -1079,8 +1119,7 @@ def main() -> int:
     dev = torch.device("cuda", 0)
 
     head = WORKLOADS[args.workload]()
-    sampler = PowerSampler() if args.power else None
-    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph, sampler=sampler)
+    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph)
     head_vendor = None if args.no_vendor else vendor(head, args.steps, res)
     print(f"bench: {head.name} {res['value']:.2f} {head.unit}", file=sys.stderr, flush=True)
     suite = {}
@@ -1134,8 +1173,10 @@ def main() -> int:
         "launch_latency": latency,
         "reference_published": published,
     }
-    if sampler is not None:
-        line["power"] = sampler.summary()
+    if not args.no_power and not args.no_suite:
+        timings = {args.workload: res["kernel_ms"]}
+        timings.update({k: r["kernel_ms"] for k, r in suite.items()})
+        line["power"] = power_phase(dev, timings)
     print(json.dumps(line), flush=True)
     return 0
 
