@@ -291,6 +291,21 @@ int32_t asc_matmul_bias_act(int32_t in_dtype, int32_t out_dtype, const void* a,
                             int64_t M, int64_t N, int64_t K, int64_t lda,
                             int64_t ldb, int64_t ldc, int32_t act, float alpha,
                             asc_stream_t stream);
+/* ---- chained matmul ------------------------------------------------------------
+ * asc2 matmul_kernel(a_ptr, b_ptr, c_ptr, a_shape, b_shape, c_shape, dtype)
+ *   python/test/asc2/kernels/test_matmul_l0c_to_l1.py:17-30: c = a @ b in L0C,
+ *   cast to dtype and moved L0C -> L1 -> L0A, then multiplied by b again.
+ * t = cast(A . B) to in_dtype (RNE), C = cast(t . B) to out_dtype, both with
+ * fp32 accumulation; A [M, K], B [K, N] with N == K, C [M, N], all row-major
+ * and contiguous.  in_dtype: ASC_DT_FLOAT16 or ASC_DT_BFLOAT16 (A, B and the
+ * intermediate alike); out_dtype as in asc_matmul.  The intermediate t
+ * (M * N elements of in_dtype, row-major) is written to `workspace`, which must
+ * hold workspace_bytes >= M * N * 2 bytes; the two matmuls run in order on
+ * `stream`, so the workspace may be reused once they have run. */
+int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a,
+                           const void* b, void* c, int64_t M, int64_t N,
+                           int64_t K, void* workspace, int64_t workspace_bytes,
+                           asc_stream_t stream);
 /* The launch asc_matmul_bias_act makes with these arguments (asc_matmul(...,
  * relu) is act = relu, bias NULL), as a kernel of the code object
  * pyasc_amd/lib/co/asc2_matmul.hsaco (asc_launch_plan_t; the blob is the

@@ -107,7 +107,34 @@ int32_t run(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, v
   return asc::check_launch("asc_matmul");
 }
 
+// t = cast(a . b) to in_dtype into `t` (t_bytes long), then c = cast(t . b) to out_dtype.
+int32_t chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
+                int64_t K, void* t, int64_t t_bytes, asc_stream_t stream, const char* who) {
+  ASC_REQUIRE(M >= 0 && N >= 0 && K >= 0, ASC_ERR_INVALID_ARG, "%s: negative shape", who);
+  ASC_REQUIRE(in_dtype == ASC_DT_FLOAT16 || in_dtype == ASC_DT_BFLOAT16, ASC_ERR_UNSUPPORTED,
+              "%s: input dtype %d is not float16 or bfloat16", who, in_dtype);
+  ASC_REQUIRE(N == K, ASC_ERR_INVALID_ARG,
+              "%s: the chained matmul multiplies (a @ b) by b again and needs N == K, got N=%lld, K=%lld", who,
+              (long long)N, (long long)K);
+  ASC_REQUIRE(M < (1 << 30) && N < (1 << 30), ASC_ERR_UNSUPPORTED, "%s: shape too large", who);
+  if (M == 0 || N == 0) return ASC_OK;
+  const int64_t need = M * N * 2;
+  ASC_REQUIRE(t_bytes >= need, ASC_ERR_INVALID_ARG, "%s: the intermediate needs %lld bytes, the workspace holds %lld",
+              who, (long long)need, (long long)t_bytes);
+  ASC_REQUIRE(t, ASC_ERR_INVALID_ARG, "%s: null workspace", who);
+  const Epilogue none{nullptr, 0, 0.0f};
+  const int32_t rc = run(in_dtype, in_dtype, a, b, t, M, N, K, K, N, N, none, stream);
+  if (rc != ASC_OK) return rc;
+  return run(in_dtype, out_dtype, t, b, c, M, N, N, N, N, N, none, stream);
+}
+
 }  // namespace
+
+extern "C" int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c,
+                                      int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                                      asc_stream_t stream) {
+  return chained(in_dtype, out_dtype, a, b, c, M, N, K, workspace, workspace_bytes, stream, "asc_matmul_chained");
+}
 
 extern "C" int32_t asc_matmul(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M,
                               int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t relu,

@@ -353,6 +353,41 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False
     _native.call("asc_matmul_bias_act", *args, _stream(stream))
 
 
+def matmul_chained(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, workspace: Optional[torch.Tensor] = None,
+                   stream: Any = None) -> None:
+    """The asc2 chained matmul (python/test/asc2/kernels/test_matmul_l0c_to_l1.py:17-30):
+    t = (a @ b) cast to a's dtype, c = cast(t @ b) to c's dtype, fp32 accumulation, N == K.
+    ``workspace`` (a contiguous device tensor of at least M * N * 2 bytes) holds t; without
+    one it is taken from torch's allocator on the launch stream."""
+    for t, n in ((a, "a"), (b, "b"), (c, "c")):
+        _contiguous(_device_tensor(t, n), n)
+    in_code = _code(a, "a", (torch.float16, torch.bfloat16))
+    if b.dtype != a.dtype:
+        raise TypeError(f"a and b must share a dtype, got {a.dtype} and {b.dtype}")
+    out_code = _code(c, "c", (torch.float32, torch.float16, torch.bfloat16))
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError(f"a and b must be 2-D, got {tuple(a.shape)} and {tuple(b.shape)}")
+    M, K = a.shape
+    K2, N = b.shape
+    if K2 != K or N != K:
+        raise ValueError(f"the chained matmul needs b square and a's columns equal to its rows: a {tuple(a.shape)}, "
+                         f"b {tuple(b.shape)}")
+    if tuple(c.shape) != (M, N):
+        raise ValueError(f"c must be {(M, N)}, got {tuple(c.shape)}")
+    handle = _stream(stream)
+    if workspace is None:
+        workspace = torch.empty(M * N, dtype=a.dtype, device=a.device)
+        # freed on return: on a stream other than torch's current one the caching
+        # allocator must not hand its memory out again before these launches have run
+        if handle != torch.cuda.current_stream(a.device).cuda_stream:
+            workspace.record_stream(torch.cuda.ExternalStream(handle, device=a.device))
+    else:
+        _contiguous(_device_tensor(workspace, "workspace"), "workspace")
+    nbytes = workspace.numel() * workspace.element_size()
+    _native.call("asc_matmul_chained", in_code, out_code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K,
+                 workspace.data_ptr(), nbytes, handle)
+
+
 def matmul_plan(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, relu: bool = False,
                 bias: Optional[torch.Tensor] = None, leaky_alpha: Optional[float] = None) -> "_native.LaunchPlan":
     """The launch matmul(...) makes, as a kernel of the asc2_matmul code object with its

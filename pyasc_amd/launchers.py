@@ -375,8 +375,9 @@ def _fixpipe_body(call: KernelCall, mm) -> None:
     mm(a, b, c, relu=True, stream=call.stream)
 
 
-def _chained_body(call: KernelCall, mm) -> None:
-    # t = (a @ b).to(dtype); c = t @ b  (needs N == K)
+def _chained_body(call: KernelCall, mm, chained=None) -> None:
+    # t = (a @ b).to(dtype); c = t @ b  (needs N == K).  ``chained``: one call that runs both
+    # matmuls with its own intermediate (the library's asc_matmul_chained); else two ``mm``.
     M, N, K = _check_shapes(call)
     if N != K:
         raise ValueError(f"the chained matmul multiplies (a@b) by b again and needs N == K, got N={N}, K={K}")
@@ -385,6 +386,9 @@ def _chained_body(call: KernelCall, mm) -> None:
     mid_dtype = as_torch_dtype(call.consts["dtype"])
     if mid_dtype != b.dtype:
         raise TypeError(f"the intermediate dtype {mid_dtype} must match b's dtype {b.dtype} for the second matmul")
+    if chained is not None and a.dtype in (torch.float16, torch.bfloat16):
+        chained(a, b, c, stream=call.stream)
+        return
     t = torch.empty((M, N), dtype=mid_dtype, device=a.device)
     mm(a, b, t, stream=call.stream)
     mm(t, b, c, stream=call.stream)
@@ -428,7 +432,7 @@ def _matmul_fixpipe(call: KernelCall) -> None:
 @register("matmul_kernel", ("a_ptr", "b_ptr", "c_ptr", "a_shape", "b_shape", "c_shape", "dtype"),
           "python/test/asc2/kernels/test_matmul_l0c_to_l1.py:17-30", code_object=_matmul_code_object(_chained_body))
 def _matmul_chained(call: KernelCall) -> None:
-    _chained_body(call, kernels.matmul)
+    _chained_body(call, kernels.matmul, kernels.matmul_chained)
 
 
 # ------------------------------------------------------------- int8 matmul (build-defined asc2 style)

@@ -67,6 +67,12 @@ def test_version_string():
     ("asc_copy_bytes", (0, 32, 16, None), _native.ERR_INVALID_ARG),  # null src
     ("asc_copy_bytes", (16, 32, 24, None), _native.ERR_ALIGNMENT),  # size not a multiple of 16
     ("asc_copy_bytes", (8, 32, 16, None), _native.ERR_ALIGNMENT),  # unaligned src
+    # chained matmul: dtype codes 1 = float16, 0 = float32; N must equal K; the workspace
+    # must hold M * N * 2 bytes and be non-null
+    ("asc_matmul_chained", (0, 0, 16, 16, 16, 64, 64, 64, 32, 1 << 20, None), _native.ERR_UNSUPPORTED),
+    ("asc_matmul_chained", (1, 0, 16, 16, 16, 64, 64, 32, 32, 1 << 20, None), _native.ERR_INVALID_ARG),
+    ("asc_matmul_chained", (1, 0, 16, 16, 16, 64, 64, 64, 32, 64 * 64 * 2 - 1, None), _native.ERR_INVALID_ARG),
+    ("asc_matmul_chained", (1, 0, 16, 16, 16, 64, 64, 64, None, 1 << 20, None), _native.ERR_INVALID_ARG),
 ])
 def test_argument_errors_are_reported(fn, args, code):
     lib = _native.load_library()
@@ -88,4 +94,5 @@ def test_zero_sized_launch_is_a_noop():
     assert lib.asc_rect_binary(0, 0, None, None, None, 8, 8, 8, 0, 2, 2, None) == 0  # clipped to nothing
     assert lib.asc_vadd(0, None, None, None, 0, 128, 4, 16, None) == 0
     assert lib.asc_copy_bytes(None, None, 0, None) == 0
+    assert lib.asc_matmul_chained(1, 0, None, None, None, 0, 64, 64, None, 0, None) == 0
     assert lib.asc_vadd(0, None, None, None, 100, 128, 0, 16, None) == 0  # tile_per_block 0 covers nothing

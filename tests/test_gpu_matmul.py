@@ -156,3 +156,61 @@ def test_direct_path_repeat_runs_are_bit_identical(device):
         outs.append(c)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("dtype,out_dtype,M,N", [
+    (torch.float16, torch.float32, 32, 64), (torch.bfloat16, torch.float32, 64, 64),  # test_matmul_l0c_to_l1.py
+    (torch.float16, torch.float32, 256, 256), (torch.bfloat16, torch.float16, 512, 1024),  # tile-aligned
+    (torch.bfloat16, torch.bfloat16, 100, 96)])  # ragged
+def test_chained_entry_point(device, dtype, out_dtype, M, N):
+    # asc_matmul_chained (one call, intermediate in a workspace) against the same two
+    # matmuls launched one by one: identical kernels, so identical bits; and against the
+    # reference test's fp32 recipe (test_matmul_l0c_to_l1.py:46-50)
+    g = torch.Generator().manual_seed(M * 7 + N)
+    a = ((torch.rand((M, N), generator=g) - .5) * 2).to(dtype).to(device)
+    b = ((torch.rand((N, N), generator=g) - .5) * 2 / N ** .5).to(dtype).to(device)
+    c = torch.full((M, N), 7.0, dtype=out_dtype, device=device)
+    kernels.matmul_chained(a, b, c)
+    t = torch.empty((M, N), dtype=dtype, device=device)
+    c2 = torch.empty_like(c)
+    kernels.matmul(a, b, t)
+    kernels.matmul(t, b, c2)
+    ws = torch.full((M * N + 64,), float("nan"), dtype=dtype, device=device)  # a larger workspace
+    c3 = torch.empty_like(c)
+    kernels.matmul_chained(a, b, c3, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16) if out_dtype != torch.float32 else c.view(torch.int32),
+                       c2.view(torch.int16) if out_dtype != torch.float32 else c2.view(torch.int32))
+    assert torch.equal(c3, c)
+    assert torch.equal(ws[:M * N].view(M, N), t)
+    ref = (a.cpu().float() @ b.cpu().float()).to(dtype).float() @ b.cpu().float()
+    tol = 1e-3 if out_dtype == torch.float32 else 1e-2
+    torch.testing.assert_close(c.cpu().float(), ref, atol=tol, rtol=tol)
+
+
+def test_chained_entry_point_on_a_side_stream(device):
+    g = torch.Generator().manual_seed(5)
+    a = ((torch.rand((256, 256), generator=g) - .5) * 2).half().to(device)
+    b = ((torch.rand((256, 256), generator=g) - .5) / 8).half().to(device)
+    c = torch.empty((256, 256), device=device)
+    expected = torch.empty_like(c)
+    kernels.matmul_chained(a, b, expected)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    for _ in range(3):  # the workspace of each call is taken from the allocator and recorded on s
+        kernels.matmul_chained(a, b, c, stream=s)
+    s.synchronize()
+    assert torch.equal(c, expected)
+
+
+def test_chained_entry_point_errors(device):
+    a = torch.zeros((64, 32), dtype=torch.float16, device=device)
+    b = torch.zeros((32, 64), dtype=torch.float16, device=device)
+    with pytest.raises(ValueError, match="square"):
+        kernels.matmul_chained(a, b, torch.empty((64, 64), device=device))
+    sq = torch.zeros((32, 32), dtype=torch.float16, device=device)
+    with pytest.raises(RuntimeError, match="workspace holds"):
+        kernels.matmul_chained(a, sq, torch.empty((64, 32), device=device),
+                               workspace=torch.empty(64 * 32 - 1, dtype=torch.float16, device=device))
+    with pytest.raises(TypeError):
+        kernels.matmul_chained(a.float(), sq.float(), torch.empty((64, 32), device=device))
