@@ -306,6 +306,19 @@ int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a,
                            const void* b, void* c, int64_t M, int64_t N,
                            int64_t K, void* workspace, int64_t workspace_bytes,
                            asc_stream_t stream);
+/* asc_matmul_chained without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc); it has no counterpart in the reference.  The
+ * intermediate lives in the library's own scratch buffer of 32 MiB per GPU (a
+ * static device array, resident until the process ends), so M * N * 2 may not
+ * exceed 33554432 bytes (ASC_ERR_UNSUPPORTED otherwise).  Nothing is allocated:
+ * no hipMalloc, hipFree or allocating library call.  Every call on one GPU shares
+ * that buffer: calls that overlap on one GPU (on different streams, or from
+ * several threads) race on it; calls on one stream are ordered and safe. */
+int32_t asc_matmul_chained_noalloc(int32_t in_dtype, int32_t out_dtype,
+                                   const void* a, const void* b, void* c,
+                                   int64_t M, int64_t N, int64_t K,
+                                   asc_stream_t stream);
 /* The launch asc_matmul_bias_act makes with these arguments (asc_matmul(...,
  * relu) is act = relu, bias NULL), as a kernel of the code object
  * pyasc_amd/lib/co/asc2_matmul.hsaco (asc_launch_plan_t; the blob is the

@@ -75,6 +75,7 @@ SIGNATURES = {
     "asc_matmul_bias_act": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                             _c_i32, _c_f32, _c_p],
     "asc_matmul_chained": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    "asc_matmul_chained_noalloc": [_c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
     "asc_matmul_i8_i32": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
     "asc_matmul_i8_dequant_f16": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
     "asc_flash_attention_fwd_bf16": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_f32, _c_i32,

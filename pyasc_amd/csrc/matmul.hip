@@ -3,7 +3,15 @@
 // python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py): the
 // library's entry points and the launch plan the asc2 code-object path replays.
 // The device code and the choice of kernels are described in matmul_kernels.h.
+#include <mutex>
+
 #include "matmul_kernels.h"
+
+// The intermediate of asc_matmul_chained_noalloc: one chained matmul's t (M * N
+// 16-bit elements) at most, one copy per GPU, held until the process ends.  Host code
+// uses the per-device address from hipGetSymbolAddress, never the array's name.
+constexpr int64_t kChainedScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) uint8_t scratch[kChainedScratchBytes];
 
 namespace {
 
@@ -107,9 +115,8 @@ int32_t run(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, v
   return asc::check_launch("asc_matmul");
 }
 
-// t = cast(a . b) to in_dtype into `t` (t_bytes long), then c = cast(t . b) to out_dtype.
-int32_t chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
-                int64_t K, void* t, int64_t t_bytes, asc_stream_t stream, const char* who) {
+// Shape and dtype checks of a chained matmul (no device call).
+int32_t chained_check(int32_t in_dtype, int64_t M, int64_t N, int64_t K, const char* who) {
   ASC_REQUIRE(M >= 0 && N >= 0 && K >= 0, ASC_ERR_INVALID_ARG, "%s: negative shape", who);
   ASC_REQUIRE(in_dtype == ASC_DT_FLOAT16 || in_dtype == ASC_DT_BFLOAT16, ASC_ERR_UNSUPPORTED,
               "%s: input dtype %d is not float16 or bfloat16", who, in_dtype);
@@ -117,6 +124,14 @@ int32_t chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* 
               "%s: the chained matmul multiplies (a @ b) by b again and needs N == K, got N=%lld, K=%lld", who,
               (long long)N, (long long)K);
   ASC_REQUIRE(M < (1 << 30) && N < (1 << 30), ASC_ERR_UNSUPPORTED, "%s: shape too large", who);
+  return ASC_OK;
+}
+
+// t = cast(a . b) to in_dtype into `t` (t_bytes long), then c = cast(t . b) to out_dtype.
+int32_t chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c, int64_t M, int64_t N,
+                int64_t K, void* t, int64_t t_bytes, asc_stream_t stream, const char* who) {
+  const int32_t checked = chained_check(in_dtype, M, N, K, who);
+  if (checked != ASC_OK) return checked;
   if (M == 0 || N == 0) return ASC_OK;
   const int64_t need = M * N * 2;
   ASC_REQUIRE(t_bytes >= need, ASC_ERR_INVALID_ARG, "%s: the intermediate needs %lld bytes, the workspace holds %lld",
@@ -128,7 +143,48 @@ int32_t chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* 
   return run(in_dtype, out_dtype, t, b, c, M, N, N, N, N, N, none, stream);
 }
 
+// Device address of `scratch` on the current device, looked up on the first call on each
+// device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+int32_t scratch_address(void** out, const char* who) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  ASC_REQUIRE(err == hipSuccess, static_cast<int32_t>(err), "%s: hipGetDevice failed: %s", who,
+              hipGetErrorString(err));
+  ASC_REQUIRE(dev >= 0 && dev < kMaxDevices, ASC_ERR_UNSUPPORTED, "%s: device %d beyond the %d supported", who, dev,
+              kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    ASC_REQUIRE(err == hipSuccess && p != nullptr, err == hipSuccess ? ASC_ERR_UNSUPPORTED : static_cast<int32_t>(err),
+                "%s: hipGetSymbolAddress of the scratch buffer failed on device %d: %s", who, dev,
+                hipGetErrorString(err));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return ASC_OK;
+}
+
 }  // namespace
+
+extern "C" int32_t asc_matmul_chained_noalloc(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b,
+                                              void* c, int64_t M, int64_t N, int64_t K, asc_stream_t stream) {
+  const char* who = "asc_matmul_chained_noalloc";
+  const int32_t checked = chained_check(in_dtype, M, N, K, who);
+  if (checked != ASC_OK) return checked;
+  if (M == 0 || N == 0) return ASC_OK;
+  ASC_REQUIRE(M * N * 2 <= kChainedScratchBytes, ASC_ERR_UNSUPPORTED,
+              "%s: the intermediate of %lld x %lld needs %lld bytes, above the %lld-byte scratch buffer", who,
+              (long long)M, (long long)N, (long long)(M * N * 2), (long long)kChainedScratchBytes);
+  void* t = nullptr;
+  const int32_t rc = scratch_address(&t, who);
+  if (rc != ASC_OK) return rc;
+  return chained(in_dtype, out_dtype, a, b, c, M, N, K, t, kChainedScratchBytes, stream, who);
+}
 
 extern "C" int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c,
                                       int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,

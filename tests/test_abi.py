@@ -73,6 +73,10 @@ def test_version_string():
     ("asc_matmul_chained", (1, 0, 16, 16, 16, 64, 64, 32, 32, 1 << 20, None), _native.ERR_INVALID_ARG),
     ("asc_matmul_chained", (1, 0, 16, 16, 16, 64, 64, 64, 32, 64 * 64 * 2 - 1, None), _native.ERR_INVALID_ARG),
     ("asc_matmul_chained", (1, 0, 16, 16, 16, 64, 64, 64, None, 1 << 20, None), _native.ERR_INVALID_ARG),
+    # the allocation-free form: same checks, and an intermediate above its 32 MiB scratch buffer
+    ("asc_matmul_chained_noalloc", (0, 0, 16, 16, 16, 64, 64, 64, None), _native.ERR_UNSUPPORTED),
+    ("asc_matmul_chained_noalloc", (1, 0, 16, 16, 16, 64, 64, 32, None), _native.ERR_INVALID_ARG),
+    ("asc_matmul_chained_noalloc", (1, 0, 16, 16, 16, 4097, 4096, 4096, None), _native.ERR_UNSUPPORTED),
 ])
 def test_argument_errors_are_reported(fn, args, code):
     lib = _native.load_library()
@@ -95,4 +99,5 @@ def test_zero_sized_launch_is_a_noop():
     assert lib.asc_vadd(0, None, None, None, 0, 128, 4, 16, None) == 0
     assert lib.asc_copy_bytes(None, None, 0, None) == 0
     assert lib.asc_matmul_chained(1, 0, None, None, None, 0, 64, 64, None, 0, None) == 0
+    assert lib.asc_matmul_chained_noalloc(2, 0, None, None, None, 0, 64, 64, None) == 0
     assert lib.asc_vadd(0, None, None, None, 100, 128, 0, 16, None) == 0  # tile_per_block 0 covers nothing

@@ -1,0 +1,59 @@
+"""asc_matmul_chained_noalloc (the allocation-free chained matmul, intermediate in the
+library's per-GPU scratch buffer) against asc_matmul_chained (intermediate in a workspace
+the caller passes), through the C ABI: bit-identical results on two calls in a row, the
+first filling the whole 32 MiB buffer, the second smaller, with other dtypes."""
+import pytest
+import torch
+
+from pyasc_amd import _native
+
+pytestmark = pytest.mark.gpu
+
+_CODES = {torch.float32: _native.DT_FLOAT32, torch.float16: _native.DT_FLOAT16, torch.bfloat16: _native.DT_BFLOAT16}
+
+
+def _inputs(M, N, dtype, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    a = ((torch.rand((M, N), generator=g) - .5) * 2).to(dtype).to(device)
+    b = ((torch.rand((N, N), generator=g) - .5) * 2 / N ** .5).to(dtype).to(device)
+    return a, b
+
+
+def _run_both(a, b, out_dtype, device):
+    M, N = a.shape
+    stream = torch.cuda.current_stream().cuda_stream
+    c_ws = torch.full((M, N), float("nan"), dtype=out_dtype, device=device)
+    c_na = torch.full((M, N), float("nan"), dtype=out_dtype, device=device)
+    ws = torch.empty(M * N, dtype=a.dtype, device=device)
+    _native.call("asc_matmul_chained", _CODES[a.dtype], _CODES[out_dtype], a.data_ptr(), b.data_ptr(),
+                 c_ws.data_ptr(), M, N, N, ws.data_ptr(), ws.numel() * ws.element_size(), stream)
+    _native.call("asc_matmul_chained_noalloc", _CODES[a.dtype], _CODES[out_dtype], a.data_ptr(), b.data_ptr(),
+                 c_na.data_ptr(), M, N, N, stream)
+    torch.cuda.synchronize()
+    return c_ws, c_na
+
+
+def test_noalloc_matches_workspace_entry_point_on_consecutive_calls(device):
+    # call 1 fills the whole scratch buffer (4096 x 4096 bf16 = 32 MiB); call 2 is smaller and
+    # ragged, so it reads back only what it wrote over call 1's contents
+    for (M, N, dtype, out_dtype, seed) in [(4096, 4096, torch.bfloat16, torch.float32, 1),
+                                           (200, 192, torch.float16, torch.bfloat16, 2)]:
+        print(f"chained noalloc vs workspace: M={M} N=K={N} {dtype} -> {out_dtype}", flush=True)
+        a, b = _inputs(M, N, dtype, seed, device)
+        c_ws, c_na = _run_both(a, b, out_dtype, device)
+        bits = torch.int32 if out_dtype == torch.float32 else torch.int16
+        assert not torch.isnan(c_ws).any()
+        assert torch.equal(c_na.view(bits), c_ws.view(bits))
+        # and the reference recipe (test_matmul_l0c_to_l1.py:48-50), on a slice of rows
+        rows = slice(0, min(M, 256))
+        ref = (a[rows].cpu().float() @ b.cpu().float()).to(dtype).float() @ b.cpu().float()
+        torch.testing.assert_close(c_na[rows].cpu().float(), ref, atol=1e-2, rtol=1e-2)
+
+
+def test_noalloc_rejects_an_intermediate_above_the_buffer(device):
+    a = torch.zeros((4097, 4096), dtype=torch.float16, device=device)
+    b = torch.zeros((4096, 4096), dtype=torch.float16, device=device)
+    c = torch.zeros((4097, 4096), dtype=torch.float16, device=device)
+    with pytest.raises(RuntimeError, match="scratch buffer"):
+        _native.call("asc_matmul_chained_noalloc", _native.DT_FLOAT16, _native.DT_FLOAT16, a.data_ptr(),
+                     b.data_ptr(), c.data_ptr(), 4097, 4096, 4096, torch.cuda.current_stream().cuda_stream)
