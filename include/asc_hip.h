@@ -300,8 +300,9 @@ int32_t asc_matmul_bias_act(int32_t in_dtype, int32_t out_dtype, const void* a,
  * and contiguous.  in_dtype: ASC_DT_FLOAT16 or ASC_DT_BFLOAT16 (A, B and the
  * intermediate alike); out_dtype as in asc_matmul.  The intermediate t
  * (M * N elements of in_dtype, row-major) is written to `workspace`, which must
- * hold workspace_bytes >= M * N * 2 bytes; the two matmuls run in order on
- * `stream`, so the workspace may be reused once they have run. */
+ * hold workspace_bytes >= M * N * 2 bytes and must not overlap A, B or C; the
+ * two matmuls run in order on `stream`, so the workspace may be reused once they
+ * have run. */
 int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a,
                            const void* b, void* c, int64_t M, int64_t N,
                            int64_t K, void* workspace, int64_t workspace_bytes,
