@@ -12,29 +12,33 @@ kernels of the adjacent rows are measured the same way and reported under
 "suite", with a plain streaming copy of the same sizes as the bandwidth
 reference of the HBM-bound kernels.
 
-Timing: W untimed warm-up steps, then exactly K steps bracketed by
-torch.cuda.synchronize().  The K launches are captured into one HIP graph and
-one replay is timed with HIP events on the replay stream (the kernels run back
-to back, without host launch overhead); --no-graph times each launch with its
-own event pair instead.  HBM-bound workloads rotate through enough
-input/output sets (> 512 MiB) that the 256 MiB Infinity Cache cannot serve
-them; so do the MFMA workloads.  The CPU baseline of every workload is the
-reference test's torch CPU golden expression (oracle/cpu_golden.py), timed on
-the host cores on the full workload (repeated to at least 2 s of CPU work, 10 s
-for the headline); each names the host (thread count, os.cpu_count(), CPU
-model) it ran on.
+Timing (steady state, in the manner of the reference's median-with-skip,
+python/asc/lib/profiling/result.py:33-47): per workload, W untimed eager launches,
+then the K timed launches captured into one HIP graph and replayed back to back
+for at least WARMUP_S seconds (clocks and caches settle), then REPLAYS replays of
+exactly K launches, each between its own pair of HIP events on the replay stream;
+the figure is the median replay / K, with the fastest and slowest replay beside
+it.  --no-graph times each launch with its own event pair instead.  HBM-bound
+workloads rotate through enough input/output sets (> 512 MiB) that the 256 MiB
+Infinity Cache cannot serve them; so do the MFMA workloads.  Every GPU leg runs
+before any CPU baseline.  The CPU baseline of every workload is the reference
+test's torch CPU golden expression (oracle/cpu_golden.py), timed on the host cores
+on the full workload (the int8 product on a quarter of A's rows), repeated to at
+least 2 s of CPU work (10 s for the headline); the line names the host (thread
+count, os.cpu_count(), CPU model) once.
 
-With the suite, a power phase follows: the headline and each MFMA workload launch for
-about 3 s while amd-smi samples socket power and graphics clock ("power" in the line;
-for the MFMA workloads also the dense peak at the sampled clock and the fraction of it
-reached).
+With the suite, a power phase follows the suite: the headline and each MFMA
+workload are measured again after 3 s of warm-up while amd-smi samples socket
+power and graphics clock ("power" in the line; for the MFMA workloads also the
+fraction of the dense peak at the sampled clock).
 
 `roofline.traffic` comes from profiles/traffic.json (rocprofv3 FETCH_SIZE /
 WRITE_SIZE passes summarised by profile_summary.py).  Each entry is stamped with
 a hash of the kernel sources it was measured on; when the sources have changed
 since, the bench reports null instead of a stale figure.
 
-Prints ONE JSON line.
+Prints ONE JSON line of under 8 KB (the headline in full, a compact entry per suite
+workload); --detail FILE writes every figure in full.
 """
 from __future__ import annotations
 
@@ -60,6 +64,9 @@ SMALL_SET_BYTES = 4 << 20  # below this a workload is latency-bound and is not r
 CSRC = os.path.join(REPO, "pyasc_amd", "csrc")
 CPU_MIN_S = 2.0  # timed CPU work per suite baseline (the full workload, repeated to at least this long)
 CPU_HEADLINE_S = 10.0  # the same for the headline's baseline
+WARMUP_S = 1.0  # least warm-up per workload: graph replays of its timed launches (clocks and caches settle)
+REPLAYS = 7  # timed graph replays per workload; the figure is their median
+LINE_LIMIT = 8192  # the stdout line stays below this many bytes (longer lines are not read back)
 
 
 class Workload:
@@ -664,10 +671,14 @@ class MatmulI8(Workload):
         a = torch.randint(-127, 128, (self.M, self.K), dtype=torch.int8, generator=g)
         b = torch.randint(-127, 128, (self.K, self.N), dtype=torch.int8, generator=g)
         scale = torch.rand(self.N, generator=g) * 0.009 + 0.001
-        return _cpu(self.work(), 1e12, "TOPS",
+        # torch's int32 CPU product runs at some 20-40 GOPS: a quarter of A's rows keeps the
+        # sample to a few seconds; the rate is per operation, so it scales to the full shape
+        rows = min(self.M, 1024)
+        a = a[:rows].contiguous()
+        return _cpu(2.0 * rows * self.N * self.K, 1e12, "TOPS",
                     "(a.to(int32) @ b.to(int32)) then (acc.float() * scale).half() "
                     "(test_matmul_iterate_all.py:116; dequant of test_matmul_quant.py)",
-                    f"the full {self.M}x{self.N}x{self.K} workload",
+                    f"the first {rows} of {self.M} rows of A ({rows}x{self.N}x{self.K}), same B and scale",
                     _time_cpu(lambda: cpu_golden.dequant(cpu_golden.matmul_i8(a, b), scale), min_total_s))
 
 
@@ -828,15 +839,24 @@ class PowerSampler:
                 "source": "amd-smi metric -p -c -g 0 (SOCKET_POWER; mean of the GFX_n CLK readings)"}
 
 
-def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True, sampler: PowerSampler = None) -> dict:
-    """Times exactly ``steps`` launches on the launch stream with HIP events.
+def _median(v):
+    v = sorted(v)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
 
-    Default: the ``steps`` launches are captured once into a HIP graph and the
-    graph is replayed between two events recorded on the replay stream, so the
-    kernels run back to back with no host launch overhead in the timed region
-    (``kernel_ms`` = region / steps).  ``graph=False``: each launch is bracketed
-    by its own event pair instead and ``kernel_ms`` is their mean (adds about
-    2 us of event overhead per launch)."""
+
+def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True, sampler: PowerSampler = None,
+            warmup_s: float = WARMUP_S, replays: int = REPLAYS) -> dict:
+    """Times ``steps`` launches on the launch stream with HIP events, ``replays`` times.
+
+    Warm-up: ``warmup`` eager launches, then the timed launches themselves (captured once
+    into a HIP graph) replayed back to back until at least ``warmup_s`` seconds have
+    passed, so the clocks and caches are in the state the timed replays run in.
+    Timed region: ``replays`` graph replays, each of exactly ``steps`` launches and each
+    between its own pair of events recorded on the replay stream, issued without a host
+    synchronisation in between (the device stays busy); ``kernel_ms`` is the median replay
+    time / ``steps``, with the fastest and slowest replay beside it.  ``graph=False`` times
+    each launch with its own event pair instead and reports the median launch."""
     import torch
     w.setup(dev)
     if sampler is not None:
@@ -844,43 +864,58 @@ def measure(w: Workload, steps: int, warmup: int, dev, graph: bool = True, sampl
     for i in range(warmup):
         w.launch(i)
     torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    warm_launches = warmup
     if graph:
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
+        s.wait_stream(stream)
         with torch.cuda.stream(s):
             with torch.cuda.graph(g, stream=s):
                 for i in range(steps):
                     w.launch(warmup + i)
         torch.cuda.synchronize()
-        g.replay()  # untimed: first replay uploads the graph
+        t0 = time.perf_counter()
+        while True:  # the first replay also uploads the graph
+            g.replay()
+            torch.cuda.synchronize()
+            warm_launches += steps
+            if time.perf_counter() - t0 >= warmup_s:
+                break
+        warm_seconds = time.perf_counter() - t0
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+        for a, b in ev:
+            a.record(stream)
+            g.replay()
+            b.record(stream)
         torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        g.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / steps
-        kernel_ms = ms
+        per_step = [a.elapsed_time(b) / steps for a, b in ev]
         del g
     else:
-        stream = torch.cuda.current_stream()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < warmup_s:
+            for i in range(steps):
+                w.launch(warmup + i)
+            torch.cuda.synchronize()
+            warm_launches += steps
+        warm_seconds = time.perf_counter() - t0
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-        torch.cuda.synchronize()
         for i in range(steps):
             ev[i][0].record(stream)
             w.launch(warmup + i)
             ev[i][1].record(stream)
         torch.cuda.synchronize()
-        ms = ev[0][0].elapsed_time(ev[-1][1]) / steps
-        kernel_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+        per_step = [a.elapsed_time(b) for a, b in ev]
     if sampler is not None:
         sampler.stop()
+    kernel_ms = _median(per_step)
     value = w.value(kernel_ms / 1e3)
-    return {"workload": w.name, "ms_per_step": ms, "kernel_ms": kernel_ms, "value": value, "unit": w.unit,
-            "rate": w.rate(kernel_ms / 1e3), "bound": w.bound, "config": w.config(),
-            "timing": "hip-graph replay" if graph else "per-launch events"}
+    return {"workload": w.name, "ms_per_step": kernel_ms, "kernel_ms": kernel_ms, "ms_min": min(per_step),
+            "ms_max": max(per_step), "value": value, "unit": w.unit, "rate": w.rate(kernel_ms / 1e3),
+            "bound": w.bound, "config": w.config(), "replays": len(per_step) if graph else 0,
+            "warmup_launches": warm_launches, "warmup_s": round(warm_seconds, 2),
+            "timing": (f"median of {replays} hip-graph replays of {steps} launches" if graph
+                       else f"median of {steps} per-launch event pairs")}
 
 
 def vendor(w: Workload, steps: int, res: dict):
@@ -925,29 +960,25 @@ POWER_WORKLOADS = ["softmax_4096x4096", "matmul_bf16_8192", "matmul_i8_4096x1100
 POWER_SECONDS = 3.0
 
 
-def power_phase(dev, kernel_ms: dict) -> dict:
-    """Socket power and graphics clock while each of POWER_WORKLOADS that ran (``kernel_ms``:
-    workload key -> ms per launch) launches for about POWER_SECONDS (its warm-up), sampled
-    with PowerSampler.  For an MFMA workload the entry also gives the dense peak at the
-    sampled clock (peak x MHz / 2400) and the fraction of it this run reached: the MFMA
-    kernels hold the board at its power limit, which sets the clock."""
+def power_phase(dev, keys, steps: int) -> dict:
+    """Socket power and graphics clock while each of ``keys`` (of POWER_WORKLOADS) is
+    measured again with POWER_SECONDS of warm-up, sampled with PowerSampler.  For an MFMA
+    workload the entry also gives the dense peak at the sampled clock (peak x MHz / 2400)
+    and the fraction of it this run reached: the MFMA kernels hold the board at its power
+    limit, which sets the clock."""
     import torch
     out = {}
-    for key in POWER_WORKLOADS:
-        ms = kernel_ms.get(key)
-        if not ms:
-            continue
+    for key in keys:
         w = WORKLOADS[key]()
         sampler = PowerSampler()
-        warmup = max(10, min(400000, int(POWER_SECONDS / (ms * 1e-3))))
-        r = measure(w, 20, warmup, dev, sampler=sampler)
-        entry = {"value": round(r["value"], 3), "unit": w.unit, "warmup_launches": warmup, **sampler.summary()}
+        r = measure(w, steps, 10, dev, sampler=sampler, warmup_s=POWER_SECONDS)
+        entry = {"value": round(r["value"], 3), "unit": w.unit, "warmup_s": r["warmup_s"], **sampler.summary()}
         mhz = entry.get("gfx_mhz_median")
         if mhz and w.bound == "mfma":
             peak = w.peak * mhz / 2400.0
             entry["dense_peak_at_clock"] = round(peak, 1)
             entry["frac_at_clock"] = round(r["value"] / peak, 4)
-        out[w.name] = entry
+        out[key] = entry
         print(f"bench: power {w.name} {r['value']:.1f} {w.unit}, {entry.get('socket_w_median')} W, "
               f"{mhz} MHz", file=sys.stderr, flush=True)
         del w
@@ -1087,11 +1118,92 @@ def traffic_for(w: Workload):
     return entry.get("bytes")
 
 
+def _sig(x, digits: int = 4):
+    """``x`` rounded to ``digits`` significant digits (None stays None)."""
+    if x is None or x == 0:
+        return x
+    return round(x, max(0, digits - 1 - int(math.floor(math.log10(abs(x))))))
+
+
+def compact_roofline(r: dict) -> dict:
+    return {"frac": r["frac"], "achieved": _sig(r["achieved"], 5), "traffic": r.get("traffic")}
+
+
+def compact_cpu(c):
+    if not c:
+        return None
+    return {"value": _sig(c["value"], 4), "unit": c["unit"], "cores": c["cores"],
+            "seconds_per_call": _sig(c["seconds_per_call"], 4)}
+
+
+def compact_entry(res: dict, roof: dict, cpu) -> dict:
+    """One suite entry of the stdout line."""
+    return {"value": _sig(res["value"], 5), "unit": res["unit"], "ms_per_step": _sig(res["ms_per_step"], 5),
+            "ms_min": _sig(res["ms_min"], 5), "ms_max": _sig(res["ms_max"], 5),
+            "roofline": compact_roofline(roof), "cpu_baseline": compact_cpu(cpu),
+            **({"vs_vendor": res["vendor"]["this_over_vendor"]} if (res.get("vendor") or {}).get("value") else {})}
+
+
+def build_line(args, head, res: dict, cpu, suite: dict, extra: dict) -> dict:
+    """The ONE stdout line: the headline's figures, roofline and CPU baseline in full, and
+    for every suite workload its value, median/min/max time per step, roofline fraction,
+    achieved rate and traffic, and CPU baseline (``suite``: key -> compact_entry).  The
+    host block appears once.  ``extra`` holds short summaries (power, launch latency, the
+    reference's published durations)."""
+    roof = roofline(head, res)
+    head_cpu = None
+    if cpu:
+        head_cpu = {"value": _sig(cpu["value"], 5), "unit": cpu["unit"], "cores": cpu["cores"], "kind": cpu["kind"],
+                    "sample": cpu["sample"], "expression": cpu["expression"],
+                    "seconds_per_call": _sig(cpu["seconds_per_call"], 5)}
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 3),
+        "unit": head.unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": head.bound != "latency",
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head.dtype,
+        "data": "synthetic (seeded torch generator on the device; distribution of BASELINE.json's config)",
+        "config": {k: v for k, v in head.config().items() if k != "input"},
+        "roofline": roof,
+        "cpu_baseline": head_cpu,
+        "timing": {"method": res["timing"], "ms_min": _sig(res["ms_min"], 5), "ms_max": _sig(res["ms_max"], 5),
+                   "warmup_s": res["warmup_s"], "warmup_launches": res["warmup_launches"],
+                   "cpu_after_gpu": True},
+        "host": host_info() if cpu or any(e.get("cpu_baseline") for e in suite.values()) else None,
+        "suite": suite,
+    }
+    line.update(extra)
+    return line
+
+
+def serialize_line(line: dict) -> str:
+    """The line as compact JSON below LINE_LIMIT bytes: should it be longer, the optional
+    summaries go first, then the suite's CPU baselines (both stay in --detail)."""
+    text = json.dumps(line, separators=(",", ":"))
+    for trim in ("power", "launch_latency_us", "reference_published_us", "suite_cpu"):
+        if len(text) < LINE_LIMIT:
+            break
+        if trim == "suite_cpu":
+            for e in line["suite"].values():
+                e.pop("cpu_baseline", None)
+        else:
+            line.pop(trim, None)
+        print(f"bench: line over {LINE_LIMIT} bytes; dropped {trim}", file=sys.stderr, flush=True)
+        text = json.dumps(line, separators=(",", ":"))
+    return text
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU baseline")
@@ -1101,6 +1213,9 @@ def main() -> int:
     ap.add_argument("--no-power", action="store_true",
                     help="skip the power phase (with the suite: socket power and graphics clock sampled with "
                          "amd-smi during about 3 s of launches of the headline and of each MFMA workload)")
+    ap.add_argument("--detail", metavar="FILE",
+                    help="also write every figure in full (configs, CPU samples, vendor comparisons, power "
+                         "readings, launch latency) to FILE as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's device copy of 256 MiB 5 times (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -1118,29 +1233,36 @@ def main() -> int:
     _native.load_library()
     dev = torch.device("cuda", 0)
 
+    # GPU legs first, back to back: the headline, the suite, the power phase, launch costs
     head = WORKLOADS[args.workload]()
     res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph)
     head_vendor = None if args.no_vendor else vendor(head, args.steps, res)
-    print(f"bench: {head.name} {res['value']:.2f} {head.unit}", file=sys.stderr, flush=True)
-    suite = {}
+    print(f"bench: {head.name} {res['value']:.2f} {head.unit} (replays {res['ms_min'] * 1e3:.2f}-"
+          f"{res['ms_max'] * 1e3:.2f} us/step)", file=sys.stderr, flush=True)
+    del head
+    torch.cuda.empty_cache()
+    head = WORKLOADS[args.workload]()
+    suite_res = {}
+    keys = [] if args.no_suite else [k for k in SUITE if k != args.workload]
+    for key in keys:
+        w = WORKLOADS[key]()
+        r = measure(w, args.steps, args.warmup, dev, graph=not args.no_graph,
+                    replays=REPLAYS if w.bound != "latency" else 3 * REPLAYS)
+        r["roofline"] = roofline(w, r)
+        r["vendor"] = None if args.no_vendor else vendor(w, args.steps, r)
+        suite_res[key] = r
+        v = r["vendor"]
+        print(f"bench: {w.name} {r['value']:.2f} {w.unit} [{r['ms_min'] * 1e3:.2f}-{r['ms_max'] * 1e3:.2f} us]" +
+              (f" (vendor {v['value']:.2f})" if v and "value" in v else ""), file=sys.stderr, flush=True)
+        del w
+        torch.cuda.empty_cache()
+    latency = published = power = None
     if not args.no_suite:
-        for name in SUITE:
-            if name == args.workload:
-                continue
-            w = WORKLOADS[name]()
-            r = measure(w, max(5, args.steps // 2), max(2, args.warmup // 2), dev, graph=not args.no_graph)
-            r["roofline"] = roofline(w, r)
-            r["vendor"] = None if args.no_vendor else vendor(w, max(5, args.steps // 2), r)
-            if not args.no_cpu:
-                r["cpu_baseline"] = w.cpu_baseline()
-            suite[name] = r
-            v = r["vendor"]
-            print(f"bench: {w.name} {r['value']:.2f} {w.unit}" +
-                  (f" (vendor {v['value']:.2f})" if v and "value" in v else ""), file=sys.stderr, flush=True)
-            del w
-            torch.cuda.empty_cache()
-    latency = None if args.no_suite else launch_latency(dev)
-    published = None if args.no_suite else reference_durations(dev)
+        latency = launch_latency(dev)
+        published = reference_durations(dev)
+        if not args.no_power:
+            power = power_phase(dev, [k for k in POWER_WORKLOADS if k == args.workload or k in suite_res],
+                                args.steps)
     if args.copy_calibration:
         src = torch.empty((256 << 20) // 4, device=dev)
         dst = torch.empty_like(src)
@@ -1148,36 +1270,43 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    cpu = None if args.no_cpu else head.cpu_baseline(CPU_HEADLINE_S)
-    line = {
-        "metric": METRIC,
-        "value": round(res["value"], 3),
-        "unit": head.unit,
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": res["ms_per_step"],
-        "kernel_ms": res["kernel_ms"],
-        "timing": res["timing"],
-        "higher_is_better": head.bound != "latency",
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": head.dtype,
-        "data": "synthetic (seeded torch generator on the device; distribution of BASELINE.json's config)",
-        "config": head.config(),
-        "roofline": roofline(head, res),
-        "cpu_baseline": cpu,
-        "vendor": head_vendor,
-        "device": _native.device_info(0),
-        "suite": suite,
-        "launch_latency": latency,
-        "reference_published": published,
-    }
-    if not args.no_power and not args.no_suite:
-        timings = {args.workload: res["kernel_ms"]}
-        timings.update({k: r["kernel_ms"] for k, r in suite.items()})
-        line["power"] = power_phase(dev, timings)
-    print(json.dumps(line), flush=True)
+    torch.cuda.synchronize()
+
+    # CPU baselines after every GPU leg (they leave the GPU idle)
+    cpu = None
+    cpu_suite = {}
+    if not args.no_cpu:
+        cpu = head.cpu_baseline(CPU_HEADLINE_S)
+        print(f"bench: cpu {head.name} {cpu['value']:.4g} {cpu['unit']}", file=sys.stderr, flush=True)
+        for key in suite_res:
+            c = WORKLOADS[key]().cpu_baseline()
+            cpu_suite[key] = c
+            print(f"bench: cpu {key} {c['value']:.4g} {c['unit']}", file=sys.stderr, flush=True)
+
+    suite = {k: compact_entry(r, r["roofline"], cpu_suite.get(k)) for k, r in suite_res.items()}
+    extra = {}
+    if power:
+        extra["power"] = {k: {"value": _sig(p["value"], 5), "w": p.get("socket_w_median"),
+                              "mhz": p.get("gfx_mhz_median"), "frac_at_clock": p.get("frac_at_clock")}
+                          for k, p in power.items()}
+    if latency:
+        extra["launch_latency_us"] = {"asc2": latency["asc2_cached_us"],
+                                      "asc2_always_compile": latency["asc2_always_compile_us"],
+                                      "kernel_api": latency["kernel_api_us"]}
+    if published:
+        extra["reference_published_us"] = {k: [v["us_per_launch"], v["reference_task_duration_us"]]
+                                           for k, v in published.items()}
+    line = build_line(args, head, res, cpu, suite, extra)
+    text = serialize_line(line)
+    if args.detail:
+        detail = {"line": line, "headline": {**res, "vendor": head_vendor, "cpu_baseline": cpu},
+                  "suite": {k: {**r, "cpu_baseline": cpu_suite.get(k)} for k, r in suite_res.items()},
+                  "power": power, "launch_latency": latency, "reference_published": published,
+                  "device": _native.device_info(0), "host": host_info()}
+        os.makedirs(os.path.dirname(os.path.abspath(args.detail)), exist_ok=True)
+        with open(args.detail, "w") as f:
+            json.dump(detail, f, indent=1, default=str)
+    print(text, flush=True)
     return 0
 
 

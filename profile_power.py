@@ -6,8 +6,9 @@ Needs the GPU and ``amd-smi``.  Two parts, both sampled with bench.PowerSampler
 (``amd-smi metric -p -c -g 0`` about every 0.4 s; median of the samples after the first
 two):
 
-1. Each workload below runs through ``bench.measure`` with a warm-up of about four
-   seconds of launches; the sampler covers the warm-up and the timed replay.  Energy per
+1. Each workload below runs through ``bench.measure`` with four seconds of warm-up
+   (graph replays of its timed launches); the sampler covers the warm-up and the timed
+   replays.  Energy per
    operation = median socket power x time per launch / operations per launch.
 2. The same GEMM kernels on one round of 128 output tiles (half of the 256 CUs busy) and
    on one round of 256 tiles (all CUs), launched back to back for three seconds each:
@@ -24,15 +25,9 @@ import bench
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 
-# workload -> warm-up launches (about 4 s each on an MI355X)
-WORKLOADS = {
-    "matmul_bf16_8192": 5000,
-    "matmul_i8_4096x11008x4096": 21000,
-    "fa_fwd_noncausal": 4500,
-    "fa_fwd_causal": 7500,
-    "softmax_4096x4096": 180000,
-    "vadd_268435456": 8000,
-}
+WORKLOADS = ["matmul_bf16_8192", "matmul_i8_4096x11008x4096", "fa_fwd_noncausal", "fa_fwd_causal",
+             "softmax_4096x4096", "vadd_268435456"]
+WARMUP_S = 4.0
 ROUNDS = [  # (dtype, M, N, K): 128 tiles of 256x256 (half the CUs), then 256 (all)
     ("int8", 2048, 4096, 4096), ("int8", 4096, 4096, 4096),
     ("int8", 2048, 4096, 16384), ("int8", 4096, 4096, 16384),
@@ -46,10 +41,10 @@ def _fmt(v, nd=1):
 
 def workloads(dev) -> list:
     rows = []
-    for name, warmup in WORKLOADS.items():
+    for name in WORKLOADS:
         w = bench.WORKLOADS[name]()
         s = bench.PowerSampler()
-        r = bench.measure(w, 20, warmup, dev, sampler=s)
+        r = bench.measure(w, 20, 10, dev, sampler=s, warmup_s=WARMUP_S)
         p = s.summary()
         watts, mhz = p.get("socket_w_median"), p.get("gfx_mhz_median")
         row = {"name": w.name, "value": r["value"], "unit": w.unit, "bound": w.bound, "power": p,

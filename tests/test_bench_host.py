@@ -59,3 +59,81 @@ def test_power_phase_covers_the_headline_and_the_mfma_workloads():
     assert bench.POWER_WORKLOADS[0] == bench.HEADLINE
     for key in bench.POWER_WORKLOADS[1:]:
         assert bench.WORKLOADS[key]().bound == "mfma"
+
+
+def _stub_result(w, ms: float) -> dict:
+    """What bench.measure returns, for a workload timed at ``ms`` per launch (no GPU)."""
+    return {"workload": w.name, "ms_per_step": ms, "kernel_ms": ms, "ms_min": ms * 0.99, "ms_max": ms * 1.013,
+            "value": w.value(ms / 1e3), "unit": w.unit, "rate": w.rate(ms / 1e3), "bound": w.bound,
+            "config": {"workload": w.name}, "replays": 7, "warmup_launches": 123456, "warmup_s": 1.0,
+            "timing": "median of 7 hip-graph replays of 20 launches",
+            "vendor": {"value": 1.0, "this_over_vendor": 1.093}}
+
+
+def _stub_cpu(unit: str) -> dict:
+    return {"value": 12.3456789, "unit": unit, "cores": 128, "kind": "port",
+            "expression": "torch.softmax(x, dim=1) (python/test/asc2/kernels/test_softmax.py:43)",
+            "sample": "the full 4096x4096 fp32 workload; 1234 timed call(s) after 1 warm-up, mean (10.0 s of CPU work)",
+            "seconds_per_call": 0.0123456789, "host": {}}
+
+
+class _Args:
+    steps, warmup = 20, 5
+
+
+def _full_line():
+    import math
+    suite = {}
+    for i, key in enumerate(bench.SUITE):
+        w = bench.WORKLOADS[key]()
+        w.sets = w.xs = [None] * 3  # config() reads the rotation count
+        r = _stub_result(w, 0.0123456789 * (i + 1) * math.pi)
+        r["roofline"] = bench.roofline(w, r)
+        r["roofline"]["traffic"] = 1234567890
+        suite[key] = bench.compact_entry(r, r["roofline"], _stub_cpu(w.unit))
+    head = bench.WORKLOADS[bench.HEADLINE]()
+    head.xs = [None] * 5
+    res = _stub_result(head, 0.0230456)
+    power = {k: {"value": 1234.5678, "w": 1391.0, "mhz": 1932, "frac_at_clock": 0.5702} for k in bench.POWER_WORKLOADS}
+    extra = {"power": power, "launch_latency_us": {"asc2": 9.87, "asc2_always_compile": 31.2, "kernel_api": 6.5},
+             "reference_published_us": {"asc1_vadd_8192_f32": [2.1, 3.6],
+                                        "asc1_matmul_256_f32_bias_leakyrelu": [9.9, 25.5]}}
+    return bench.build_line(_Args, head, res, _stub_cpu("GB/s"), suite, extra)
+
+
+def test_stdout_line_is_compact_and_parses():
+    import io
+    import json
+    text = bench.serialize_line(_full_line())
+    assert len(text) < 8192, len(text)
+    # what a reader of the run's stdout sees: progress on stderr, the line last on stdout
+    out = io.StringIO("some earlier output\n" + text + "\n")
+    line = json.loads(out.getvalue().strip().splitlines()[-1])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in line, key
+    assert set(line["roofline"]) >= {"bound", "achieved", "peak", "unit", "frac", "traffic"}
+    assert set(line["cpu_baseline"]) >= {"value", "unit", "cores", "kind", "sample"}
+    assert line["steps"] == 20 and line["warmup"] == 5 and line["n_gpus"] == 1
+    assert set(line["suite"]) == set(bench.SUITE)
+    for key, e in line["suite"].items():
+        assert set(e["roofline"]) == {"frac", "achieved", "traffic"}, key
+        assert set(e["cpu_baseline"]) == {"value", "unit", "cores", "seconds_per_call"}, key
+        assert e["ms_min"] <= e["ms_per_step"] <= e["ms_max"], key
+    assert "power" in line and "host" in line
+
+
+def test_serialize_trims_optional_parts_before_the_suite():
+    line = _full_line()
+    line["power"] = {f"k{i}": "x" * 100 for i in range(100)}  # 10 KB of padding
+    text = bench.serialize_line(line)
+    import json
+    parsed = json.loads(text)
+    assert len(text) < 8192 and "power" not in parsed
+    assert all("cpu_baseline" in e for e in parsed["suite"].values())
+
+
+def test_median_of_replays():
+    assert bench._median([3.0, 1.0, 2.0]) == 2.0
+    assert bench._median([4.0, 1.0, 2.0, 3.0]) == 2.5
+    assert bench._sig(1234.5678, 4) == 1235 and bench._sig(0.000123456, 3) == 0.000123
