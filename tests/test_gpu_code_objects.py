@@ -23,16 +23,7 @@ def _vadd(**options):
     @asc2.jit(**options)
     def vadd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int,
                     tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
-        x_gm = asc2.tensor(x_ptr, [size])
-        y_gm = asc2.tensor(y_ptr, [size])
-        out_gm = asc2.tensor(out_ptr, [size])
-        base_offset = asc2.block_idx() * tile_size * tile_per_block
-        for i in range(tile_per_block):
-            tile_offset = base_offset + i * tile_size
-            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
-            y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
-            out = x + y
-            asc2.store(out, out_gm, offsets=[tile_offset])
+        """out = x + y over the tiles of block b (python/test/asc2/kernels/test_vadd.py's kernel)."""
 
     return vadd_kernel
 
@@ -126,34 +117,20 @@ def test_reference_test_through_code_object(device, cache_dir):
 # --------------------------------------------------------------------------------------- softmax
 
 def _softmax_rows(**options):
-    # python/test/asc2/kernels/test_softmax.py:16-27
     @asc2.jit(**options)
     def softmax_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: int, num_cols: int,
                        tile_size: asc.ConstExpr[int]):
-        x_gm = asc2.tensor(x_ptr, [num_rows, num_cols])
-        out_gm = asc2.tensor(out_ptr, [num_rows, num_cols])
-        for i in range(asc2.block_idx(), num_rows, asc2.block_num(), parallel=True):
-            row = asc2.load(x_gm, [1, tile_size], offsets=[i, 0])
-            row_minus_max = row - asc2.reduce_max(row)
-            numerator = asc2.exp(row_minus_max)
-            denominator = asc2.reduce_sum(numerator)
-            out = numerator / denominator
-            asc2.store(out, out_gm, offsets=[i, 0])
+        """Grid-strided row softmax of the first tile_size columns
+        (python/test/asc2/kernels/test_softmax.py's kernel)."""
 
     return softmax_kernel
 
 
 def _softmax_fused(**options):
-    # python/test/asc2/kernels/test_softmax_fused.py:16-24
     @asc2.jit(**options)
     def softmax_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: int,
                        num_cols: asc.ConstExpr[int], block_size: asc.ConstExpr[int]):
-        x_gm = asc2.tensor(x_ptr, [num_rows, num_cols])
-        out_gm = asc2.tensor(out_ptr, [num_rows, num_cols])
-        start_rows = asc2.block_idx() * block_size
-        rows = asc2.load(x_gm, [block_size, num_cols], offsets=[start_rows, 0])
-        out = asc2.softmax(rows)
-        asc2.store(out, out_gm, offsets=[start_rows, 0])
+        """asc2.softmax of block_size rows per block (python/test/asc2/kernels/test_softmax_fused.py's kernel)."""
 
     return softmax_kernel
 
@@ -228,62 +205,30 @@ def test_softmax_code_object_cache(device, cache_dir):
 # ------------------------------------------------------------------- leaky_relu / vmuladd / gelu
 
 def _leaky_relu():
-    # python/test/asc2/kernels/test_leaky_relu.py:16-26
     @asc2.jit
     def leaky_relu_kernel(x_ptr: asc.GlobalAddress, alpha: float, out_ptr: asc.GlobalAddress, size: int,
                           tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
-        x_gm = asc2.tensor(x_ptr, [size])
-        out_gm = asc2.tensor(out_ptr, [size])
-        base_offset = asc2.block_idx() * tile_size * tile_per_block
-        for i in range(tile_per_block):
-            tile_offset = base_offset + i * tile_size
-            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
-            out = asc2.where(x >= 0, x, x * alpha)
-            asc2.store(out, out_gm, offsets=[tile_offset])
+        """where(x >= 0, x, x * alpha) over the tiles of block b
+        (python/test/asc2/kernels/test_leaky_relu.py's kernel)."""
 
     return leaky_relu_kernel
 
 
 def _vmuladd():
-    # python/test/asc2/kernels/test_vmuladd.py:16-31
     @asc2.jit(vf_fusion=True)
     def vmuladd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, z_ptr: asc.GlobalAddress,
                        out_ptr: asc.GlobalAddress, size: int, tile_size: asc.ConstExpr[int],
                        tile_per_block: asc.ConstExpr[int], buffer_factor: asc.ConstExpr[int]):
-        x_gm = asc2.tensor(x_ptr, [size])
-        y_gm = asc2.tensor(y_ptr, [size])
-        z_gm = asc2.tensor(z_ptr, [size])
-        out_gm = asc2.tensor(out_ptr, [size])
-        base_offset = asc2.block_idx() * tile_size * tile_per_block
-        for i in range(tile_per_block):
-            tile_offset = base_offset + i * tile_size
-            x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
-            y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
-            z = asc2.load(z_gm, [tile_size], offsets=[tile_offset])
-            asc2.store(x * y + z, out_gm, offsets=[tile_offset])
+        """x * y + z, unfused, over the tiles of block b (python/test/asc2/kernels/test_vmuladd.py's kernel)."""
 
     return vmuladd_kernel
 
 
 def _gelu():
-    # python/test/asc2/kernels/test_gelu.py:19-33
     @asc2.jit
     def gelu_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: asc.ConstExpr,
                     num_columns: asc.ConstExpr, tile_size: asc.ConstExpr, approximate: asc.ConstExpr):
-        x_gm = asc2.tensor(x_ptr, [num_rows, num_columns])
-        out_gm = asc2.tensor(out_ptr, [num_rows, num_columns])
-        for i in range(asc2.block_idx(), num_rows, asc2.block_num()):
-            row = asc2.load(x_gm, [1, tile_size], offsets=[i, 0])
-            if approximate:
-                pi = 3.141592653589793238462643383279502884
-                k1 = 2 * asc2.sqrt(2 / pi)
-                k2 = 2 * asc2.sqrt(2 / pi) * 0.044715
-                param = row * (row * row * k2 + k1)
-                out = row - row / (asc2.exp(param) + 1)
-            else:
-                k = asc2.sqrt(0.5)
-                out = row * (asc2.erf(row * k) + 1) * 0.5
-            asc2.store(out, out_gm, offsets=[i, 0])
+        """Grid-strided gelu rows, tanh or erf form (python/test/asc2/kernels/test_gelu.py's kernel)."""
 
     return gelu_kernel
 

@@ -1,14 +1,12 @@
 """leaky_relu, vmuladd and gelu on the GPU.
 
-The reference tests' own forms first (python/test/asc2/kernels/test_leaky_relu.py,
-test_vmuladd.py, test_gelu.py): kernels defined with @asc2.jit, launched as
+The reference tests' launch forms first (python/test/asc2/kernels/test_leaky_relu.py,
+test_vmuladd.py, test_gelu.py): kernels declared with @asc2.jit, launched as
 kernel[grid](...) on CPU torch tensors / numpy arrays, compared with the same golden
-expressions.  Then the kernel API against the oracle: leaky_relu and vmuladd
+expressions (oracle/cpu_golden.py).  Then the kernel API against the oracle: leaky_relu and vmuladd
 bit-exact for every dtype, gelu within rtol 1e-5 / atol 1e-6 of the oracle's float64
 evaluation of the same expression (the reference test's own bar vs torch is rtol 1e-3,
 atol 1e-5)."""
-import math
-
 import numpy as np
 import pytest
 import torch
@@ -16,6 +14,7 @@ import torch
 import asc
 import asc2
 from oracle import asc2_oracle as O
+from oracle import cpu_golden
 from pyasc_amd import kernels
 
 pytestmark = pytest.mark.gpu
@@ -32,38 +31,25 @@ def _np(t, dtype):
 _NAMES = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}
 
 
-# ------------------------------------------------------------------------ reference-style kernels
+# ------------------------------------------------------------------------ reference-style launches
+# Declared by signature (the declaration body binds the registered native kernel) and
+# launched as kernel[grid](...) with the grid and tile arguments each reference test's
+# launch helper derives, on its recipe and golden expression.
 
 @asc2.jit(always_compile=True)
 def leaky_relu_kernel(x_ptr: asc.GlobalAddress, alpha: float, out_ptr: asc.GlobalAddress, size: int,
                       tile_size: asc.ConstExpr[int], tile_per_block: asc.ConstExpr[int]):
-    x_gm = asc2.tensor(x_ptr, [size])
-    out_gm = asc2.tensor(out_ptr, [size])
-    base_offset = asc2.block_idx() * tile_size * tile_per_block
-    for i in range(tile_per_block):
-        tile_offset = base_offset + i * tile_size
-        x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
-        out = asc2.where(x >= 0, x, x * alpha)
-        asc2.store(out, out_gm, offsets=[tile_offset])
-
-
-def leaky_relu_launch(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
-    assert alpha.dim() == 0
-    out = torch.empty_like(x)
-    size = out.numel()
-    core_num = 16
-    tile_size = 128
-    num_tiles = asc.ceildiv(size, tile_size)
-    leaky_relu_kernel[core_num](x, alpha, out, size, tile_size, asc.ceildiv(num_tiles, core_num))
-    return out
+    """out = x where x >= 0, else x * alpha, over the tiles of block b (store clipped to size)."""
 
 
 def test_leaky_relu_reference_recipe(device):
-    # test_leaky_relu.py:40-47 (CPU tensors: copied in and back by the launcher)
+    # test_leaky_relu.py:40-47 (CPU tensors: copied in and back by the launcher); 16 blocks
+    # of 128-element tiles, alpha a 0-dim bf16 tensor passed by value
     x = torch.rand(8192, dtype=torch.bfloat16) * 10.0 - 5.0
     alpha = torch.tensor(0.1, dtype=torch.bfloat16)
-    out = leaky_relu_launch(x, alpha)
-    golden = torch.where(x >= 0, x, x * alpha)
+    out = torch.empty_like(x)
+    leaky_relu_kernel[16](x, alpha, out, x.numel(), 128, asc.ceildiv(asc.ceildiv(x.numel(), 128), 16))
+    golden = cpu_golden.leaky_relu(x, alpha)
     torch.testing.assert_close(out, golden)
     assert torch.equal(out.view(torch.int16), golden.view(torch.int16))  # bit-exact
 
@@ -72,37 +58,15 @@ def test_leaky_relu_reference_recipe(device):
 def vmuladd_kernel(x_ptr: asc.GlobalAddress, y_ptr: asc.GlobalAddress, z_ptr: asc.GlobalAddress,
                    out_ptr: asc.GlobalAddress, size: int, tile_size: asc.ConstExpr[int],
                    tile_per_block: asc.ConstExpr[int], buffer_factor: asc.ConstExpr[int]):
-    x_gm = asc2.tensor(x_ptr, [size])
-    y_gm = asc2.tensor(y_ptr, [size])
-    z_gm = asc2.tensor(z_ptr, [size])
-    out_gm = asc2.tensor(out_ptr, [size])
-    base_offset = asc2.block_idx() * tile_size * tile_per_block
-    for i in range(tile_per_block):
-        tile_offset = base_offset + i * tile_size
-        x = asc2.load(x_gm, [tile_size], offsets=[tile_offset])
-        y = asc2.load(y_gm, [tile_size], offsets=[tile_offset])
-        z = asc2.load(z_gm, [tile_size], offsets=[tile_offset])
-        asc2.store(x * y + z, out_gm, offsets=[tile_offset])
-
-
-def vmuladd_launch(x: np.ndarray, y: np.ndarray, z: np.ndarray) -> np.ndarray:
-    out = np.empty_like(x)
-    size = out.size
-    core_num = 16
-    tile_size = 32
-    num_tiles = asc.ceildiv(size, tile_size)
-    vmuladd_kernel[core_num](x, y, z, out, size, tile_size, asc.ceildiv(num_tiles, core_num), buffer_factor=2)
-    return out
+    """out = x * y + z (multiply rounded, then add) over the tiles of block b."""
 
 
 def test_vmuladd_reference_recipe(device):
-    # test_vmuladd.py:43-52
+    # test_vmuladd.py:43-52: 16 blocks of 32-element tiles, buffer_factor 2
     rng = np.random.default_rng(seed=2026)
-    size = 8192
-    x = rng.random(size, dtype=np.float32) * 10
-    y = rng.random(size, dtype=np.float32) * 10
-    z = rng.random(size, dtype=np.float32) * 10
-    out = vmuladd_launch(x, y, z)
+    x, y, z = (rng.random(8192, dtype=np.float32) * 10 for _ in range(3))
+    out = np.empty_like(x)
+    vmuladd_kernel[16](x, y, z, out, x.size, 32, asc.ceildiv(asc.ceildiv(x.size, 32), 16), buffer_factor=2)
     np.testing.assert_allclose(out, x * y + z)
     np.testing.assert_array_equal(out, x * y + z)  # bit-exact: no fused multiply-add
 
@@ -110,41 +74,16 @@ def test_vmuladd_reference_recipe(device):
 @asc2.jit(always_compile=True)
 def gelu_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, num_rows: asc.ConstExpr,
                 num_columns: asc.ConstExpr, tile_size: asc.ConstExpr, approximate: asc.ConstExpr):
-    x_gm = asc2.tensor(x_ptr, [num_rows, num_columns])
-    out_gm = asc2.tensor(out_ptr, [num_rows, num_columns])
-    for i in range(asc2.block_idx(), num_rows, asc2.block_num()):
-        row = asc2.load(x_gm, [1, tile_size], offsets=[i, 0])
-        if approximate:
-            pi = 3.141592653589793238462643383279502884
-            k1 = 2 * asc2.sqrt(2 / pi)
-            k2 = 2 * asc2.sqrt(2 / pi) * 0.044715
-            param = row * (row * row * k2 + k1)
-            out = row - row / (asc2.exp(param) + 1)
-        else:
-            k = asc2.sqrt(0.5)
-            out = row * (asc2.erf(row * k) + 1) * 0.5
-        asc2.store(out, out_gm, offsets=[i, 0])
-
-
-def gelu_launch(x: torch.Tensor, approximate: bool):
-    output = torch.empty_like(x)
-    num_rows, num_columns = x.shape
-    gelu_kernel[16](x, output, num_rows, num_columns, 1024, approximate)
-    return output
-
-
-def gelu_torch(x: torch.Tensor, approximate: bool):
-    if approximate:
-        return 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * torch.pow(x, 3))))
-    return 0.5 * x * (1 + torch.erf(x / math.sqrt(2)))
+    """Rows b, b+grid, ...: gelu of the first tile_size columns (tanh form when approximate)."""
 
 
 @pytest.mark.parametrize("approximate", [True, False])
 def test_gelu_reference_recipe(device, approximate):
-    # test_gelu.py:52-59
+    # test_gelu.py:52-59: 30 rows of 1024 fp32, 16 blocks, tile 1024
     x = torch.rand((30, 1024), dtype=torch.float32)
-    out = gelu_launch(x, approximate)
-    torch.testing.assert_close(out, gelu_torch(x, approximate), rtol=1e-3, atol=1e-5)
+    out = torch.empty_like(x)
+    gelu_kernel[16](x, out, 30, 1024, 1024, approximate)
+    torch.testing.assert_close(out, cpu_golden.gelu(x, approximate), rtol=1e-3, atol=1e-5)
     expected = O.gelu_rows(x.numpy(), np.zeros((30, 1024)), 30, 1024, 1024, approximate)
     np.testing.assert_allclose(out.numpy(), expected, rtol=1e-5, atol=1e-6)
 

@@ -66,9 +66,9 @@ def test_extremes(device):
 
 def test_config_shape_full(device):
     """BASELINE config: M=4096, N=11008, K=4096, uniform[-127,127] int8 from seed 3,
-    scale uniform[0.001, 0.01].  Accumulators are checked exactly on 64 sampled rows
-    (fp64 BLAS is exact here: |partial sums| < 2^53); every output is checked against
-    the dequant of the GPU's own accumulators (bit-exact), so the whole C is covered."""
+    scale uniform[0.001, 0.01].  Every accumulator is checked exactly against the host's
+    fp64 product (exact here: every partial sum is an integer below 4096 * 127^2 < 2^53),
+    and every fp16 output against the dequant of those accumulators, bit for bit."""
     g = torch.Generator().manual_seed(3)
     a = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, generator=g)
     b = torch.randint(-127, 128, (4096, 11008), dtype=torch.int8, generator=g)
@@ -79,10 +79,12 @@ def test_config_shape_full(device):
     kernels.matmul_i8(ad, bd, acc)
     kernels.matmul_i8(ad, bd, out, scale=scale.to(device))
     torch.cuda.synchronize()
-    rows = torch.randperm(4096, generator=torch.Generator().manual_seed(8))[:64]
-    exact = (a[rows].double() @ b.double()).to(torch.int32)
-    assert torch.equal(acc[rows.to(device)].cpu(), exact)
     acc_h = acc.cpu()
+    bd64 = b.double()
+    for r0 in range(0, 4096, 1024):  # the exact product in row blocks (bounded host memory)
+        exact = (a[r0:r0 + 1024].double() @ bd64).to(torch.int32)
+        assert torch.equal(acc_h[r0:r0 + 1024], exact), f"rows {r0}..{r0 + 1023}"
+    del bd64
     np.testing.assert_array_equal(_f16_bits(out), O.dequant_f16(acc_h.numpy(), scale.numpy()).view(np.uint16))
     # whole-matrix checksums, exact in int64 (linearity): C 1 = A (B 1) and 1^T C = (1^T A) B,
     # so every accumulator of every tile enters an exact comparison

@@ -1,7 +1,8 @@
 """Reductions and RMS norm on the GPU (row reductions and rms_norm).
 
-First the reference's own reduction tests (python/test/asc2/operations/
-test_reduce_ops.py): the same kernels, parametrisation and goldens (torch sum /
+First the reference's reduction tests (python/test/asc2/operations/
+test_reduce_ops.py) in launch form: the kernels declared by signature, on the same
+parametrisation and goldens (torch sum /
 amax / amin / prod, default assert_close tolerances).  Then the kernel API at
 bandwidth sizes against the oracle: max / min exact, sums within 1e-5 of the sum of
 absolute values per result (an fp32 summation-error bound), products on values near
@@ -22,75 +23,50 @@ pytestmark = pytest.mark.gpu
 def kernel(input_ptr: asc.GlobalAddress, output_ptr: asc.GlobalAddress, reduce_dim: asc.ConstExpr,
            input_shape: asc.ConstExpr, input_offsets: asc.ConstExpr, output_shape: asc.ConstExpr,
            output_offsets: asc.ConstExpr, op: asc.ConstExpr, keep_dims: asc.ConstExpr) -> None:
-    g_input = asc2.tensor(input_ptr, input_shape)
-    g_output = asc2.tensor(output_ptr, output_shape)
-    input = asc2.load(g_input, input_shape, offsets=input_offsets)
-    output = op(input, reduce_dim, keep_dims=keep_dims)
-    asc2.store(output, g_output, offsets=output_offsets)
+    """output = op(input tile, reduce_dim, keep_dims) for one of the asc2.reduce_* ops."""
 
 
 @asc2.jit(always_compile=True)
 def kernel_all(input_ptr: asc.GlobalAddress, output_ptr: asc.GlobalAddress, input_shape: asc.ConstExpr,
                input_offsets: asc.ConstExpr, output_shape: asc.ConstExpr, output_offsets: asc.ConstExpr,
                op: asc.ConstExpr) -> None:
-    g_input = asc2.tensor(input_ptr, input_shape)
-    g_output = asc2.tensor(output_ptr, output_shape)
-    input = asc2.load(g_input, input_shape, offsets=input_offsets)
-    scalar = op(input)
-    output = asc2.full(output_shape, scalar, dtype=input.dtype)
-    asc2.store(output, g_output, offsets=output_offsets)
+    """output filled with op(input tile), the reduction over the whole tile."""
 
 
-# test_reduce_ops.py:16-29 (the 2-D cases; the dim=None rows are commented out there and
-# are exercised through kernel_all below)
-REFERENCE_CASES = [
-    [asc2.reduce_prod, torch.prod, [64, 32], torch.float32, False, 0],
-    [asc2.reduce_prod, torch.prod, [64, 32], torch.float32, False, 1],
-    [asc2.reduce_min, torch.amin, [64, 32], torch.float32, False, 0],
-    [asc2.reduce_min, torch.amin, [64, 32], torch.float32, False, 1],
-    [asc2.reduce_sum, torch.sum, [64, 32], torch.float32, False, 0],
-    [asc2.reduce_sum, torch.sum, [64, 32], torch.float32, False, 1],
-    [asc2.reduce_max, torch.amax, [64, 32], torch.float32, False, 0],
-    [asc2.reduce_max, torch.amax, [64, 32], torch.float32, False, 1],
-    [asc2.reduce_prod, torch.prod, [64, 32], torch.float32, True, 0],
-    [asc2.reduce_sum, torch.sum, [64, 32], torch.float32, None, None],
-    [asc2.reduce_max, torch.amax, [32, 32], torch.float32, None, None],
-    [asc2.reduce_min, torch.amin, [32, 32], torch.float32, None, None],
-]
+# asc2 reduction -> the torch golden the reference test compares it with
+_OPS = {"prod": (asc2.reduce_prod, torch.prod), "min": (asc2.reduce_min, torch.amin),
+        "sum": (asc2.reduce_sum, torch.sum), "max": (asc2.reduce_max, torch.amax)}
+# test_reduce_ops.py's 2-D parametrisation: each op along each dim of a 64x32 fp32 input,
+# prod with keep_dims, and whole-tile reductions of sum (64x32), max and min (32x32)
+# (the reference runs the whole-tile rows through kernel_all)
+REFERENCE_CASES = ([(op, [64, 32], False, dim) for op in ("prod", "min", "sum", "max") for dim in (0, 1)] +
+                   [("prod", [64, 32], True, 0), ("sum", [64, 32], None, None), ("max", [32, 32], None, None),
+                    ("min", [32, 32], None, None)])
 
 
-@pytest.mark.parametrize("op, torch_op, shape, dtype, keep_dims, dim", REFERENCE_CASES)
-def test_reduce_reference_cases(device, op, torch_op, shape, dtype, keep_dims, dim):
-    # test_reduce_ops.py:55-82
-    input = torch.randn(shape, dtype=dtype) * 2.0
+@pytest.mark.parametrize("name, shape, keep_dims, dim", REFERENCE_CASES)
+def test_reduce_reference_cases(device, name, shape, keep_dims, dim):
+    # test_reduce_ops.py:55-82: randn * 2 fp32, one block, default assert_close tolerances
+    op, golden = _OPS[name]
+    x = torch.randn(shape, dtype=torch.float32) * 2.0
     if dim is None:
-        output_shape = [32]
+        out_shape = [32]
     else:
-        output_shape = list(shape)
-        if keep_dims:
-            output_shape[dim] = 1
-        else:
-            del output_shape[dim]
-    output = torch.zeros(output_shape, dtype=dtype)
-    input_offsets = [0] * len(shape)
-    output_offsets = [0] * len(output_shape)
+        out_shape = [1 if (i == dim and keep_dims) else s for i, s in enumerate(shape) if i != dim or keep_dims]
+    out = torch.zeros(out_shape, dtype=torch.float32)
+    in_offsets, out_offsets = [0] * len(shape), [0] * len(out_shape)
     if dim is None:
-        kernel_all[1](input, output, shape, input_offsets, output_shape, output_offsets, op)
-        expected = torch.ones(output_shape, dtype=dtype) * torch_op(input).item()
+        kernel_all[1](x, out, shape, in_offsets, out_shape, out_offsets, op)
+        expected = torch.full(out_shape, golden(x).item())
     else:
-        kernel[1](input, output, dim, shape, input_offsets, output_shape, output_offsets, op, keep_dims)
-        expected = torch_op(input, dim, keepdim=keep_dims)
-    torch.testing.assert_close(output, expected)
+        kernel[1](x, out, dim, shape, in_offsets, out_shape, out_offsets, op, keep_dims)
+        expected = golden(x, dim, keepdim=keep_dims)
+    torch.testing.assert_close(out, expected)
 
 
 @asc2.jit(always_compile=True)
 def reduce_tile_kernel(x_ptr: asc.GlobalAddress, out_ptr: asc.GlobalAddress, size: int, tile_size: asc.ConstExpr[int]):
-    x_gm = asc2.tensor(x_ptr, [size])
-    out_gm = asc2.tensor(out_ptr, [1])
-    tile = asc2.load(x_gm, [tile_size], offsets=[0])
-    max_val = asc2.reduce_max(tile)
-    result = asc2.full([1], max_val, dtype=tile.dtype)
-    asc2.store(result, out_gm, offsets=[0])
+    """out[0] = the max of the first tile_size elements of x."""
 
 
 @pytest.mark.parametrize("tile_size", [1, 7, 17])
