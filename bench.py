@@ -1169,7 +1169,7 @@ def build_line(args, head, res: dict, cpu, suite: dict, extra: dict) -> dict:
         "vs_baseline": None,
         "dtype": head.dtype,
         "data": "synthetic (seeded torch generator on the device; distribution of BASELINE.json's config)",
-        "config": {k: v for k, v in head.config().items() if k != "input"},
+        "config": {k: v for k, v in res["config"].items() if k != "input"},
         "roofline": roof,
         "cpu_baseline": head_cpu,
         "timing": {"method": res["timing"], "ms_min": _sig(res["ms_min"], 5), "ms_max": _sig(res["ms_max"], 5),

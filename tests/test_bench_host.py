@@ -91,9 +91,10 @@ def _full_line():
         r["roofline"] = bench.roofline(w, r)
         r["roofline"]["traffic"] = 1234567890
         suite[key] = bench.compact_entry(r, r["roofline"], _stub_cpu(w.unit))
-    head = bench.WORKLOADS[bench.HEADLINE]()
-    head.xs = [None] * 5
+    head = bench.WORKLOADS[bench.HEADLINE]()  # not set up: the line takes the config measure() recorded
     res = _stub_result(head, 0.0230456)
+    res["config"] = {"workload": head.name, "rows": 4096, "cols": 4096, "tile_size": 4096, "grid": 16,
+                     "input": "randn*2 (N(0,4)), seed 1", "rotating_sets": 5}
     power = {k: {"value": 1234.5678, "w": 1391.0, "mhz": 1932, "frac_at_clock": 0.5702} for k in bench.POWER_WORKLOADS}
     extra = {"power": power, "launch_latency_us": {"asc2": 9.87, "asc2_always_compile": 31.2, "kernel_api": 6.5},
              "reference_published_us": {"asc1_vadd_8192_f32": [2.1, 3.6],
@@ -137,3 +138,50 @@ def test_median_of_replays():
     assert bench._median([3.0, 1.0, 2.0]) == 2.0
     assert bench._median([4.0, 1.0, 2.0, 3.0]) == 2.5
     assert bench._sig(1234.5678, 4) == 1235 and bench._sig(0.000123456, 3) == 0.000123
+
+
+def test_main_end_to_end_with_stubbed_gpu_legs(monkeypatch, capsys, tmp_path):
+    # bench.main's control flow on the CPU: every GPU leg replaced by a stub of the same
+    # return shape, the CPU baselines too; the last stdout line must be the parsed line
+    import json
+    import sys
+    import torch
+    from pyasc_amd import _native
+
+    def fake_measure(w, steps, warmup, dev, graph=True, sampler=None, warmup_s=1.0, replays=7):
+        r = _stub_result(w, 0.5)
+        r["config"] = {"workload": w.name, "input": "stub"}
+        return r
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a: None)
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda *a: None)
+    monkeypatch.setattr(_native, "load_library", lambda *a, **k: None)
+    monkeypatch.setattr(_native, "device_info", lambda *a: {"name": "stub"})
+    monkeypatch.setattr(bench, "measure", fake_measure)
+    monkeypatch.setattr(bench, "vendor", lambda w, steps, res: None)
+    monkeypatch.setattr(bench, "launch_latency", lambda dev: {"asc2_cached_us": 9.0, "asc2_always_compile_us": 30.0,
+                                                              "kernel_api_us": 6.0})
+    monkeypatch.setattr(bench, "reference_durations", lambda dev: {
+        "asc1_vadd_8192_f32": {"us_per_launch": 2.0, "reference_task_duration_us": 3.6}})
+    monkeypatch.setattr(bench, "power_phase", lambda dev, keys, steps: {
+        k: {"value": 1.0, "socket_w_median": 1400.0, "gfx_mhz_median": 1600, "frac_at_clock": 0.7} for k in keys})
+    for cls in {type(bench.WORKLOADS[k]()) for k in bench.WORKLOADS}:
+        monkeypatch.setattr(cls, "cpu_baseline", lambda self, min_total_s=2.0: _stub_cpu(self.unit))
+    detail = tmp_path / "detail.json"
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "20", "--warmup", "5", "--detail", str(detail)])
+    assert bench.main() == 0
+    out = capsys.readouterr().out.strip().splitlines()
+    assert len(out) == 1 and len(out[0]) < 8192
+    line = json.loads(out[-1])
+    assert line["steps"] == 20 and line["warmup"] == 5 and set(line["suite"]) == set(bench.SUITE) - {bench.HEADLINE}
+    assert line["config"] == {"workload": "softmax_4096x4096_f32"}
+    assert line["cpu_baseline"]["unit"] == "GB/s" and set(line["power"]) == set(bench.POWER_WORKLOADS)
+    assert json.loads(detail.read_text())["line"] == line
+
+
+def test_more_than_one_gpu_is_refused(monkeypatch, capsys):
+    import sys
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "8"])
+    assert bench.main() == 2
+    assert "one GPU only" in capsys.readouterr().err
