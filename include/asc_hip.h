@@ -44,6 +44,7 @@ typedef void* asc_stream_t; /* hipStream_t */
 #define ASC_ERR_INVALID_ARG (-1)
 #define ASC_ERR_UNSUPPORTED (-2)
 #define ASC_ERR_ALIGNMENT (-3)
+#define ASC_ERR_BUSY (-4) /* a shared resource is still in use by another stream */
 
 /* Element type codes, named after asc.language.core.dtype
  * (python/asc/language/core/dtype.py:111-124). */
@@ -314,8 +315,13 @@ int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a,
  * static device array, resident until the process ends), so M * N * 2 may not
  * exceed 33554432 bytes (ASC_ERR_UNSUPPORTED otherwise).  Nothing is allocated:
  * no hipMalloc, hipFree or allocating library call.  Every call on one GPU shares
- * that buffer: calls that overlap on one GPU (on different streams, or from
- * several threads) race on it; calls on one stream are ordered and safe. */
+ * that buffer, so the rule is: issue every call on one GPU on one stream, or order
+ * the streams (an event) so that calls do not overlap; calls on one stream are
+ * ordered and safe, calls that overlap (on different streams, or from several
+ * threads) race on the buffer.  With ASC_NOALLOC_CHECK=1 in the environment (a
+ * debugging aid; it creates one HIP event per GPU on its first checked call) a
+ * call on another stream while the previous call on that GPU is still running is
+ * refused with ASC_ERR_BUSY; streams under graph capture are not checked. */
 int32_t asc_matmul_chained_noalloc(int32_t in_dtype, int32_t out_dtype,
                                    const void* a, const void* b, void* c,
                                    int64_t M, int64_t N, int64_t K,

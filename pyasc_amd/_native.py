@@ -30,6 +30,7 @@ DT_INT16 = 5
 ERR_INVALID_ARG = -1
 ERR_UNSUPPORTED = -2
 ERR_ALIGNMENT = -3
+ERR_BUSY = -4
 
 _c_i32, _c_i64, _c_p, _c_f32, _c_f64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_double
 

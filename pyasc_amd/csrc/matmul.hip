@@ -3,6 +3,8 @@
 // python/test/asc2/kernels/test_matmul_{mnblock,tiled,fixpipe,l0c_to_l1}.py): the
 // library's entry points and the launch plan the asc2 code-object path replays.
 // The device code and the choice of kernels are described in matmul_kernels.h.
+#include <stdlib.h>
+
 #include <mutex>
 
 #include "matmul_kernels.h"
@@ -169,6 +171,31 @@ int32_t scratch_address(void** out, const char* who) {
   return ASC_OK;
 }
 
+// Optional check of the rule that calls sharing one GPU's scratch buffer must not
+// overlap (ASC_NOALLOC_CHECK=1 in the environment; a debugging aid, off by default).
+// Each checked call records a per-device event on its stream after its two launches;
+// a call on another stream while that event is still pending is refused with
+// ASC_ERR_BUSY before anything is launched.  The event is created on the device's
+// first checked call (the only allocation the check makes).  Streams under graph
+// capture are not checked: their launches run at replay.
+struct ScratchUse {
+  hipStream_t stream = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+};
+ScratchUse g_use[kMaxDevices];
+std::mutex g_use_mu;
+
+bool noalloc_check_enabled() {
+  const char* v = getenv("ASC_NOALLOC_CHECK");
+  return v != nullptr && v[0] != '\0' && !(v[0] == '0' && v[1] == '\0');
+}
+
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 }  // namespace
 
 extern "C" int32_t asc_matmul_chained_noalloc(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b,
@@ -183,7 +210,34 @@ extern "C" int32_t asc_matmul_chained_noalloc(int32_t in_dtype, int32_t out_dtyp
   void* t = nullptr;
   const int32_t rc = scratch_address(&t, who);
   if (rc != ASC_OK) return rc;
-  return chained(in_dtype, out_dtype, a, b, c, M, N, K, t, kChainedScratchBytes, stream, who);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!noalloc_check_enabled() || capturing(s)) {
+    return chained(in_dtype, out_dtype, a, b, c, M, N, K, t, kChainedScratchBytes, stream, who);
+  }
+  int dev = -1;
+  ASC_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, ASC_ERR_UNSUPPORTED,
+              "%s: no current device", who);
+  std::lock_guard<std::mutex> lock(g_use_mu);
+  ScratchUse& use = g_use[dev];
+  if (use.recorded && use.stream != s) {
+    const hipError_t q = hipEventQuery(use.done);
+    ASC_REQUIRE(q != hipErrorNotReady, ASC_ERR_BUSY,
+                "%s: the previous call on this GPU (another stream) has not finished with the shared scratch "
+                "buffer; order the streams (an event) or use one stream",
+                who);
+  }
+  if (use.done == nullptr) {
+    const hipError_t e = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
+    ASC_REQUIRE(e == hipSuccess, static_cast<int32_t>(e), "%s: hipEventCreateWithFlags failed: %s", who,
+                hipGetErrorString(e));
+  }
+  const int32_t run_rc = chained(in_dtype, out_dtype, a, b, c, M, N, K, t, kChainedScratchBytes, stream, who);
+  if (run_rc != ASC_OK) return run_rc;
+  const hipError_t e = hipEventRecord(use.done, s);
+  ASC_REQUIRE(e == hipSuccess, static_cast<int32_t>(e), "%s: hipEventRecord failed: %s", who, hipGetErrorString(e));
+  use.stream = s;
+  use.recorded = true;
+  return ASC_OK;
 }
 
 extern "C" int32_t asc_matmul_chained(int32_t in_dtype, int32_t out_dtype, const void* a, const void* b, void* c,

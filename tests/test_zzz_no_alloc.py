@@ -1,7 +1,9 @@
 """asc_matmul_chained_noalloc (the allocation-free chained matmul, intermediate in the
 library's per-GPU scratch buffer) against asc_matmul_chained (intermediate in a workspace
 the caller passes), through the C ABI: bit-identical results on two calls in a row, the
-first filling the whole 32 MiB buffer, the second smaller, with other dtypes."""
+first filling the whole 32 MiB buffer, the second smaller, with other dtypes; and the
+optional overlap check (ASC_NOALLOC_CHECK=1) refusing a call on a second stream while the
+first stream's call still uses the buffer."""
 import pytest
 import torch
 
@@ -57,3 +59,40 @@ def test_noalloc_rejects_an_intermediate_above_the_buffer(device):
     with pytest.raises(RuntimeError, match="scratch buffer"):
         _native.call("asc_matmul_chained_noalloc", _native.DT_FLOAT16, _native.DT_FLOAT16, a.data_ptr(),
                      b.data_ptr(), c.data_ptr(), 4097, 4096, 4096, torch.cuda.current_stream().cuda_stream)
+
+
+def test_noalloc_check_refuses_an_overlapping_call_on_another_stream(device, monkeypatch):
+    # ASC_NOALLOC_CHECK=1: a call on a second stream while the first stream's call still
+    # holds the scratch buffer is refused before launching anything; once the first stream
+    # has finished, the same call runs and matches the first bit for bit
+    if not hasattr(torch.cuda, "_sleep"):
+        pytest.skip("torch.cuda._sleep is not available")
+    monkeypatch.setenv("ASC_NOALLOC_CHECK", "1")
+    a, b = _inputs(256, 256, torch.bfloat16, 3, device)
+    c1 = torch.full((256, 256), float("nan"), device=device)
+    c2 = torch.full((256, 256), float("nan"), device=device)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+
+    def call(c, s):
+        _native.call("asc_matmul_chained_noalloc", _native.DT_BFLOAT16, _native.DT_FLOAT32, a.data_ptr(),
+                     b.data_ptr(), c.data_ptr(), 256, 256, 256, s.cuda_stream)
+
+    with torch.cuda.stream(s1):
+        torch.cuda._sleep(50_000_000)  # a bounded spin that keeps s1 busy while the host goes on
+    call(c1, s1)
+    with pytest.raises(RuntimeError, match="has not finished"):
+        call(c2, s2)
+    s1.synchronize()
+    call(c2, s2)
+    s2.synchronize()
+    assert not torch.isnan(c1).any()
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
+    # one stream is never refused, busy or not
+    with torch.cuda.stream(s1):
+        torch.cuda._sleep(5_000_000)
+    call(c1, s1)
+    call(c1, s1)
+    s1.synchronize()
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
