@@ -68,23 +68,17 @@ def test_closed_forms(device, D):
 @pytest.mark.parametrize("causal", [False, True])
 def test_config_shape_all_heads(device, causal):
     """BASELINE config B4 H32 S4096 D128, bf16 randn from seed 4, scale 1/sqrt(128):
-    four (batch, head) pairs are compared in full with the fp32 CPU reference, and every
-    other pair on 256 query rows spread over all query blocks (rows 16i + (b*H+h) % 16)."""
+    every (batch, head) pair is compared in full with the fp32 CPU reference (about
+    1.1 TFLOP of host work, a few seconds on the box's cores)."""
     B, H, S, D = 4, 32, 4096, 128
     g = torch.Generator().manual_seed(4)
     q, k, v = [torch.randn(B, H, S, D, generator=g).to(torch.bfloat16) for _ in range(3)]
     out, _ = _run(q, k, v, 1 / math.sqrt(D), causal, device)
     assert torch.isfinite(out.float()).all()
-    full = {(0, 0), (1, 7), (2, 19), (3, 31)}
     for b in range(B):
         for hh in range(H):
-            if (b, hh) in full:
-                ref = cpu_golden.attention(q[b, hh], k[b, hh], v[b, hh], 1 / math.sqrt(D), causal)
-                torch.testing.assert_close(out[b, hh].float(), ref, atol=TOL, rtol=TOL)
-            else:
-                rows = torch.arange(0, S, 16) + (b * H + hh) % 16
-                ref = cpu_golden.attention(q[b, hh], k[b, hh], v[b, hh], 1 / math.sqrt(D), causal, rows=rows)
-                torch.testing.assert_close(out[b, hh][rows].float(), ref, atol=TOL, rtol=TOL)
+            ref = cpu_golden.attention(q[b, hh], k[b, hh], v[b, hh], 1 / math.sqrt(D), causal)
+            torch.testing.assert_close(out[b, hh].float(), ref, atol=TOL, rtol=TOL, msg=lambda m: f"({b}, {hh}): {m}")
 
 
 @pytest.mark.parametrize("causal", [False, True])
