@@ -1213,6 +1213,8 @@ def main() -> int:
     ap.add_argument("--no-power", action="store_true",
                     help="skip the power phase (with the suite: socket power and graphics clock sampled with "
                          "amd-smi during about 3 s of launches of the headline and of each MFMA workload)")
+    ap.add_argument("--warmup-s", type=float, default=WARMUP_S,
+                    help="least seconds of warm-up replays per workload (default %(default)s; 0 for profiler runs)")
     ap.add_argument("--detail", metavar="FILE",
                     help="also write every figure in full (configs, CPU samples, vendor comparisons, power "
                          "readings, launch latency) to FILE as JSON")
@@ -1235,7 +1237,7 @@ def main() -> int:
 
     # GPU legs first, back to back: the headline, the suite, the power phase, launch costs
     head = WORKLOADS[args.workload]()
-    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph)
+    res = measure(head, args.steps, args.warmup, dev, graph=not args.no_graph, warmup_s=args.warmup_s)
     head_vendor = None if args.no_vendor else vendor(head, args.steps, res)
     print(f"bench: {head.name} {res['value']:.2f} {head.unit} (replays {res['ms_min'] * 1e3:.2f}-"
           f"{res['ms_max'] * 1e3:.2f} us/step)", file=sys.stderr, flush=True)
@@ -1246,7 +1248,7 @@ def main() -> int:
     keys = [] if args.no_suite else [k for k in SUITE if k != args.workload]
     for key in keys:
         w = WORKLOADS[key]()
-        r = measure(w, args.steps, args.warmup, dev, graph=not args.no_graph,
+        r = measure(w, args.steps, args.warmup, dev, graph=not args.no_graph, warmup_s=args.warmup_s,
                     replays=REPLAYS if w.bound != "latency" else 3 * REPLAYS)
         r["roofline"] = roofline(w, r)
         r["vendor"] = None if args.no_vendor else vendor(w, args.steps, r)

@@ -3,20 +3,25 @@
     python profile_summary.py traffic DIR   # FETCH_SIZE / WRITE_SIZE passes -> profiles/traffic.json + hbm_traffic.md
     python profile_summary.py mfma DIR      # MFMA-busy / clock passes -> profiles/mfma_counters.md
     python profile_summary.py trace DIR     # kernel traces -> profiles/kernel_trace_suite.md
+    python profile_summary.py ea DIR        # L2 read-miss requests by destination -> profiles/l2_miss_destinations.md
 
 DIR holds one rocprofv3 output folder per pass, written with ``-f csv -o run`` by
 the commands the summaries print:
 
   traffic: DIR/<workload>_FETCH_SIZE and DIR/<workload>_WRITE_SIZE, from
       rocprofv3 --pmc FETCH_SIZE -f csv -d DIR/<workload>_FETCH_SIZE -o run -- \
-          python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --copy-calibration
+          python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --warmup-s 0 --copy-calibration
   trace: DIR/<workload>_TRACE and the bench's output in DIR/<workload>_TRACE.log, from
       rocprofv3 --kernel-trace --stats -f csv -d DIR/<workload>_TRACE -o run -- \
           python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 20 --warmup 3 > DIR/<workload>_TRACE.log
   mfma: DIR/<workload>_MFMA, from
       rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv \
           -d DIR/<workload>_MFMA -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 \
-          --warmup 1
+          --warmup 1 --warmup-s 0
+  ea: DIR/<workload>_EA, from
+      rocprofv3 --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_DRAM_sum TCC_EA0_RDREQ_32B_sum -f csv -d DIR/<workload>_EA \
+          -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 \
+          --warmup-s 0 --copy-calibration
 
 FETCH_SIZE and WRITE_SIZE are KiB per dispatch past the L2.  ``--copy-calibration``
 adds five torch device copies of exactly 256 MiB; their readings give the factor that
@@ -142,9 +147,9 @@ def _write_traffic_md(table: dict) -> None:
         "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
         "```",
         "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc/${W}_FETCH_SIZE -o run -- python3 bench.py "
-        "--workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --copy-calibration",
+        "--workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --warmup-s 0 --copy-calibration",
         "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc/${W}_WRITE_SIZE -o run -- python3 bench.py "
-        "--workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --copy-calibration",
+        "--workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --warmup-s 0 --copy-calibration",
         "```", "",
         "`FETCH_SIZE` and `WRITE_SIZE` count the bytes that pass the L2 (misses and write-backs, including "
         "those the 256 MiB MALL then serves), so for kernels with operand reuse (the GEMMs) they bound HBM "
@@ -183,7 +188,7 @@ def mfma(folder: str) -> int:
         "```",
         "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE --kernel-trace -f csv "
         "-d gpurun_out/pmc/${W}_MFMA -o run -- python3 bench.py --workload $W --no-suite --no-cpu --no-vendor --steps 5 "
-        "--warmup 1",
+        "--warmup 1 --warmup-s 0",
         "```", "",
         f"Device: {info}.  `SQ_VALU_MFMA_BUSY_CYCLES` is summed over all SIMDs; `GRBM_GUI_ACTIVE` over the "
         "XCDs, so cycles per XCD = GRBM_GUI_ACTIVE / XCDs.  clock = cycles per XCD / dispatch duration "
@@ -243,9 +248,10 @@ def trace(folder: str) -> int:
         "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof/${W}_TRACE -o run -- python3 bench.py "
         "--workload $W --no-suite --no-cpu --no-vendor --steps 20 --warmup 3 > gpurun_out/prof/${W}_TRACE.log",
         "```", "",
-        "Durations in microseconds: average, minimum and maximum of the timed replay's dispatches "
-        "(Start/End timestamps), the bench's figure for the same replay (HIP events around the graph "
-        "replay on the launch stream, divided by the launches) and the bench's value computed from it.", "",
+        "Durations in microseconds: average, minimum and maximum of the last timed replay's dispatches "
+        "(Start/End timestamps), the bench's figure (HIP events around each graph replay on the launch "
+        "stream, the median of its seven timed replays divided by the launches) and the bench's value "
+        "computed from it.", "",
         "| Workload | Kernel | timed dispatches | avg us | min | max | bench events us | trace / events | "
         "bench value |",
         "|---|---|---:|---:|---:|---:|---:|---:|---:|",
@@ -275,12 +281,78 @@ def trace(folder: str) -> int:
         durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in timed]
         names = sorted({_short(r["Kernel_Name"]) for r in timed})
         per_step = sum(durs) / steps
-        ev = res["kernel_ms"] * 1e3
+        ev = res.get("kernel_ms", res["ms_per_step"]) * 1e3  # the bench's median replay / launches
         lines.append(f"| `{w.name}` | {', '.join(f'`{n}`' for n in names)} | {len(durs)} | {per_step:.2f} | "
                      f"{min(durs):.2f} | {max(durs):.2f} | {ev:.2f} | {per_step / ev:.3f} | "
                      f"{res['value']:.4g} {res['unit']} |")
         print(lines[-1])
     with open(os.path.join(PROFILES, "kernel_trace_suite.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    return 0
+
+
+def ea(folder: str) -> int:
+    """L2 read misses by destination for the MFMA workloads: TCC_EA0_RDREQ (every read
+    request the L2s send out) against TCC_EA0_RDREQ_DRAM (those destined for DRAM, i.e.
+    the memory controllers, in front of which the MALL sits), with the 256 MiB
+    calibration copies giving the bytes per request; and the floor the GEMMs' tile walk
+    sets on those reads."""
+    lines = [
+        "# L2 read misses by destination (rocprofv3 PMC), one MI355X", "",
+        "Generated by `python profile_summary.py ea DIR` from one counter pass per workload "
+        "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
+        "```",
+        "rocprofv3 --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_DRAM_sum TCC_EA0_RDREQ_32B_sum -f csv "
+        "-d gpurun_out/pmc/${W}_EA -o run -- python3 bench.py --workload $W --no-suite --no-cpu --no-vendor "
+        "--steps 5 --warmup 1 --warmup-s 0 --copy-calibration",
+        "```", "",
+        "`TCC_EA0_RDREQ_sum` counts the read requests the L2s send to the data fabric, "
+        "`TCC_EA0_RDREQ_DRAM_sum` those destined for DRAM (the memory controllers; the 256 MiB MALL, AMD "
+        "Infinity Cache, sits in front of them on the memory side), `TCC_EA0_RDREQ_32B_sum` the 32-byte "
+        "ones.  The calibration copy reads exactly 256 MiB; its request count gives the bytes per "
+        "request.  `rocprofv3 --list-avail` on this image offers no MALL or memory-controller counter, so "
+        "reads the MALL serves and reads that reach HBM cannot be told apart: every L2 read miss is "
+        "destined for DRAM, and the MALL's share is not observable here.", "",
+        "The floor column is what the GEMMs' tile walk cannot go below: each XCD runs 32 workgroups of "
+        "256x256 output tiles at once, in groups of 8 tile-rows x 4 tile-columns, so every round streams "
+        "8 A panels and 4 B panels (256 rows or columns x K) through that XCD's 4 MB L2 once; a panel "
+        "(4 MiB for bf16 at K = 8192, 1 MiB for int8 at K = 4096) does not fit the L2 twice over, so no "
+        "round reuses the previous one's panels.  Any 32 tiles need at least 12 distinct panels (r + c "
+        "with r x c = 32).  Floor = XCDs x rounds x 12 panels.", "",
+        "| Workload | Kernel | RDREQ | RDREQ_DRAM | 32B | bytes per request (copy) | L2 read misses MB | "
+        "A+B MB | misses / (A+B) | tile-walk floor MB |",
+        "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for key, make in bench.WORKLOADS.items():
+        d = os.path.join(folder, f"{key}_EA")
+        if not os.path.isdir(d):
+            continue
+        w = make()
+        vals = {c: _per_kernel(d, c) for c in ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_DRAM_sum",
+                                              "TCC_EA0_RDREQ_32B_sum")}
+        avg = {}
+        for c, per in vals.items():
+            lib = {k: v for k, v in per.items() if _is_library_kernel(k) and w.kernel_hint in k}
+            copy = [v for k, v in per.items() if "copyBuffer" in k]
+            if len(lib) != 1 or len(copy) != 1:
+                raise RuntimeError(f"{d}: expected one library kernel and the calibration copy for {c}")
+            (kname, kv), = lib.items()
+            avg[c] = (sum(kv) / len(kv), sum(copy[0]) / len(copy[0]), _short(kname))
+        req, copy_req, kname = avg["TCC_EA0_RDREQ_sum"]
+        per_req = COPY_KIB * 1024 / copy_req
+        miss = req * per_req
+        if isinstance(w, bench.Matmul):
+            ab, panel, tiles = 2 * 2 * w.n * w.n, 256 * w.n * 2, (w.n // 256) ** 2
+        elif isinstance(w, bench.MatmulI8):
+            ab, panel, tiles = w.M * w.K + w.K * w.N, 256 * w.K, (w.M // 256) * (w.N // 256)
+        else:
+            ab, panel, tiles = 3 * w.B * w.H * w.S * w.D * 2, None, None
+        floor = f"{8 * (tiles / 256) * 12 * panel / 1e6:.0f}" if panel else "-"
+        lines.append(f"| `{w.name}` | `{kname}` | {req:.0f} | {avg['TCC_EA0_RDREQ_DRAM_sum'][0]:.0f} | "
+                     f"{avg['TCC_EA0_RDREQ_32B_sum'][0]:.0f} | {per_req:.0f} | {miss / 1e6:.1f} | {ab / 1e6:.1f} | "
+                     f"{miss / ab:.2f} | {floor} |")
+        print(lines[-1])
+    with open(os.path.join(PROFILES, "l2_miss_destinations.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     return 0
 
@@ -307,7 +379,7 @@ def device_shape(folder: str):
 
 
 def main(argv) -> int:
-    modes = {"traffic": traffic, "mfma": mfma, "trace": trace}
+    modes = {"traffic": traffic, "mfma": mfma, "trace": trace, "ea": ea}
     if len(argv) != 3 or argv[1] not in modes:
         print(__doc__, file=sys.stderr)
         return 2
