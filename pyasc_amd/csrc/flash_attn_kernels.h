@@ -255,6 +255,63 @@ struct FaState {
     }
   }
 
+  // Probability iteration i (0..15) of query block qb: the two values of registers
+  // 8u + 2w and 8u + 2w + 1 of score block kb (i = 8kb + 4u + w), as in probs.
+  __device__ __forceinline__ void prob_pair(int qb, int i, const f32x16 (&sp)[2], float neg_m, u32x4 (&pb)[2][2],
+                                            float& rs) const {
+    const int kb = i >> 3, u = (i >> 2) & 1, w = i & 3;
+    const float e0 = __builtin_amdgcn_exp2f(fmaf(sp[kb][8 * u + 2 * w], scale_log2, neg_m));
+    const float e1 = __builtin_amdgcn_exp2f(fmaf(sp[kb][8 * u + 2 * w + 1], scale_log2, neg_m));
+    rs += e0;
+    rs += e1;
+    pb[kb][u][w] = pack_bf16(e0, e1);
+  }
+
+  // The clean step's two streams in one: S^T = K Q^T of the next tile (into s, as
+  // scores) and the probabilities of this tile (from sp, as probs, sums into rs), with
+  // the probability iterations spread between the MFMAs (kPer after each K operand's
+  // MFMAs).  Each chunk (operand wait, MFMAs, exp2 work, next operand read) is pinned
+  // with a scheduling barrier, so the wave issues its exp2 work while its MFMAs run
+  // instead of before them.  Values and summation order are those of probs and scores.
+  __device__ __forceinline__ void scores_probs(const uint8_t* ks_, f32x16 (&s)[QB][2], const f32x16 (&sp)[QB][2],
+                                               u32x4 (&pb)[QB][2][2], float (&rs)[QB]) const {
+    const uint32_t base = lds_addr(ks_);
+    constexpr int kWin = 4;
+    constexpr int kReads = 2 * kKSteps;
+    constexpr int kIters = 16 * QB;
+    static_assert(kIters % kReads == 0, "probability iterations per K operand");
+    constexpr int kPer = kIters / kReads;
+    float neg_m[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      neg_m[qb] = m_run[qb] == -INFINITY ? 0.f : -m_run[qb];
+      rs[qb] = 0.f;
+      s[qb][0] = f32x16{};
+      s[qb][1] = f32x16{};
+    }
+    u32x4 a[kReads];
+#pragma unroll
+    for (int r = 0; r < kWin; ++r) a[r] = lds_read_b128(base + kaddr[r % kKSteps], (r / kKSteps) * 32 * (D * 2));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) {
+      lds_wait(a[r], r + kWin <= kReads ? kWin - 1 : kReads - 1 - r);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        s[qb][r / kKSteps] = mfma_bf16(a[r], qreg[qb][r % kKSteps], s[qb][r / kKSteps]);
+      }
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const int it = r * kPer + t;
+        prob_pair(it / 16, it % 16, sp[it / 16], neg_m[it / 16], pb[it / 16], rs[it / 16]);
+      }
+      if (r + kWin < kReads) {
+        a[r + kWin] = lds_read_b128(base + kaddr[(r + kWin) % kKSteps], ((r + kWin) / kKSteps) * 32 * (D * 2));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
   // Keys >= S and (causal) keys after the query score -inf.
   __device__ __forceinline__ void mask(f32x16 (&s)[QB][2], int k0) const {
 #pragma unroll
@@ -385,12 +442,16 @@ __device__ __forceinline__ void fa_step(FaState<D, kWaves, QB>& st, int j, int n
   if (load_k) st.template load_tile<false>(ring + c * T, k1 + 2 * BKV);
   u32x4 pb[QB][2][2];
   float rs[QB];
-  if (act) {
+  if constexpr (!kGuard) {
+    st.scores_probs(ring + c1 * T, sn, sc, pb, rs);  // both streams, interleaved
+  } else {
+    if (act) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rs[qb] = st.probs(qb, sc[qb], pb[qb]);
+      for (int qb = 0; qb < QB; ++qb) rs[qb] = st.probs(qb, sc[qb], pb[qb]);
+    }
+    if (act_next) st.scores(ring + c1 * T, sn);
+    if (act_next) st.mask(sn, k1);
   }
-  if (act_next) st.scores(ring + c1 * T, sn);
-  if (kGuard && act_next) st.mask(sn, k1);
   if (act) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
