@@ -444,13 +444,12 @@ __device__ __forceinline__ void fa_step(FaState<D, kWaves, QB>& st, int j, int n
   float rs[QB];
   if constexpr (!kGuard) {
     st.scores_probs(ring + c1 * T, sn, sc, pb, rs);  // both streams, interleaved
-  } else {
-    if (act) {
+  } else if (act_next) {  // a wave active for tile j+1 is active for tile j
+    st.scores_probs(ring + c1 * T, sn, sc, pb, rs);
+    st.mask(sn, k1);
+  } else if (act) {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) rs[qb] = st.probs(qb, sc[qb], pb[qb]);
-    }
-    if (act_next) st.scores(ring + c1 * T, sn);
-    if (act_next) st.mask(sn, k1);
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = st.probs(qb, sc[qb], pb[qb]);
   }
   if (act) {
 #pragma unroll
