@@ -65,7 +65,7 @@ CSRC = os.path.join(REPO, "pyasc_amd", "csrc")
 CPU_MIN_S = 2.0  # timed CPU work per suite baseline (the full workload, repeated to at least this long)
 CPU_HEADLINE_S = 10.0  # the same for the headline's baseline
 WARMUP_S = 1.0  # least warm-up per workload: graph replays of its timed launches (clocks and caches settle)
-REPLAYS = 7  # timed graph replays per workload; the figure is their median
+REPLAYS = 20  # timed graph replays per workload (60 for the us-scale launch); the figure is their median
 LINE_LIMIT = 8192  # the stdout line stays below this many bytes (longer lines are not read back)
 
 

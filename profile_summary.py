@@ -250,7 +250,7 @@ def trace(folder: str) -> int:
         "```", "",
         "Durations in microseconds: average, minimum and maximum of the last timed replay's dispatches "
         "(Start/End timestamps), the bench's figure (HIP events around each graph replay on the launch "
-        "stream, the median of its seven timed replays divided by the launches) and the bench's value "
+        "stream, the median of its timed replays divided by the launches) and the bench's value "
         "computed from it.", "",
         "| Workload | Kernel | timed dispatches | avg us | min | max | bench events us | trace / events | "
         "bench value |",

@@ -65,8 +65,8 @@ def _stub_result(w, ms: float) -> dict:
     """What bench.measure returns, for a workload timed at ``ms`` per launch (no GPU)."""
     return {"workload": w.name, "ms_per_step": ms, "kernel_ms": ms, "ms_min": ms * 0.99, "ms_max": ms * 1.013,
             "value": w.value(ms / 1e3), "unit": w.unit, "rate": w.rate(ms / 1e3), "bound": w.bound,
-            "config": {"workload": w.name}, "replays": 7, "warmup_launches": 123456, "warmup_s": 1.0,
-            "timing": "median of 7 hip-graph replays of 20 launches",
+            "config": {"workload": w.name}, "replays": 20, "warmup_launches": 123456, "warmup_s": 1.0,
+            "timing": "median of 20 hip-graph replays of 20 launches",
             "vendor": {"value": 1.0, "this_over_vendor": 1.093}}
 
 

@@ -19,7 +19,7 @@ goldens in test/all_task_durations_golden.csv).  Here:
   recorded absolute value.
 
 Each figure is bench.py's own measurement (bench.measure: at least a second of warm-up
-replays, then the median of seven timed HIP-graph replays), with fewer launches per
+replays, then the median of twenty timed HIP-graph replays), with fewer launches per
 replay than the bench."""
 import pytest
 
