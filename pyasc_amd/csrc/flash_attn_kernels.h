@@ -9,7 +9,7 @@
 // Design (gfx950, wave64, MFMA 32x32x16 bf16):
 //  - A wave owns 32 queries of one (batch, head); a workgroup has 4 waves
 //    (128 queries; head_dim 64) or 8 waves (256 queries; head_dim 128).  Keys/values stream through LDS in tiles of 64,
-//    double-buffered.
+//    K and V each in a ring of three stages filled by direct-to-LDS loads.
 //  - Each wave computes S^T = K Q^T (keys x queries) instead of S = Q K^T:
 //    in the MFMA result layout a lane then holds ONE query column and 16 keys
 //    per 32x32 block, so the online-softmax max/sum of a query live in two
@@ -18,12 +18,14 @@
 //    data movement; A and B agree on which key each operand slot holds), V^T is
 //    read from the row-major V tile with ds_read_b64_tr_b16 (gfx950 LDS
 //    transpose read).  Q^T stays in registers for the whole kernel.
-//  - Online softmax in the exp2 domain: the max is taken on raw scores and
-//    scale*log2(e) and the shift fold into one FMA before exp2; the reference
-//    point only moves when a tile max exceeds it by more than 8 (exact
-//    arithmetic either way, O and l are rescaled rarely); causal tiles above
-//    the diagonal are skipped and the diagonal tile is masked; heavy (late)
-//    query blocks are scheduled first.
+//  - Online softmax in the exp2 domain: scale*log2(e) and the shift by the
+//    reference point fold into one FMA before exp2; the reference point is not
+//    moved per tile but only when a lane's probability sum over a tile exceeds
+//    kTileSumLimit, and then to the tile max (exact arithmetic either way, O
+//    and l are rescaled rarely); causal tiles above the diagonal are skipped and
+//    the diagonal tile is masked; heavy (late) query blocks are scheduled first.
+//  - The clean step computes tile j's probabilities between the S^T MFMAs of
+//    tile j+1, so one wave's exp2 work and MFMAs overlap.
 // LDS tiles use XOR-swizzled 16-byte chunks so that both the MFMA operand
 // reads and the transpose reads are free of bank conflicts.
 #pragma once
