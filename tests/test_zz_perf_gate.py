@@ -10,11 +10,14 @@ goldens in test/all_task_durations_golden.csv).  Here:
 - every bench configuration of the asc2 hot path must keep at least 0.9 x the speed it
   had in a full steady-state bench.py run (RECORDED below), relative to a yardstick timed
   in the same run on the same box: the ROCm library kernel torch calls for the same
-  operation (hipBLASLt, SDPA, torch's softmax; the bench's ``vendor``) for the MFMA
-  kernels and the softmax headline, the plain streaming copy of the same bytes for the
-  other HBM-bound kernels.  Boxes of this pool differ by up to about 9% in absolute speed
-  at the 1.4 kW power limit (the MFMA kernels and the library's alike), so the 10% rule
-  is applied to the same-run ratio, which that spread does not move;
+  operation (hipBLASLt, SDPA, torch's softmax; the bench's ``vendor``) for the bf16 GEMM,
+  attention and the softmax headline, the plain streaming copy of the same bytes for the
+  other HBM-bound kernels, and this library's bf16 GEMM for the int8 GEMM (hipBLASLt's
+  int8 GEMM ran 1311 and 1469 TOPS in two runs on two boxes, while the int8 and bf16
+  GEMMs here, one loop at one power limit, kept their ratio within 1%).  Boxes of this
+  pool differ by up to about 9% in absolute speed at the 1.4 kW power limit (the MFMA
+  kernels and the library's alike), so the 10% rule is applied to the same-run ratio,
+  which that spread does not move;
 - and, as a backstop against a lost fast path, every figure stays above 0.85 x its
   recorded absolute value.
 
@@ -29,25 +32,26 @@ pytestmark = pytest.mark.gpu
 
 # workload key -> (figure, unit, yardstick, figure / yardstick) of a full
 # `python bench.py --steps 20 --warmup 5` run on an MI355X (steady state); yardstick
-# "vendor" is the bench's library comparison, a workload key is that copy's figure
+# "vendor" is the bench's library comparison, a workload key is that workload's figure
 RECORDED = {
-    "softmax_4096x4096": (5848.5, "GB/s", "vendor", 1.376),
-    "softmax_16384x1024": (5969.7, "GB/s", "copy_128MiB", 1.0141),
-    "vadd_268435456": (6284.3, "GB/s", "copy_3GiB", 1.0695),
-    "rms_norm_4096x4096": (5686.7, "GB/s", "copy_128MiB", 0.9661),
-    "matmul_bf16_8192": (1284.4, "TFLOP/s", "vendor", 1.075),
-    "matmul_i8_4096x11008x4096": (1984.2, "TOPS", "vendor", 1.435),
-    "fa_fwd_noncausal": (1138.4, "TFLOP/s", "vendor", 1.801),
-    "fa_fwd_causal": (1026.0, "TFLOP/s", "vendor", 2.848),
+    "softmax_4096x4096": (5824.9, "GB/s", "vendor", 1.378),
+    "softmax_16384x1024": (5952.3, "GB/s", "copy_128MiB", 1.0156),
+    "vadd_268435456": (6263.2, "GB/s", "copy_3GiB", 1.0658),
+    "rms_norm_4096x4096": (5657.9, "GB/s", "copy_128MiB", 0.9654),
+    "matmul_bf16_8192": (1266.9, "TFLOP/s", "vendor", 1.080),
+    "matmul_i8_4096x11008x4096": (1933.8, "TOPS", "matmul_bf16_8192", 1.5264),
+    "fa_fwd_noncausal": (1149.9, "TFLOP/s", "vendor", 1.864),
+    "fa_fwd_causal": (1015.0, "TFLOP/s", "vendor", 2.840),
 }
 RATIO_RULE = 0.9     # the reference's +10% duration threshold (run_presmoke_npu_test.sh)
 ABSOLUTE_RULE = 0.85
 
 
 @pytest.fixture(scope="module")
-def copies(device):
+def yardsticks(device):
+    """Same-run figures of the workloads the entries of RECORDED are compared with."""
     out = {}
-    for key in ("copy_128MiB", "copy_3GiB"):
+    for key in sorted({r[2] for r in RECORDED.values()} - {"vendor"}):
         w = bench.WORKLOADS[key]()
         out[key] = bench.measure(w, steps=10, warmup=5, dev=device)["value"]
         del w
@@ -55,7 +59,7 @@ def copies(device):
 
 
 @pytest.mark.parametrize("key", sorted(RECORDED))
-def test_hot_path_speed(device, copies, key):
+def test_hot_path_speed(device, yardsticks, key):
     recorded, unit, yardstick, ratio = RECORDED[key]
     w = bench.WORKLOADS[key]()
     res = bench.measure(w, steps=10, warmup=5, dev=device)
@@ -65,7 +69,7 @@ def test_hot_path_speed(device, copies, key):
         assert v is not None and "value" in v, v
         ref = v["value"]
     else:
-        ref = copies[yardstick]
+        ref = yardsticks[yardstick]
     got = res["value"] / ref
     print(f"{w.name}: {res['value']:.1f} {unit} ({got:.3f} x {yardstick} {ref:.1f}; recorded {recorded}, "
           f"{ratio} x)")
