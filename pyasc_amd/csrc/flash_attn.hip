@@ -35,9 +35,12 @@ int32_t geometry(FaLaunch& L) {
       return asc::set_error(static_cast<int32_t>(e), "asc_flash_attention_fwd_bf16: cannot read the CU count: %s",
                             hipGetErrorString(e));
     }
-    // Twice the smallest group that fills them: at the bench shape (64 slots, 32
-    // blocks per head) groups of 1, 2, 4, 8, 16 heads measured 582-621, 569-591,
-    // 564-575, 572-578 and 581-586 us.
+    // Twice the smallest group that fills them.  At the bench shape (32 slots, 16
+    // blocks per head) groups of 1, 2, 4 and 8 heads measured 561, 531, 533 and 536 us
+    // in one run, and 2 against 4 in ten alternating rounds 530.3 against 520.2 us;
+    // their reads past the L2 (FETCH_SIZE) were 1.00x, 1.37x, 1.46x and 2.15x Q + K + V (one
+    // head's K and V, 2 MiB, stay in the 4 MB L2 while its blocks run; more heads at
+    // once compete for it, fewer leave the heavy blocks of later heads to the end).
     const int64_t slots = static_cast<int64_t>(cus) / 8 * Cfg::kWgPerCu;
     const int64_t g = 2 * ((slots + p.n_qblocks - 1) / p.n_qblocks);
     const int64_t heads_xcd = p.heads_total / 8;
