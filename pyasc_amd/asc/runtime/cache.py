@@ -10,7 +10,7 @@ result twice (python/asc/runtime/jit.py:158-186, python/asc/runtime/cache.py):
     (cache.py:156-159), whose first component identifies the compiler itself
     (``pyasc_key``: a hash of the package sources and libpyasc), as files kept by
     ``FileCacheManager`` (cache.py:56-125) in ``$PYASC_CACHE_DIR`` (default
-    ``~/.pyasc/cache``), one directory per key.
+    ``~/.pyasc/cache``).
 ``always_compile=True`` skips both lookups and stores nothing.
 
 Here the kernels are compiled for gfx950 ahead of time: into libasc_hip.so (the
@@ -19,17 +19,17 @@ standalone code objects (pyasc_amd/lib/co/*.hsaco, see module.py).  The memory
 level holds what resolving a call produces (``ResolvedKernel`` in jit.py) and,
 after the first launch, the loaded code object's function handles; the file level
 keeps each specialisation's code object under its file cache key in
-``$PYASC_AMD_CACHE_DIR`` (default ``~/.pyasc_amd/cache``), where the next process
-loads it from.  The prebuilt binaries' identity takes the place of ``pyasc_key``
+``$PYASC_AMD_CACHE_DIR`` (default ``~/.pyasc_amd/cache``), one directory per key,
+where the next process loads it from.  The prebuilt binaries' identity takes the place of ``pyasc_key``
 (``library_key``): a rebuilt library or code object changes every key.
 """
 from __future__ import annotations
 
-import base64
+import contextlib
 import functools
 import hashlib
 import os
-import uuid
+import tempfile
 from pathlib import Path
 from typing import Optional
 
@@ -67,49 +67,44 @@ def cache_dir() -> str:
 
 
 class FileCacheManager:
-    """Files of one cache key, in their own directory (cache.py:56-125): ``get_file``
-    returns a file's path if present, ``put`` writes it atomically (a temporary
-    directory named by pid and a random id, then os.replace)."""
+    """The files of one cache key, in a directory named by the key.  A file is
+    published by writing it to a temporary file in that directory and renaming it
+    over its name: a reader finds either no file or the whole file, and writers of
+    the same key in several processes leave one complete copy."""
 
     def __init__(self, key: str):
-        self.key = key
         root = cache_dir()
         if not root:
             raise RuntimeError("Could not create or locate cache dir")
+        self.key = key
         self.cache_dir = os.path.join(root, key)
         os.makedirs(self.cache_dir, exist_ok=True)
 
-    def _make_path(self, filename: str) -> str:
-        return os.path.join(self.cache_dir, filename)
+    def get_file(self, filename: str) -> Optional[str]:
+        path = os.path.join(self.cache_dir, filename)
+        return path if os.path.isfile(path) else None
 
     def has_file(self, filename: str) -> bool:
-        return os.path.exists(self._make_path(filename))
-
-    def get_file(self, filename: str) -> Optional[str]:
-        return self._make_path(filename) if self.has_file(filename) else None
+        return self.get_file(filename) is not None
 
     def put(self, data, filename: str) -> str:
-        binary = isinstance(data, bytes)
-        if not binary:
-            data = str(data)
-        path = self._make_path(filename)
-        temp_dir = os.path.join(self.cache_dir, f"tmp.pid_{os.getpid()}_{uuid.uuid4()}")
-        os.makedirs(temp_dir, exist_ok=True)
-        temp_path = os.path.join(temp_dir, filename)
-        with open(temp_path, "wb" if binary else "w") as f:
-            f.write(data)
-        os.replace(temp_path, path)  # atomic on POSIX: readers never see a partial file
-        os.removedirs(temp_dir)
+        payload = data if isinstance(data, bytes) else str(data).encode("utf-8")
+        path = os.path.join(self.cache_dir, filename)
+        fd, tmp = tempfile.mkstemp(prefix=f".{filename}.", dir=self.cache_dir)
+        try:
+            with os.fdopen(fd, "wb") as f:
+                f.write(payload)
+            os.replace(tmp, path)
+        except BaseException:
+            with contextlib.suppress(FileNotFoundError):
+                os.unlink(tmp)
+            raise
         return path
 
 
-def _base32(key: str) -> str:
-    return base64.b32encode(bytes.fromhex(key)).decode("utf-8").rstrip("=")
-
-
 def get_cache_manager(key: str) -> FileCacheManager:
-    """The file cache of a hex key, in a directory named by its base32 form (cache.py:128-134)."""
-    return FileCacheManager(_base32(key))
+    """The file cache of a hex key (the reference's get_cache_manager, cache.py:128-134)."""
+    return FileCacheManager(key)
 
 
 @functools.lru_cache(maxsize=4096)
