@@ -4,6 +4,7 @@
     python profile_summary.py mfma DIR      # MFMA-busy / clock passes -> profiles/mfma_counters.md
     python profile_summary.py trace DIR     # kernel traces -> profiles/kernel_trace_suite.md
     python profile_summary.py ea DIR        # L2 read-miss requests by destination -> profiles/l2_miss_destinations.md
+    python profile_summary.py lds DIR       # LDS / VALU / MFMA instruction and LDS-busy passes -> profiles/lds_valu_counters.md
 
 DIR holds one rocprofv3 output folder per pass, written with ``-f csv -o run`` by
 the commands the summaries print:
@@ -22,6 +23,10 @@ the commands the summaries print:
       rocprofv3 --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_DRAM_sum TCC_EA0_RDREQ_32B_sum -f csv -d DIR/<workload>_EA \
           -o run -- python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 \
           --warmup-s 0 --copy-calibration
+  lds: DIR/<workload>_LDS, from
+      rocprofv3 --pmc SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT SQ_INSTS_LDS SQ_INSTS_VALU SQ_INSTS_MFMA \
+          SQ_INSTS_VALU_TRANS_F32 GRBM_GUI_ACTIVE --kernel-trace -f csv -d DIR/<workload>_LDS -o run -- \
+          python3 bench.py --workload <workload> --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --warmup-s 0
 
 FETCH_SIZE and WRITE_SIZE are KiB per dispatch past the L2.  ``--copy-calibration``
 adds five torch device copies of exactly 256 MiB; their readings give the factor that
@@ -367,6 +372,69 @@ def _gpu_agent(folder: str) -> dict:
     return {}
 
 
+def lds(folder: str) -> int:
+    """LDS and VALU activity of the MFMA kernels from one counter pass each.
+
+    SQ_LDS_IDX_ACTIVE and SQ_LDS_BANK_CONFLICT count LDS cycles (indexed accesses, and
+    the cycles of those stalled by bank conflicts), summed over the CUs; the SQ_INSTS_*
+    counters count wave instructions issued, summed over the SIMDs.  So
+      LDS busy          = SQ_LDS_IDX_ACTIVE / (cycles per XCD x CUs)
+      conflict share    = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE
+    and the instruction counts are given per MFMA instruction."""
+    cus, xcds, info = device_shape(folder)
+    lines = [
+        "# LDS, VALU and MFMA activity (rocprofv3 PMC), one MI355X", "",
+        "Generated by `python profile_summary.py lds DIR` from one counter pass per workload "
+        "(repository root on the GPU box, `TMPDIR=/tmp`, `W` a bench workload key):", "",
+        "```",
+        "rocprofv3 --pmc SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT SQ_INSTS_LDS SQ_INSTS_VALU SQ_INSTS_MFMA "
+        "SQ_INSTS_VALU_TRANS_F32 GRBM_GUI_ACTIVE --kernel-trace -f csv -d gpurun_out/pmc/${W}_LDS -o run -- "
+        "python3 bench.py --workload $W --no-suite --no-cpu --no-vendor --steps 5 --warmup 1 --warmup-s 0",
+        "```", "",
+        f"Device: {info}.  LDS busy = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE / XCDs x CUs), the share of "
+        "each CU's cycles in which its LDS serves indexed reads or writes (the direct-to-LDS loads are "
+        "not indexed accesses); bank conflicts = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.  The "
+        "instruction columns are wave instructions issued per MFMA instruction (`SQ_INSTS_VALU` counts "
+        "every VALU-issued instruction, the MFMAs included; `TRANS` counts fp32 transcendentals, here "
+        "`v_exp_f32`).", "",
+        "| Workload | Kernel | dispatches | duration us | LDS busy % | bank conflicts % of LDS busy | "
+        "LDS instr / MFMA | VALU instr / MFMA | TRANS / MFMA |",
+        "|---|---|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for key, make in bench.WORKLOADS.items():
+        d = os.path.join(folder, f"{key}_LDS")
+        if not os.path.isdir(d):
+            continue
+        w = make()
+        per = collections.defaultdict(dict)
+        for r in _rows(d):
+            if not (_is_library_kernel(r["Kernel_Name"]) and w.kernel_hint in r["Kernel_Name"]):
+                continue
+            e = per[r["Dispatch_Id"]]
+            e["kernel"] = _short(r["Kernel_Name"])
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            e["dur"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
+        need = ("SQ_LDS_IDX_ACTIVE", "SQ_INSTS_MFMA", "GRBM_GUI_ACTIVE")
+        disp = [e for e in per.values() if all(k in e for k in need)]
+        if not disp:
+            raise RuntimeError(f"{d}: no dispatch of a kernel matching {w.kernel_hint!r}")
+        n = len(disp)
+
+        def avg(k):
+            return sum(e.get(k, 0.0) for e in disp) / n
+        gui = avg("GRBM_GUI_ACTIVE") / xcds
+        lds_active, mfma = avg("SQ_LDS_IDX_ACTIVE"), avg("SQ_INSTS_MFMA")
+        lines.append(f"| `{w.name}` | `{disp[0]['kernel']}` | {n} | {avg('dur') * 1e6:.1f} | "
+                     f"{100 * lds_active / (gui * cus):.1f} | "
+                     f"{100 * avg('SQ_LDS_BANK_CONFLICT') / max(lds_active, 1.0):.2f} | "
+                     f"{avg('SQ_INSTS_LDS') / mfma:.3f} | {avg('SQ_INSTS_VALU') / mfma:.3f} | "
+                     f"{avg('SQ_INSTS_VALU_TRANS_F32') / mfma:.3f} |")
+        print(lines[-1])
+    with open(os.path.join(PROFILES, "lds_valu_counters.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    return 0
+
+
 def device_shape(folder: str):
     """(CUs, XCDs, description) of the profiled GPU (256, 8 for MI355X)."""
     for d in sorted(glob.glob(os.path.join(folder, "*"))):
@@ -379,7 +447,7 @@ def device_shape(folder: str):
 
 
 def main(argv) -> int:
-    modes = {"traffic": traffic, "mfma": mfma, "trace": trace, "ea": ea}
+    modes = {"traffic": traffic, "mfma": mfma, "trace": trace, "ea": ea, "lds": lds}
     if len(argv) != 3 or argv[1] not in modes:
         print(__doc__, file=sys.stderr)
         return 2
